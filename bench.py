@@ -1,0 +1,209 @@
+#!/usr/bin/env python3
+"""Benchmark of the pruned-weight SpMM hot path on one MI355X.
+
+Workload (the headline configuration): fp32 CSR SpMM, W 4096 x 4096 with each
+entry kept with probability 0.1 (nnz ~= 1.68 M, values N(0, 0.02)), X dense
+4096 x 256 N(0, 1), Y = W . X, strict (bit-exact) mode.  One step = one
+kernel launch over one batch, inputs already resident in HBM.  16 distinct
+(W, X, Y) copies rotate so the working set (~350 MB) exceeds the 256 MB
+Infinity Cache.
+
+Prints ONE JSON line.  `value` is effective GFLOP/s (2 * nnz * N per step);
+`roofline` prices the kernel's algorithmic bytes per launch against HBM
+(8 TB/s); `cpu_baseline` is the reference's own sparse_matmul (compiled from
+its sources) -- or the oracle port where that library is absent -- timed
+single-threaded on this host on the same input.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (packed FMA)
+M = K = 4096
+DENSITY = 0.1
+N_MAIN = 256
+N_SETS = 16
+
+
+def csr_bytes(nnz, M, K, N):
+    """Algorithmic bytes of one SpMM launch: CSR values + int32 column
+    indices + int32 row pointers + X + Y (each read or written once)."""
+    return 8 * nnz + 4 * (M + 1) + 4 * K * N + 4 * M * N
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_gpu(sets, N, steps, warmup, mode):
+    """ms per launch over `steps` back-to-back launches on the context's
+    stream (torch's current stream), bracketed by HIP events."""
+    import torch
+
+    for i in range(warmup):
+        W, dX, dY = sets[i % len(sets)]
+        W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        W, dX, dY = sets[i % len(sets)]
+        W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_baseline(ip, ix, v, X, gpu_Y, budget_s):
+    """Reference sparse_matmul, single thread, on the same W and X; also the
+    parity check of the GPU output against it."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    nnz = len(v)
+    N = X.shape[1]
+    if O.have_ref():
+        ts, ref_out = O.ref_time_sparse_matmul(M, K, ip, ix, v, X, 1)
+        reps = max(3, min(200, int(budget_s / max(ts[0], 1e-3))))
+        ts, ref_out = O.ref_time_sparse_matmul(M, K, ip, ix, v, X, reps)
+        kind = "reference"
+        what = "pruning::sparse_matmul (sparse_tensor.cpp:473-519) compiled from the reference sources, -O3"
+    else:
+        ts = []
+        ref_out = None
+        t_end = time.perf_counter() + budget_s
+        while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 200):
+            t0 = time.perf_counter()
+            ref_out = O.orc_csr_spmm(M, K, ip, ix, v, X)
+            ts.append(time.perf_counter() - t0)
+        ts = np.array(ts)
+        kind = "port"
+        what = "oracle restatement of sparse_matmul (oracle/pfr_oracle.c), -O3"
+    med = float(np.median(ts))
+    exact = bool(np.array_equal(ref_out.view(np.uint32), gpu_Y.view(np.uint32)))
+    return {
+        "value": round(2.0 * nnz * N / med / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"full workload W 4096x4096 nnz={nnz} x X 4096x{N}; median of {len(ts)} calls "
+                  f"({med * 1e3:.1f} ms each) of {what}",
+        "ms_per_call": round(med * 1e3, 3),
+    }, exact
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--mode", default="strict", choices=["strict", "fast"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the path on "
+              "a single MI355X and reports that GPU's throughput.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import rocm, workloads
+
+    torch.cuda.init()
+    ctx = rocm.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    log("generating W 4096x4096 at 10% density ...")
+    ip, ix, v = workloads.csr_uniform(M, K, DENSITY, 0.02, seed=1234)
+    nnz = len(v)
+    Xh = workloads.dense_normal((K, N_MAIN), 1.0, seed=2024)
+
+    extra = {}
+    results = {}
+    for N in (N_MAIN, 64, 1):
+        sets = []
+        for s in range(N_SETS):
+            W = ctx.csr_upload(M, K, ip, ix, v)
+            dX = torch.from_numpy(np.ascontiguousarray(Xh[:, :N])).cuda()
+            dY = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            sets.append((W, dX, dY))
+        torch.cuda.synchronize()
+        steps = args.steps if N == N_MAIN else max(200, args.steps // 4)
+        ms = time_gpu(sets, N, steps, args.warmup, args.mode)
+        Y0 = sets[0][2].cpu().numpy()
+        byts = csr_bytes(nnz, M, K, N)
+        flops = 2.0 * nnz * N
+        results[N] = (ms, Y0, steps)
+        extra[f"N{N}"] = {
+            "ms_per_launch": round(ms, 5),
+            "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": byts,
+            "flop_per_launch": flops,
+        }
+        log(f"N={N}: {ms * 1e3:.2f} us/launch  {extra[f'N{N}']}")
+        for W, _, _ in sets:
+            W.free()
+        del sets
+        torch.cuda.empty_cache()
+
+    ms, Y0, steps = results[N_MAIN]
+    byts = csr_bytes(nnz, M, K, N_MAIN)
+    flops = 2.0 * nnz * N_MAIN
+    gbs = byts / (ms * 1e-3) / 1e9
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        cpu, exact = cpu_baseline(ip, ix, v, Xh, Y0, args.cpu_seconds)
+        parity = "bit-exact" if exact else "MISMATCH"
+    out = {
+        "metric": "effective GFLOP/s + HBM GB/s (% roofline) for pruned SpMM at 90% sparsity, 1 GPU",
+        "value": round(flops / (ms * 1e-3) / 1e9, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy: W 10% uniform-random N(0,0.02), X N(0,1))",
+        "config": {"workload": "fp32 CSR SpMM W[4096x4096] 90% sparse x X[4096x256]",
+                   "nnz": nnz, "N": N_MAIN, "mode": args.mode, "buffer_sets": N_SETS},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "compute": {
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "fp32_valu_peak_tflops": FP32_VALU_PEAK_TFLOPS,
+            "note": "strict mode issues a separate v_mul_f32 and v_add_f32 per term (no FMA, no packed "
+                    "FP32): its VALU ceiling is 1/4 of the packed-FMA peak",
+        },
+        "parity": parity,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+/*
+ * pfr_rocm.h -- C ABI of the MI355X (gfx950) kernels for PyFlameRT's
+ * pruned-weight MatMul/Gemm path.
+ *
+ * This is the boundary a `src/backends/rocm` backend inside PyFlameRT binds
+ * to.  Plain pointers and sizes only; no exceptions cross it.  Every function
+ * returns PFR_OK (0) or an error code; pfr_last_error() then describes the
+ * failure (thread-local).  Functions whose pointer arguments are documented
+ * as "host" copy in and out and synchronise before returning, matching the
+ * synchronous OpFunc contract of the reference
+ * (include/pyflame_rt/registry.hpp:26-29, src/backends/cpu/executor.cpp:106).
+ * The *_dev variants take device pointers, enqueue on the context's stream
+ * and do not synchronise.
+ *
+ * Numerics (defined by the reference CPU kernels):
+ *   PFR_MODE_STRICT  fp32 results bit-identical to cpu_matmul / cpu_gemm /
+ *                    sparse_matmul (math.cpp:268-438, sparse_tensor.cpp:473-554):
+ *                    each output is the ascending-k sequence of separately
+ *                    rounded products and sums, bias added last.
+ *   PFR_MODE_FAST    same order with fused multiply-add (one rounding per
+ *                    term); close to, not equal to, the reference.
+ *   int8 paths       int32 accumulators and requantised int8 bit-exact to
+ *                    quantized_matmul + quantize_tensor (quant_ops.cpp:387-506,
+ *                    :15-127).
+ */
+#ifndef PFR_ROCM_H
+#define PFR_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PFR_OK 0
+#define PFR_ERR_INVALID_ARG 1 /* maps to std::invalid_argument in the OpFunc */
+#define PFR_ERR_HIP 2         /* HIP runtime error; text from hipGetErrorString */
+#define PFR_ERR_UNSUPPORTED 3 /* shape/dtype not handled by any kernel */
+#define PFR_ERR_NO_DEVICE 4
+
+/* Element types; the values are those of pyflame_rt::DType (types.hpp:48-59). */
+typedef enum pfr_dtype {
+    PFR_F32 = 0,
+    PFR_BF16 = 2,
+    PFR_I32 = 5,
+    PFR_I8 = 7,
+    PFR_U8 = 8
+} pfr_dtype;
+
+typedef enum pfr_mode { PFR_MODE_STRICT = 0, PFR_MODE_FAST = 1 } pfr_mode;
+
+typedef struct pfr_ctx pfr_ctx;   /* one device + one stream + scratch */
+typedef struct pfr_csr pfr_csr;   /* device-resident CSR weight */
+typedef struct pfr_sp24 pfr_sp24; /* device-resident 2:4 compressed weight */
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Text of the last error on this thread ("" if none). */
+const char* pfr_last_error(void);
+int pfr_device_count(int* count);
+/* Bind to `device`, create a stream.  Replaces the CPU-only backend choice of
+ * InferenceSession::select_backend (src/session.cpp:67-95). */
+int pfr_rocm_init(int device, pfr_ctx** out);
+int pfr_rocm_destroy(pfr_ctx* ctx);
+/* The hipStream_t the context enqueues on (as void*), and a way to replace
+ * it with a caller-owned stream.  NULL is the device's null stream, as in
+ * HIP; the context's own stream is whatever pfr_ctx_get_stream returned
+ * right after pfr_rocm_init. */
+int pfr_ctx_get_stream(pfr_ctx* ctx, void** stream);
+int pfr_ctx_set_stream(pfr_ctx* ctx, void* stream);
+int pfr_synchronize(pfr_ctx* ctx);
+
+/* ---- CSR weights (reference: pruning::SparseTensor, sparse_tensor.hpp:19-132) */
+
+/* Upload an M x K CSR matrix given as the reference's SparseTensor stores it
+ * (indptr/indices int64, sparse_tensor.hpp:124-126; values float).  Indices
+ * are range-checked (the check from_csr leaves out, sparse_tensor.cpp:39-49
+ * is never called) and must ascend within a row.  values_dtype is PFR_F32 or
+ * PFR_I8; for PFR_I8, row_scales[M] are the per-output-channel scales of a
+ * symmetric weight (dequantised value = (float)q * row_scales[m],
+ * quant_ops.cpp:182-196).  Host pointers. */
+int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz,
+                   const int64_t* indptr, const int64_t* indices,
+                   const void* values, pfr_dtype values_dtype,
+                   const float* row_scales, pfr_csr** out);
+/* Build the CSR of a dense, zero-filled pruned weight the way
+ * to_sparse(dense, threshold, CSR) does (sparse_tensor.cpp:560-610: keeps
+ * |v| > threshold, columns ascending).  dense is rows x cols, row-major,
+ * host.  With transpose != 0 the CSR is of dense^T (cols x rows): the form a
+ * Gemm/MatMul weight in the B position needs, so each output column's terms
+ * stay in ascending k. */
+int pfr_csr_from_dense(pfr_ctx* ctx, const float* dense, int64_t rows,
+                       int64_t cols, int transpose, float threshold,
+                       pfr_csr** out);
+int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz);
+int pfr_csr_free(pfr_csr* w);
+
+/* ---- CSR products --------------------------------------------------------- */
+
+/* Y[M,N] = W[M,K] . X[K,N] (row-major, host).  N == 1 is the SpMV of
+ * sparse_matvec (sparse_tensor.cpp:521-554).  Replaces sparse_matmul
+ * (sparse_tensor.cpp:473-519) and MatMul with a pruned first operand
+ * (math.cpp:268-374). */
+int pfr_spmm_csr(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N,
+                 float* Y, int mode);
+/* Device variant.  X rows are ldx floats apart, Y rows ldy floats apart
+ * (ldx, ldy >= N). */
+int pfr_spmm_csr_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X,
+                     int64_t N, int64_t ldx, float* Y, int64_t ldy, int mode);
+
+/* Gemm with the weight in the B position (cpu_gemm, math.cpp:377-438):
+ *   Y[Mb, Nf] = alpha * op(A)[Mb, K] . B[K, Nf] + beta * C[(i*Nf+j) % c_size]
+ * where BT is the CSR of op(B)^T (Nf x K, from pfr_csr_from_dense with
+ * transpose = !transB).  A is Mb x K (transA == 0) or K x Mb, host.  C may be
+ * NULL (c_size ignored).  MatMul(X, W) with a pruned W is the case alpha = 1,
+ * C = NULL (math.cpp:327-333). */
+int pfr_gemm_csr(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
+                 int transA, const pfr_csr* BT, float alpha, float beta,
+                 const float* C, int64_t c_size, float* Y, int mode);
+/* Device variant (A, C, Y device pointers, all contiguous). */
+int pfr_gemm_csr_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
+                     int transA, const pfr_csr* BT, float alpha, float beta,
+                     const float* C, int64_t c_size, float* Y, int mode);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -87,6 +87,7 @@ def ref_lib():
             "ref_run_op": (_INT, [C.c_char_p, _INT, _P, _P, _P, _P, _INT, _P, _P, _INT, _P, _P, _P, _I64, _P, _P]),
             "ref_to_sparse_csr": (_INT, [_P, _I64, _I64, _F, _P, _P, _P, _P]),
             "ref_sparse_matmul": (_INT, [_I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P]),
+            "ref_time_sparse_matmul": (_INT, [_I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P, _P]),
             "ref_sparse_matvec": (_INT, [_I64, _I64, _P, _P, _P, _I64, _P, _P]),
             "ref_apply_mask": (_INT, [_P, _P, _I64, _P]),
             "ref_magnitude_mask": (_INT, [_P, _I64, _I64, _F, _P]),
@@ -407,6 +408,19 @@ def ref_sparse_matmul(m, k, indptr, indices, values, b):
                                            _ptr(_c(values, np.float32)), len(values), _ptr(b),
                                            int(b.ndim == 1), _ptr(out)))
     return out
+
+
+def ref_time_sparse_matmul(m, k, indptr, indices, values, b, reps):
+    """Per-call seconds of the reference sparse_matmul (after one warm-up),
+    and its output."""
+    b = _c(b, np.float32)
+    n = b.shape[1]
+    ns = np.zeros(reps, np.int64)
+    out = np.empty((m, n), np.float32)
+    _ref_check(ref_lib().ref_time_sparse_matmul(m, k, n, _ptr(_c(indptr, np.int64)), _ptr(_c(indices, np.int64)),
+                                                _ptr(_c(values, np.float32)), len(values), _ptr(b), reps,
+                                                _ptr(ns), _ptr(out)))
+    return ns.astype(np.float64) * 1e-9, out
 
 
 def ref_sparse_matvec(m, k, indptr, indices, values, x):

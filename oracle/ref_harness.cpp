@@ -18,6 +18,7 @@
 #include "backends/cpu/executor.hpp"
 #include "io/pyflame_format.hpp"
 
+#include <chrono>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -117,6 +118,28 @@ int ref_sparse_matmul(int64_t m, int64_t k, int64_t n, const int64_t* indptr,
         pr::SparseTensor s = pr::SparseTensor::from_csr({m, k}, ip, ix, vv);
         Tensor bt = b_is_1d ? make_f32(b, {k}) : make_f32(b, {k, n});
         Tensor r = pr::sparse_matmul(s, bt);
+        std::memcpy(out, r.data(), r.size_bytes());
+    });
+}
+
+// Wall time of the reference's sparse_matmul on a prebuilt SparseTensor and
+// input Tensor: one warm-up call, then `reps` timed calls (ns each).  The last
+// result goes to out.  Single thread, as the reference runs.
+int ref_time_sparse_matmul(int64_t m, int64_t k, int64_t n, const int64_t* indptr,
+                           const int64_t* indices, const float* values, int64_t nnz,
+                           const float* b, int reps, int64_t* ns, float* out) {
+    return guard([&] {
+        std::vector<int64_t> ip(indptr, indptr + m + 1), ix(indices, indices + nnz);
+        std::vector<float> vv(values, values + nnz);
+        pr::SparseTensor s = pr::SparseTensor::from_csr({m, k}, ip, ix, vv);
+        Tensor bt = make_f32(b, {k, n});
+        Tensor r = pr::sparse_matmul(s, bt);
+        for (int i = 0; i < reps; ++i) {
+            auto t0 = std::chrono::steady_clock::now();
+            r = pr::sparse_matmul(s, bt);
+            auto t1 = std::chrono::steady_clock::now();
+            ns[i] = std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        }
         std::memcpy(out, r.data(), r.size_bytes());
     });
 }

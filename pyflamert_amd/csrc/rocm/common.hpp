@@ -1,0 +1,116 @@
+// Internal plumbing shared by the gfx950 kernel library: error capture for
+// the C ABI, the context and weight handles, grow-only device scratch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "pfr_rocm.h"
+
+namespace pfr {
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+void clear_last_error();
+
+#define PFR_HIP(call)                                                          \
+    do {                                                                       \
+        hipError_t e_ = (call);                                                \
+        if (e_ != hipSuccess)                                                  \
+            throw ::pfr::Error(PFR_ERR_HIP, std::string(#call) + ": " +        \
+                                                hipGetErrorString(e_));        \
+    } while (0)
+
+inline void require(bool ok, const std::string& msg) {
+    if (!ok) throw Error(PFR_ERR_INVALID_ARG, msg);
+}
+
+// Runs f and converts exceptions into a C status + thread-local message.
+template <class F>
+int guarded(F&& f) {
+    try {
+        clear_last_error();
+        f();
+        return PFR_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_last_error("host allocation failed");
+        return PFR_ERR_INVALID_ARG;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return PFR_ERR_INVALID_ARG;
+    }
+}
+
+// Grow-only device buffer owned by a context.
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    void* ensure(size_t n) {
+        if (p && n <= bytes) return p;
+        if (p) PFR_HIP(hipFree(p));
+        p = nullptr;
+        bytes = 0;
+        size_t want = n < 256 ? 256 : n;
+        PFR_HIP(hipMalloc(&p, want));
+        bytes = want;
+        return p;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+}  // namespace pfr
+
+struct pfr_ctx {
+    int device = 0;
+    int num_cu = 256;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // scratch[0..1]: staged inputs, scratch[2]: staged output, scratch[3]:
+    // transposed activations of the Gemm form.
+    pfr::DevBuf scratch[4];
+};
+
+struct pfr_csr {
+    pfr_ctx* ctx = nullptr;
+    int64_t M = 0, K = 0, nnz = 0;
+    int32_t* rowptr = nullptr;  // [M+1]
+    int32_t* col = nullptr;     // [nnz], ascending within a row
+    void* val = nullptr;        // [nnz] float or int8
+    pfr_dtype vdt = PFR_F32;
+    float* row_scale = nullptr;  // [M] for int8 values
+    // Row blocks for the vector (N == 1) kernel: each block is a run of
+    // consecutive rows holding at most a fixed nnz budget.
+    int32_t* spmv_blocks = nullptr;  // [n_spmv_blocks + 1] first row of each
+    int64_t n_spmv_blocks = 0;
+    int32_t max_row_nnz = 0;
+    // Columns ascend within every row (the order to_sparse produces).  Only
+    // then is the K-chunk table valid and the LDS-tiled kernel usable.
+    bool cols_sorted = false;
+    // chunk_ptr[r * (n_chunks + 1) + c]: first nnz of row r with column
+    // >= c * kChunkK (c = n_chunks gives the row end).
+    int32_t* chunk_ptr = nullptr;
+    int32_t n_chunks = 0;
+};
+
+namespace pfr {
+constexpr int kChunkK = 256;  // K rows of X staged per LDS chunk
+}
+
+namespace pfr {
+// Makes ctx's device current (cheap when it already is).
+void bind(pfr_ctx* ctx);
+}  // namespace pfr

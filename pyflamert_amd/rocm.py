@@ -1,0 +1,146 @@
+"""Python front-end of the gfx950 kernels (thin wrappers over the C ABI).
+
+Host entry points take and return numpy arrays; the ``*_dev`` methods take
+device pointers (e.g. ``torch.Tensor.data_ptr()``) and enqueue on the
+context's stream without synchronising.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import MODE_FAST, MODE_STRICT, PFR_F32, PFR_I8, check
+
+_MODES = {"strict": MODE_STRICT, "fast": MODE_FAST, MODE_STRICT: MODE_STRICT, MODE_FAST: MODE_FAST}
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def device_count():
+    n = C.c_int(0)
+    check(_lib.load().pfr_device_count(C.byref(n)))
+    return n.value
+
+
+class Context:
+    """One device, one stream, grow-only scratch (pfr_ctx)."""
+
+    def __init__(self, device=0):
+        self._lib = _lib.load()
+        h = C.c_void_p()
+        check(self._lib.pfr_rocm_init(device, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            check(self._lib.pfr_rocm_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self):
+        s = C.c_void_p()
+        check(self._lib.pfr_ctx_get_stream(self.handle, C.byref(s)))
+        return s.value
+
+    def set_stream(self, stream_ptr):
+        check(self._lib.pfr_ctx_set_stream(self.handle, stream_ptr))
+
+    def synchronize(self):
+        check(self._lib.pfr_synchronize(self.handle))
+
+    # -- weights ---------------------------------------------------------
+    def csr_upload(self, M, K, indptr, indices, values, row_scales=None):
+        """CSR as the reference's SparseTensor holds it (int64 indptr/indices,
+        float32 values) or int8 values with per-row float32 scales."""
+        indptr = np.ascontiguousarray(indptr, np.int64)
+        indices = np.ascontiguousarray(indices, np.int64)
+        values = np.ascontiguousarray(values)
+        if values.dtype == np.int8:
+            vdt = PFR_I8
+            row_scales = np.ascontiguousarray(row_scales, np.float32)
+        else:
+            values = values.astype(np.float32, copy=False)
+            vdt = PFR_F32
+            row_scales = None
+        h = C.c_void_p()
+        check(self._lib.pfr_csr_upload(self.handle, M, K, len(values), _ptr(indptr), _ptr(indices),
+                                       _ptr(values), vdt, _ptr(row_scales), C.byref(h)))
+        return CsrWeight(self, h)
+
+    def csr_from_dense(self, dense, transpose=False, threshold=0.0):
+        dense = np.ascontiguousarray(dense, np.float32)
+        rows, cols = dense.shape
+        h = C.c_void_p()
+        check(self._lib.pfr_csr_from_dense(self.handle, _ptr(dense), rows, cols, int(bool(transpose)),
+                                           threshold, C.byref(h)))
+        return CsrWeight(self, h)
+
+    # -- products --------------------------------------------------------
+    def gemm_csr(self, A, BT, alpha=1.0, beta=1.0, C_=None, transA=False, mode="strict"):
+        """cpu_gemm with the pruned weight in the B position; BT is the CSR of
+        op(B)^T (csr_from_dense(B, transpose=not transB))."""
+        A = np.ascontiguousarray(A, np.float32)
+        Mb = A.shape[1] if transA else A.shape[0]
+        K = A.shape[0] if transA else A.shape[1]
+        Y = np.empty((Mb, BT.M), np.float32)
+        csz = 0
+        if C_ is not None:
+            C_ = np.ascontiguousarray(C_, np.float32)
+            csz = C_.size
+        check(self._lib.pfr_gemm_csr(self.handle, _ptr(A), Mb, K, int(bool(transA)), BT.handle,
+                                     alpha, beta, _ptr(C_), csz, _ptr(Y), _MODES[mode]))
+        return Y
+
+    def gemm_csr_dev(self, A_ptr, Mb, K, BT, Y_ptr, alpha=1.0, beta=1.0, C_ptr=None, c_size=0,
+                     transA=False, mode="strict"):
+        check(self._lib.pfr_gemm_csr_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
+                                         alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode]))
+
+
+class CsrWeight:
+    """Device-resident CSR weight (pfr_csr)."""
+
+    def __init__(self, ctx, handle):
+        self.ctx = ctx
+        self.handle = handle
+        M, K, nnz = C.c_int64(), C.c_int64(), C.c_int64()
+        check(ctx._lib.pfr_csr_info(handle, C.byref(M), C.byref(K), C.byref(nnz)))
+        self.M, self.K, self.nnz = M.value, K.value, nnz.value
+
+    def free(self):
+        if self.handle:
+            check(self.ctx._lib.pfr_csr_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.ctx.handle:
+                self.free()
+        except Exception:
+            pass
+
+    def spmm(self, X, mode="strict"):
+        """Y = W . X with host numpy X of shape [K, N] or [K]."""
+        X = np.ascontiguousarray(X, np.float32)
+        vec = X.ndim == 1
+        N = 1 if vec else X.shape[1]
+        if X.shape[0] != self.K:
+            raise ValueError(f"Dimension mismatch in sparse matmul: K={self.K}, X has {X.shape[0]} rows")
+        Y = np.empty((self.M,) if vec else (self.M, N), np.float32)
+        check(self.ctx._lib.pfr_spmm_csr(self.ctx.handle, self.handle, _ptr(X), N, _ptr(Y), _MODES[mode]))
+        return Y
+
+    def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict"):
+        check(self.ctx._lib.pfr_spmm_csr_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
+                                             ldy or N, _MODES[mode]))

@@ -1,0 +1,57 @@
+"""Seeded synthetic inputs for the pruned-weight workloads.
+
+All generators are deterministic numpy draws (PCG64).  CSR arrays follow the
+reference's SparseTensor (int64 indptr/indices, float32 values, columns
+ascending within a row: the order to_sparse produces, sparse_tensor.cpp:575-585).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def csr_from_mask(mask, values):
+    """CSR (row-major scan order) of the entries of `values` where mask holds."""
+    rows, cols = np.nonzero(mask)
+    indptr = np.zeros(mask.shape[0] + 1, np.int64)
+    np.cumsum(np.bincount(rows, minlength=mask.shape[0]), out=indptr[1:])
+    return indptr, cols.astype(np.int64), np.ascontiguousarray(values[rows, cols], np.float32)
+
+
+def csr_uniform(M, K, density, std, seed):
+    """Each entry kept independently with probability `density`, values
+    N(0, std) (the 4096x4096 90 %-sparse SpMM workload uses 0.1 / 0.02)."""
+    rng = np.random.default_rng(seed)
+    mask = rng.random((M, K), dtype=np.float32) < density
+    nnz = int(mask.sum())
+    vals = np.zeros((M, K), np.float32)
+    vals[mask] = (rng.standard_normal(nnz, dtype=np.float32) * np.float32(std))
+    return csr_from_mask(mask, vals)
+
+
+def csr_lognormal_rows(M, K, mean_density, sigma, std, seed):
+    """Per-row nnz ~ lognormal(sigma), scaled to a mean density and capped at
+    K; positions uniform within a row (the skewed decode-linear workload)."""
+    rng = np.random.default_rng(seed)
+    w = rng.lognormal(0.0, sigma, M)
+    counts = np.minimum(np.rint(w / w.mean() * mean_density * K).astype(np.int64), K)
+    indptr = np.zeros(M + 1, np.int64)
+    np.cumsum(counts, out=indptr[1:])
+    indices = np.empty(int(indptr[-1]), np.int64)
+    for r in range(M):
+        c = counts[r]
+        if c:
+            indices[indptr[r]:indptr[r + 1]] = np.sort(rng.choice(K, size=c, replace=False))
+    values = (rng.standard_normal(int(indptr[-1]), dtype=np.float32) * np.float32(std))
+    return indptr, indices, values
+
+
+def dense_normal(shape, std, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def csr_to_dense(M, K, indptr, indices, values):
+    d = np.zeros((M, K), np.float32)
+    rows = np.repeat(np.arange(M), np.diff(indptr))
+    d[rows, indices] = values
+    return d

@@ -1,0 +1,211 @@
+"""GPU parity of the CSR SpMM/SpMV/Gemm kernels against the oracle and the
+golden vectors written by the compiled reference.
+
+Bar: strict mode is bit-exact (fp32 bits compared with array_equal on the
+uint32 view).  Fast mode (fused multiply-add, same order) is checked with a
+normwise bound: max|y - r| <= 1e-5 * max|r|.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pyflamert_amd import _lib, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def first_diff(a, b):
+    d = np.nonzero(a.view(np.uint32).ravel() != b.view(np.uint32).ravel())[0]
+    return (len(d), d[:5], a.ravel()[d[:5]], b.ravel()[d[:5]]) if len(d) else None
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from pyflamert_amd import rocm
+
+    c = rocm.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def cfg_weight():
+    """4096 x 4096, each entry kept with p = 0.1, values N(0, 0.02)."""
+    return workloads.csr_uniform(4096, 4096, 0.1, 0.02, seed=1234)
+
+
+@pytest.mark.parametrize("N", [1, 64, 256])
+def test_spmm_4096_strict_bit_exact(ctx, cfg_weight, N):
+    ip, ix, v = cfg_weight
+    say(f"spmm 4096x4096 nnz={len(v)} N={N} strict")
+    W = ctx.csr_upload(4096, 4096, ip, ix, v)
+    X = workloads.dense_normal((4096, N), 1.0, seed=99 + N)
+    Y = W.spmm(X if N > 1 else X[:, 0], mode="strict")
+    R = O.orc_csr_spmm(4096, 4096, ip, ix, v, X if N > 1 else X[:, 0])
+    assert bits_equal(Y, R), first_diff(Y, R)
+    W.free()
+
+
+@pytest.mark.parametrize("N", [2, 3, 8, 17, 33, 63, 65, 100, 130, 257])
+def test_spmm_odd_widths_strict(ctx, N):
+    ip, ix, v = workloads.csr_uniform(517, 389, 0.12, 0.05, seed=N)
+    say(f"spmm 517x389 N={N}")
+    W = ctx.csr_upload(517, 389, ip, ix, v)
+    X = workloads.dense_normal((389, N), 1.0, seed=7 * N)
+    assert bits_equal(W.spmm(X), O.orc_csr_spmm(517, 389, ip, ix, v, X))
+
+
+@pytest.mark.parametrize("N", [1, 8, 64, 256])
+def test_spmm_fast_normwise(ctx, cfg_weight, N):
+    ip, ix, v = cfg_weight
+    say(f"spmm fast N={N}")
+    W = ctx.csr_upload(4096, 4096, ip, ix, v)
+    X = workloads.dense_normal((4096, N), 1.0, seed=5 + N)
+    Y = W.spmm(X, mode="fast")
+    R = O.orc_csr_spmm(4096, 4096, ip, ix, v, X)
+    assert np.abs(Y - R).max() <= 1e-5 * np.abs(R).max()
+
+
+def test_golden_csr(ctx, golden):
+    g = golden("csr.npz")
+    M, K = g["W"].shape
+    say("golden csr.npz")
+    for tag in ("t0", "t1"):
+        W = ctx.csr_upload(M, K, g[f"{tag}_indptr"], g[f"{tag}_indices"], g[f"{tag}_values"])
+        if tag == "t0":
+            for n in (1, 8, 64):
+                X = g[f"X{n}"]
+                assert bits_equal(W.spmm(X), g[f"Y{n}"]), n
+            assert bits_equal(W.spmm(g["x"]), g["y_matvec"])
+            assert bits_equal(W.spmm(g["x"]), g["y_1d"])
+        W.free()
+    # from the dense weight with to_sparse's threshold rule
+    Wd = ctx.csr_from_dense(g["W"], threshold=0.0)
+    assert Wd.nnz == len(g["t0_values"])
+    assert bits_equal(Wd.spmm(g["X64"]), g["Y64"])
+    Wt = ctx.csr_from_dense(g["W"], threshold=0.005)
+    assert Wt.nnz == len(g["t1_values"])
+
+
+def test_golden_gemm(ctx, golden):
+    """cpu_gemm cases: alpha/beta, transA/transB, bias broadcast by modulo."""
+    g = golden("gemm.npz")
+    for i in range(int(g["n"])):
+        al, be, ta, tb = (float(x) for x in g[f"c{i}_p"])
+        A, B, Cb = g[f"c{i}_A"], g[f"c{i}_B"], g[f"c{i}_C"]
+        say(f"golden gemm case {i} A{A.shape} B{B.shape} ta={ta} tb={tb} c={Cb.size}")
+        BT = ctx.csr_from_dense(B, transpose=not tb)
+        Y = ctx.gemm_csr(A, BT, al, be, Cb if Cb.size else None, transA=bool(ta))
+        assert bits_equal(Y, g[f"c{i}_out"]), (i, first_diff(Y, g[f"c{i}_out"]))
+
+
+def test_golden_matmul_and_kat(ctx, golden):
+    """MatMul(X, W) with a pruned W as the Gemm form (alpha 1, no bias); the
+    batched case [3,4,5] x [5,6] flattens the broadcast batch into rows."""
+    g = golden("matmul.npz")
+    a, b = g["c0_a"], g["c0_b"]
+    BT = ctx.csr_from_dense(b, transpose=True)
+    Y = ctx.gemm_csr(a.reshape(-1, a.shape[-1]), BT).reshape(g["c0_out"].shape)
+    assert bits_equal(Y, g["c0_out"])
+    a, b = g["c3_a"], g["c3_b"]
+    assert bits_equal(ctx.gemm_csr(a, ctx.csr_from_dense(b, transpose=True)), g["c3_out"])
+    k = golden("kat_matmul.npz")
+    Y = ctx.gemm_csr(k["a"], ctx.csr_from_dense(k["b"], transpose=True))
+    assert Y.tolist() == [[22.0, 28.0], [49.0, 64.0]]
+
+
+@pytest.mark.parametrize("Mb", [1, 5, 32, 100, 1024])
+def test_gemm_form_vs_oracle(ctx, Mb):
+    rng = np.random.default_rng(Mb)
+    K, Nf = 768, 300
+    B = rng.normal(0, 0.02, (K, Nf)).astype(np.float32)
+    B[rng.random(B.shape) < 0.8] = 0.0
+    A = rng.standard_normal((Mb, K)).astype(np.float32)
+    bias = rng.standard_normal(Nf).astype(np.float32)
+    say(f"gemm form Mb={Mb}")
+    BT = ctx.csr_from_dense(B, transpose=True)
+    Y = ctx.gemm_csr(A, BT, 1.0, 1.0, bias)
+    R = O.orc_gemm(A, B, bias, 1.0, 1.0)
+    assert bits_equal(Y, R), first_diff(Y, R)
+
+
+def test_edge_cases(ctx):
+    say("edge: empty matrix, empty rows, long row, many tiny rows, skewed rows")
+    # nnz == 0: all +0
+    W = ctx.csr_upload(5, 7, np.zeros(6, np.int64), np.zeros(0, np.int64), np.zeros(0, np.float32))
+    Y = W.spmm(np.ones((7, 3), np.float32))
+    assert bits_equal(Y, np.zeros((5, 3), np.float32))
+    assert bits_equal(W.spmm(np.ones(7, np.float32)), np.zeros(5, np.float32))
+    # one row longer than the vector kernel's LDS chunk, plus empty rows
+    K = 9000
+    ip = np.array([0, 0, 8500, 8500, 8600], np.int64)
+    rng = np.random.default_rng(3)
+    ix = np.concatenate([np.sort(rng.choice(K, 8500, replace=False)), np.sort(rng.choice(K, 100, replace=False))])
+    v = rng.standard_normal(8600).astype(np.float32)
+    W = ctx.csr_upload(4, K, ip, ix, v)
+    for n in (1, 2, 64):
+        X = rng.standard_normal((K, n)).astype(np.float32)
+        assert bits_equal(W.spmm(X), O.orc_csr_spmm(4, K, ip, ix, v, X)), n
+    # many rows with one entry each (64-row vector blocks)
+    M = 10000
+    ip = np.arange(M + 1, dtype=np.int64)
+    ix = rng.integers(0, 50, M).astype(np.int64)
+    v = rng.standard_normal(M).astype(np.float32)
+    W = ctx.csr_upload(M, 50, ip, ix, v)
+    x = rng.standard_normal(50).astype(np.float32)
+    assert bits_equal(W.spmm(x), O.orc_csr_spmv(M, 50, ip, ix, v, x))
+    # lognormal row lengths (skewed), vector and matrix
+    ip, ix, v = workloads.csr_lognormal_rows(2000, 3000, 0.3, 0.8, 0.02, seed=11)
+    W = ctx.csr_upload(2000, 3000, ip, ix, v)
+    for n in (1, 8, 64):
+        X = rng.standard_normal((3000, n)).astype(np.float32)
+        assert bits_equal(W.spmm(X), O.orc_csr_spmm(2000, 3000, ip, ix, v, X)), n
+    # unsorted / duplicate columns: storage order is the summation order
+    ip = np.array([0, 4], np.int64)
+    ix = np.array([3, 1, 3, 0], np.int64)
+    v = np.array([1e8, 1.0, -1e8, 0.5], np.float32)
+    W = ctx.csr_upload(1, 4, ip, ix, v)
+    X = np.array([[1.0], [1.0], [0.0], [1.0]], np.float32)
+    assert bits_equal(W.spmm(X[:, 0]), O.orc_csr_spmv(1, 4, ip, ix, v, X[:, 0]))
+
+
+def test_rejects_bad_csr(ctx):
+    say("argument errors")
+    with pytest.raises(_lib.InvalidArgument, match="out of range"):
+        ctx.csr_upload(2, 3, np.array([0, 1, 2]), np.array([0, 3]), np.ones(2, np.float32))
+    with pytest.raises(_lib.InvalidArgument, match="non-decreasing"):
+        ctx.csr_upload(3, 3, np.array([0, 2, 1, 2]), np.array([0, 1]), np.ones(2, np.float32))
+    with pytest.raises(_lib.InvalidArgument, match="indptr"):
+        ctx.csr_upload(2, 3, np.array([0, 1, 3]), np.array([0, 1]), np.ones(2, np.float32))
+    BT = ctx.csr_from_dense(np.ones((4, 3), np.float32), transpose=True)
+    with pytest.raises(_lib.InvalidArgument, match="incompatible dimensions"):
+        ctx.gemm_csr(np.ones((2, 5), np.float32), BT)
+
+
+def test_device_pointer_variant(ctx, cfg_weight):
+    import torch
+
+    ip, ix, v = cfg_weight
+    say("spmm_dev via torch device tensors")
+    W = ctx.csr_upload(4096, 4096, ip, ix, v)
+    X = workloads.dense_normal((4096, 256), 1.0, seed=17)
+    dX = torch.from_numpy(X).cuda()
+    dY = torch.empty((4096, 300), dtype=torch.float32, device="cuda")  # ldy > N
+    torch.cuda.synchronize()
+    W.spmm_dev(dX.data_ptr(), 256, dY.data_ptr(), ldx=256, ldy=300)
+    ctx.synchronize()
+    Y = dY[:, :256].cpu().numpy()
+    assert bits_equal(Y, O.orc_csr_spmm(4096, 4096, ip, ix, v, X))
