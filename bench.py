@@ -25,6 +25,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (packed FMA)
+INT8_DENSE_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (the 2:4 instruction doubles K per issue)
 M = K = 4096
 DENSITY = 0.1
 N_MAIN = 256
@@ -59,6 +60,58 @@ def time_gpu(sets, N, steps, warmup, mode):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def bench_sp24(ctx, args):
+    """2:4 int8 GEMM: W 11008 x 4096 (top-2-of-4, per-row int8), X 4096 x 512
+    int8 (scale 0.05), int32 accumulate, requantised int8 output.  One launch
+    includes the activation transpose the kernel reads B from."""
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import workloads
+
+    M, K, N = 11008, 4096, 512
+    q, s = workloads.sp24_int8_weight(M, K, seed=3)
+    X = workloads.quantize_per_tensor(workloads.dense_normal((K, N), 1.0, seed=4), 0.05)
+    sets = []
+    for _ in range(8):  # 8 x (22.5 MB values + 5.6 MB indices) > 256 MB cache
+        W = ctx.sp24_pack(q, s)
+        dX = torch.from_numpy(X).cuda()
+        dY = torch.empty((M, N), dtype=torch.int8, device="cuda")
+        sets.append((W, dX, dY))
+    torch.cuda.synchronize()
+
+    def launch(i):
+        W, dX, dY = sets[i % len(sets)]
+        W.gemm_i8_dev(dX.data_ptr(), N, dY.data_ptr(), x_scale=0.05, out="i8", out_scale=0.6, out_zp=0)
+
+    for i in range(20):
+        launch(i)
+    torch.cuda.synchronize()
+    steps = max(50, args.steps // 10)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        launch(i)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    useful_ops = M * N * K  # 2 ops x the M*N*K/2 kept products
+    byts = M * K // 2 + M * K // 8 + K * N + M * N + 4 * M
+    res = {
+        "ms_per_launch": round(ms, 5),
+        "useful_tops": round(useful_ops / (ms * 1e-3) / 1e12, 1),
+        "dense_equiv_tops": round(2 * useful_ops / (ms * 1e-3) / 1e12, 1),
+        "frac_of_int8_peak": round(useful_ops / (ms * 1e-3) / 1e12 / INT8_DENSE_PEAK_TOPS, 4),
+        "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "shape": [M, K, N],
+    }
+    log(f"sp24 i8: {res}")
+    for W, _, _ in sets:
+        W.free()
+    return res
 
 
 def cpu_baseline(ip, ix, v, X, gpu_Y, budget_s):
@@ -157,6 +210,8 @@ def main():
             W.free()
         del sets
         torch.cuda.empty_cache()
+
+    extra["sp24_i8"] = bench_sp24(ctx, args)
 
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)

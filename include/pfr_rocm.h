@@ -122,6 +122,57 @@ int pfr_gemm_csr_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
                      int transA, const pfr_csr* BT, float alpha, float beta,
                      const float* C, int64_t c_size, float* Y, int mode);
 
+/* ---- 2:4 structured weights (sparse MFMA, gfx950 smfmac) ------------------- */
+
+/* Pack a dense M x K weight that is 2:4 sparse along K (every group of four
+ * consecutive k holds at most two nonzeros: what NMSparsityPruning(2, 4)
+ * produces, nm_sparsity.cpp:45-120) into the compressed operand layout of
+ * the gfx950 sparse MFMA: kept values + 2-bit positions, pre-arranged in
+ * per-lane register order.  W is host, int8 (dtype PFR_I8, the output of
+ * quantize_tensor) or bf16 bits (PFR_BF16).  w_scales holds n_scales = 1
+ * (per-tensor, the reference's QuantParams::scales[0]) or M (per output
+ * channel) symmetric scales; only used by the int8 float/requant outputs.
+ * Fails with PFR_ERR_INVALID_ARG naming the first group with > 2 nonzeros. */
+int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W,
+                  pfr_dtype dtype, const float* w_scales, int64_t n_scales,
+                  pfr_sp24** out);
+int pfr_sp24_info(const pfr_sp24* w, int64_t* M, int64_t* K, pfr_dtype* dtype);
+int pfr_sp24_free(pfr_sp24* w);
+
+/* Output form of the int8 2:4 GEMM. */
+typedef enum pfr_sp24_out {
+    PFR_SP24_OUT_I32 = 0,  /* raw int32 accumulators (exact) */
+    PFR_SP24_OUT_F32 = 1,  /* (float)acc * (w_scale[m] * x_scale)
+                              (quant_ops.cpp:435, :467) */
+    PFR_SP24_OUT_I8 = 2    /* the float above requantised per tensor:
+                              clamp(round(f * (1/out_scale)) + out_zp,
+                              -128, 127) (quant_ops.cpp:500-503 -> :42-47) */
+} pfr_sp24_out;
+
+/* Y[M, N] = W[M, K] . X[K, N] with int8 X (row-major, zero-point 0) and
+ * int32 accumulation: quantization::quantized_matmul
+ * (quant_ops.cpp:387-506) with a 2:4 weight.  Host pointers; Y is int32,
+ * float or int8 per out_kind. */
+int pfr_sp24_gemm_i8(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X,
+                     int64_t N, float x_scale, int out_kind, float out_scale,
+                     int32_t out_zp, void* Y);
+/* Device variant.  X is K x N row-major with row stride ldx; Y row stride
+ * ldy (elements). */
+int pfr_sp24_gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X,
+                         int64_t N, int64_t ldx, float x_scale, int out_kind,
+                         float out_scale, int32_t out_zp, void* Y,
+                         int64_t ldy);
+
+/* Y[M, N] (float) = W[M, K] . X[K, N] with bf16 operands and fp32
+ * accumulation: cpu_gemm on bf16-rounded operands
+ * (half_types.cpp:132-174 then math.cpp:377-438), within the bf16
+ * tolerance (summation order differs).  X is bf16 bits, row-major. */
+int pfr_sp24_gemm_bf16(pfr_ctx* ctx, const pfr_sp24* W, const uint16_t* X,
+                       int64_t N, float* Y);
+int pfr_sp24_gemm_bf16_dev(pfr_ctx* ctx, const pfr_sp24* W,
+                           const uint16_t* X, int64_t N, int64_t ldx,
+                           float* Y, int64_t ldy);
+
 #ifdef __cplusplus
 }
 #endif

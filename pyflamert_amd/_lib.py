@@ -23,6 +23,7 @@ PFR_ERR_NO_DEVICE = 4
 
 PFR_F32, PFR_BF16, PFR_I32, PFR_I8, PFR_U8 = 0, 2, 5, 7, 8
 MODE_STRICT, MODE_FAST = 0, 1
+SP24_OUT_I32, SP24_OUT_F32, SP24_OUT_I8 = 0, 1, 2
 
 _P = C.c_void_p
 _PP = C.POINTER(C.c_void_p)
@@ -48,6 +49,13 @@ SIGNATURES = {
     "pfr_spmm_csr_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64, _INT]),
     "pfr_gemm_csr": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
     "pfr_gemm_csr_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
+    "pfr_sp24_pack": (_INT, [_P, _I64, _I64, _P, _INT, _P, _I64, _PP]),
+    "pfr_sp24_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_INT)]),
+    "pfr_sp24_free": (_INT, [_P]),
+    "pfr_sp24_gemm_i8": (_INT, [_P, _P, _P, _I64, _F, _INT, _F, _I32, _P]),
+    "pfr_sp24_gemm_i8_dev": (_INT, [_P, _P, _P, _I64, _I64, _F, _INT, _F, _I32, _P, _I64]),
+    "pfr_sp24_gemm_bf16": (_INT, [_P, _P, _P, _I64, _P]),
+    "pfr_sp24_gemm_bf16_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64]),
 }
 
 _lib = None

@@ -11,7 +11,8 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import MODE_FAST, MODE_STRICT, PFR_F32, PFR_I8, check
+from ._lib import (MODE_FAST, MODE_STRICT, PFR_BF16, PFR_F32, PFR_I8, SP24_OUT_F32, SP24_OUT_I8,
+                   SP24_OUT_I32, check)
 
 _MODES = {"strict": MODE_STRICT, "fast": MODE_FAST, MODE_STRICT: MODE_STRICT, MODE_FAST: MODE_FAST}
 
@@ -86,6 +87,21 @@ class Context:
                                            threshold, C.byref(h)))
         return CsrWeight(self, h)
 
+    def sp24_pack(self, W, w_scales=None):
+        """2:4 weight [M, K]: int8 (with 1 or M symmetric scales) or bf16 bits
+        (uint16)."""
+        W = np.ascontiguousarray(W)
+        M, K = W.shape
+        h = C.c_void_p()
+        if W.dtype == np.int8:
+            sc = np.ascontiguousarray(np.atleast_1d(w_scales), np.float32)
+            check(self._lib.pfr_sp24_pack(self.handle, M, K, _ptr(W), PFR_I8, _ptr(sc), sc.size, C.byref(h)))
+        elif W.dtype == np.uint16:
+            check(self._lib.pfr_sp24_pack(self.handle, M, K, _ptr(W), PFR_BF16, None, 0, C.byref(h)))
+        else:
+            raise TypeError("2:4 weights are int8 or bf16 bits (uint16)")
+        return Sp24Weight(self, h)
+
     # -- products --------------------------------------------------------
     def gemm_csr(self, A, BT, alpha=1.0, beta=1.0, C_=None, transA=False, mode="strict"):
         """cpu_gemm with the pruned weight in the B position; BT is the CSR of
@@ -144,3 +160,57 @@ class CsrWeight:
     def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict"):
         check(self.ctx._lib.pfr_spmm_csr_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
                                              ldy or N, _MODES[mode]))
+
+
+_SP24_OUT = {"i32": SP24_OUT_I32, "f32": SP24_OUT_F32, "i8": SP24_OUT_I8}
+
+
+class Sp24Weight:
+    """Device-resident 2:4 compressed weight (pfr_sp24)."""
+
+    def __init__(self, ctx, handle):
+        self.ctx = ctx
+        self.handle = handle
+        M, K, dt = C.c_int64(), C.c_int64(), C.c_int()
+        check(ctx._lib.pfr_sp24_info(handle, C.byref(M), C.byref(K), C.byref(dt)))
+        self.M, self.K, self.dtype = M.value, K.value, dt.value
+
+    def free(self):
+        if self.handle:
+            check(self.ctx._lib.pfr_sp24_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.ctx.handle:
+                self.free()
+        except Exception:
+            pass
+
+    def gemm_i8(self, X, x_scale=1.0, out="i32", out_scale=1.0, out_zp=0):
+        """Y = W . X for int8 X [K, N]; out = "i32" | "f32" | "i8"."""
+        X = np.ascontiguousarray(X, np.int8)
+        if X.shape[0] != self.K:
+            raise ValueError("quantized_matmul: inner dimensions must match")
+        N = X.shape[1]
+        dt = {"i32": np.int32, "f32": np.float32, "i8": np.int8}[out]
+        Y = np.empty((self.M, N), dt)
+        check(self.ctx._lib.pfr_sp24_gemm_i8(self.ctx.handle, self.handle, _ptr(X), N, x_scale, _SP24_OUT[out],
+                                             out_scale, out_zp, _ptr(Y)))
+        return Y
+
+    def gemm_i8_dev(self, X_ptr, N, Y_ptr, x_scale=1.0, out="i32", out_scale=1.0, out_zp=0, ldx=None, ldy=None):
+        check(self.ctx._lib.pfr_sp24_gemm_i8_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, x_scale,
+                                                 _SP24_OUT[out], out_scale, out_zp, Y_ptr, ldy or N))
+
+    def gemm_bf16(self, X):
+        """Y (float32) = W . X for bf16-bit X [K, N] (uint16)."""
+        X = np.ascontiguousarray(X, np.uint16)
+        N = X.shape[1]
+        Y = np.empty((self.M, N), np.float32)
+        check(self.ctx._lib.pfr_sp24_gemm_bf16(self.ctx.handle, self.handle, _ptr(X), N, _ptr(Y)))
+        return Y
+
+    def gemm_bf16_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None):
+        check(self.ctx._lib.pfr_sp24_gemm_bf16_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
+                                                   ldy or N))

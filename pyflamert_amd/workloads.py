@@ -55,3 +55,41 @@ def csr_to_dense(M, K, indptr, indices, values):
     rows = np.repeat(np.arange(M), np.diff(indptr))
     d[rows, indices] = values
     return d
+
+
+def round_half_away(x):
+    """std::round on float32 values (half away from zero)."""
+    x = np.asarray(x, np.float32)
+    return (np.sign(x) * np.floor(np.abs(x) + np.float32(0.5))).astype(np.float32)
+
+
+def keep_top2_of_4(w):
+    """2:4 along the last axis: keep the two largest |w| of every group of
+    four consecutive entries (NMSparsityPruning(2, 4) on continuous draws)."""
+    M, K = w.shape
+    g = np.abs(w.reshape(M, K // 4, 4))
+    order = np.argsort(-g, axis=2, kind="stable")[:, :, :2]
+    mask = np.zeros_like(g, dtype=bool)
+    np.put_along_axis(mask, order, True, axis=2)
+    return np.where(mask.reshape(M, K), w, np.float32(0)).astype(np.float32)
+
+
+def symmetric_int8_rows(w):
+    """Per-row symmetric int8: scale = absmax / 127, q = clamp(round(w / s))."""
+    absmax = np.abs(w).max(axis=1).astype(np.float32)
+    scale = np.where(absmax > 0, absmax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    q = np.clip(round_half_away(w * inv[:, None]), -128, 127).astype(np.int8)
+    return q, scale
+
+
+def quantize_per_tensor(x, scale):
+    inv = np.float32(1.0) / np.float32(scale)
+    return np.clip(round_half_away(np.asarray(x, np.float32) * inv), -128, 127).astype(np.int8)
+
+
+def sp24_int8_weight(M, K, seed):
+    """The 2:4 int8 GEMM weight: N(0,1) draws, top-2-of-4 along K, per-row
+    symmetric int8."""
+    w = keep_top2_of_4(np.random.default_rng(seed).standard_normal((M, K), dtype=np.float32))
+    return symmetric_int8_rows(w)

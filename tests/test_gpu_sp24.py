@@ -1,0 +1,151 @@
+"""GPU parity of the 2:4 sparse-MFMA GEMMs.
+
+int8: int32 accumulators and requantised int8 are bit-exact against the
+oracle (quantized_matmul + quantize_tensor) and the golden vectors written
+by the compiled reference; at the full 11008 x 4096 x 512 size every row and
+every column is pinned by exact integer sum identities, and a sample of rows
+by the oracle.  bf16: fp32 output within 1e-2 relative error of the fp32
+product of the bf16-rounded operands (float64 reference; the MFMA sums in a
+different order, so bit equality is not expected).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pyflamert_amd import _lib, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from pyflamert_amd import rocm
+
+    c = rocm.Context(0)
+    yield c
+    c.close()
+
+
+def rand_24_int8(rng, M, K, zero_frac=0.0):
+    w = rng.standard_normal((M, K)).astype(np.float32)
+    w = O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(M, K))
+    if zero_frac:
+        w[rng.random(w.shape) < zero_frac] = 0.0
+    s, _ = O.orc_dynamic_params_per_channel(w.reshape(1, M, K))
+    q = O.orc_quantize(w, s, np.zeros(M, np.int32), O.I8, (1, M, K))
+    return q, s
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 128, 16), (200, 300, 70), (128, 4096, 512), (33, 257, 1)])
+def test_i8_accumulators_exact(ctx, M, K, N):
+    rng = np.random.default_rng(M * 7 + K)
+    K4 = (K + 3) // 4 * 4
+    q, s = rand_24_int8(rng, M, K4, zero_frac=0.1)
+    q = np.ascontiguousarray(q[:, :K])
+    X = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    say(f"sp24 i8 acc M={M} K={K} N={N}")
+    W = ctx.sp24_pack(q, s)
+    Y = W.gemm_i8(X, out="i32")
+    assert np.array_equal(Y, O.orc_int8_matmul_acc(q, X))
+
+
+def test_i8_rowscale_float_and_requant(ctx):
+    rng = np.random.default_rng(11)
+    M, K, N = 96, 512, 80
+    q, s = rand_24_int8(rng, M, K)
+    X = O.orc_quantize(rng.standard_normal((K, N)).astype(np.float32), [0.05], [0], O.I8)
+    say("sp24 i8 per-row scales: float and requant outputs")
+    W = ctx.sp24_pack(q, s)
+    F = W.gemm_i8(X, x_scale=0.05, out="f32")
+    R = O.orc_quantized_matmul_rowscale(q, X, s, 0.05)
+    assert np.array_equal(F.view(np.uint32), R.view(np.uint32))
+    os_, oz = O.orc_dynamic_params(R)
+    for zp in (0, 3, -5):
+        Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=float(os_), out_zp=zp)
+        assert np.array_equal(Q, O.orc_quantize(R, [os_], [zp], O.I8)), zp
+    # scale small enough that outputs saturate and round half away at .5
+    Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=float(os_) / 7.0, out_zp=0)
+    assert np.array_equal(Q, O.orc_quantize(R, [np.float32(os_) / np.float32(7.0)], [0], O.I8))
+
+
+def test_i8_golden(ctx, golden):
+    """quantized_matmul with a per-tensor 2:4 weight and its requant, exactly
+    as the compiled reference produced them."""
+    g = golden("qmatmul.npz")
+    say("sp24 golden qmatmul")
+    W = ctx.sp24_pack(g["sp_wq"], [g["sp_ws"]])
+    F = W.gemm_i8(g["sp_xq"], x_scale=0.05, out="f32")
+    assert np.array_equal(F.view(np.uint32), g["sp_yf"].view(np.uint32))
+    ys, yz = g["sp_y_params"]
+    Q = W.gemm_i8(g["sp_xq"], x_scale=0.05, out="i8", out_scale=float(ys), out_zp=int(yz))
+    assert np.array_equal(Q, g["sp_yq"])
+
+
+def test_i8_full_size_properties(ctx):
+    """W 11008 x 4096 (2:4, per-row int8), X 4096 x 512 int8 (scale 0.05):
+    exact row sums and column sums of the int32 accumulators, plus 192 rows
+    checked against the oracle (accumulators and requantised int8)."""
+    M, K, N = 11008, 4096, 512
+    say("sp24 full size: generating")
+    q, s = workloads.sp24_int8_weight(M, K, seed=3)
+    X = workloads.quantize_per_tensor(workloads.dense_normal((K, N), 1.0, seed=4), 0.05)
+    W = ctx.sp24_pack(q, s)
+    say("sp24 full size: int32")
+    Y = W.gemm_i8(X, out="i32")
+    q64, x64 = q.astype(np.int64), X.astype(np.int64)
+    assert np.array_equal(Y.astype(np.int64).sum(axis=1), q64 @ x64.sum(axis=1))
+    assert np.array_equal(Y.astype(np.int64).sum(axis=0), q64.sum(axis=0) @ x64)
+    rows = np.random.default_rng(5).choice(M, 192, replace=False)
+    rows.sort()
+    acc = O.orc_int8_matmul_acc(q[rows], X)
+    assert np.array_equal(Y[rows], acc)
+    say("sp24 full size: requant")
+    F = O.orc_quantized_matmul_rowscale(q[rows], X, s[rows], 0.05)
+    os_, _ = O.orc_dynamic_params(F)
+    Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=float(os_), out_zp=0)
+    assert np.array_equal(Q[rows], O.orc_quantize(F, [os_], [0], O.I8))
+
+
+def rne_bf16(x):
+    """Round-to-nearest-even bf16 bits of finite float32 values."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (200, 512, 96), (1024, 2048, 256)])
+def test_bf16_within_tolerance(ctx, M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    w = rng.standard_normal((M, K)).astype(np.float32)
+    w = O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(M, K))
+    wb = rne_bf16(w)
+    xb = rne_bf16(rng.standard_normal((K, N)).astype(np.float32))
+    say(f"sp24 bf16 M={M} K={K} N={N}")
+    W = ctx.sp24_pack(wb.astype(np.uint16))
+    Y = W.gemm_bf16(xb.astype(np.uint16))
+    R = O.orc_bf16_to_f32(wb).astype(np.float64) @ O.orc_bf16_to_f32(xb).astype(np.float64)
+    err = np.abs(Y - R) / np.maximum(np.abs(R), 1e-3 * np.abs(R).max())
+    assert err.max() <= 1e-2, err.max()
+    F32 = O.orc_gemm(O.orc_bf16_to_f32(wb), O.orc_bf16_to_f32(xb))   # cpu_gemm on bf16 operands
+    assert (np.abs(Y - F32) <= 1e-2 * np.maximum(np.abs(F32), 1e-3 * np.abs(F32).max())).all()
+
+
+def test_rejects_non_24(ctx):
+    say("sp24 argument errors")
+    w = np.zeros((16, 8), np.int8)
+    w[3, 4:7] = 1  # three nonzeros in one group
+    with pytest.raises(_lib.InvalidArgument, match="not 2:4 sparse: row 3, k 4..7"):
+        ctx.sp24_pack(w, [1.0])
+    with pytest.raises(_lib.InvalidArgument, match="scales"):
+        ctx.sp24_pack(np.zeros((16, 8), np.int8), np.ones(3, np.float32))
+    W = ctx.sp24_pack(np.zeros((16, 8), np.int8), [1.0])
+    with pytest.raises(ValueError, match="inner dimensions"):
+        W.gemm_i8(np.zeros((9, 4), np.int8))
+    with pytest.raises(_lib.InvalidArgument, match="output scale"):
+        W.gemm_i8(np.zeros((8, 4), np.int8), x_scale=1.0, out="i8", out_scale=0.0)
