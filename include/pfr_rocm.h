@@ -173,6 +173,18 @@ int pfr_sp24_gemm_bf16_dev(pfr_ctx* ctx, const pfr_sp24* W,
                            const uint16_t* X, int64_t N, int64_t ldx,
                            float* Y, int64_t ldy);
 
+/* ---- graph neighbours kept on the device ---------------------------------- */
+
+/* Relu, activation.cpp:45-60 (bit-exact).  Host pointers; _dev: device. */
+int pfr_relu(pfr_ctx* ctx, const float* x, int64_t n, float* y);
+int pfr_relu_dev(pfr_ctx* ctx, const float* x, int64_t n, float* y);
+/* Softmax over the middle extent of x viewed as [outer, axis, inner],
+ * activation.cpp:157-237 (same order and special cases; device expf). */
+int pfr_softmax(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
+                int64_t inner, float* y);
+int pfr_softmax_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
+                    int64_t inner, float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,10 @@ SIGNATURES = {
     "pfr_sp24_gemm_i8_dev": (_INT, [_P, _P, _P, _I64, _I64, _F, _INT, _F, _I32, _P, _I64]),
     "pfr_sp24_gemm_bf16": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_sp24_gemm_bf16_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64]),
+    "pfr_relu": (_INT, [_P, _P, _I64, _P]),
+    "pfr_relu_dev": (_INT, [_P, _P, _I64, _P]),
+    "pfr_softmax": (_INT, [_P, _P, _I64, _I64, _I64, _P]),
+    "pfr_softmax_dev": (_INT, [_P, _P, _I64, _I64, _I64, _P]),
 }
 
 _lib = None

@@ -1,0 +1,175 @@
+// The rocm:: kernels registered in the OperatorRegistry.  Each is an OpFunc
+// with the reference's calling convention: borrowed host inputs in, owning
+// host outputs out, synchronous.  The arithmetic runs on the GPU through the
+// C ABI; shapes, attributes and error texts follow the reference kernels
+// (src/backends/cpu/ops/math.cpp:268-438, quantized_ops.cpp:77-167,
+// activation.cpp:45-60 and :157-237).
+#include <stdexcept>
+#include <string>
+
+#include "pyflame_rt/errors.hpp"
+#include "rocm_executor.hpp"
+
+namespace pyflame_rt {
+namespace {
+
+RocmExecutor& exec() {
+    RocmExecutor* e = RocmExecutor::current();
+    if (!e) throw std::runtime_error("rocm kernel called outside RocmExecutor::execute");
+    return *e;
+}
+
+void need_inputs(const std::vector<const Tensor*>& in, size_t n, const char* op) {
+    if (in.size() < n)
+        throw std::invalid_argument(std::string(op) + ": expected at least " + std::to_string(n) + " inputs, got " +
+                                    std::to_string(in.size()));
+}
+
+void need_f32(const Tensor& t, const char* what) {
+    if (t.dtype() != DType::Float32)
+        throw std::invalid_argument(std::string(what) + " must be float32, got " + dtype_name(t.dtype()));
+}
+
+// MatMul with one pruned, initializer operand (math.cpp:268-374 semantics).
+std::vector<Tensor> rocm_matmul(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 2, "MatMul");
+    RocmExecutor& ex = exec();
+    const auto* w = ex.weight(ctx.node);
+    const Tensor& a = *in[0];
+    const Tensor& b = *in[1];
+    if (a.ndim() < 2 || b.ndim() < 2) throw std::invalid_argument("MatMul: inputs must have at least 2 dimensions");
+    const int64_t Ka = a.shape().back(), Kb = b.shape()[b.ndim() - 2];
+    if (Ka != Kb)
+        throw std::invalid_argument("MatMul: incompatible dimensions - A has inner dim " + std::to_string(Ka) +
+                                    ", B has inner dim " + std::to_string(Kb));
+    if (w && w->kind == RocmExecutor::DeviceWeight::CsrB) {
+        // A [..., M, K] (broadcast over the batch dims) x W [K, N]: rows flatten.
+        need_f32(a, "MatMul input A");
+        const int64_t N = b.shape()[1];
+        std::vector<int64_t> os(a.shape().begin(), a.shape().end() - 1);
+        os.push_back(N);
+        Tensor out(os, DType::Float32);
+        const int64_t rows = a.num_elements() / Ka;
+        pfr_check(pfr_gemm_csr(ex.ctx(), a.data_ptr<float>(), rows, Ka, 0, w->csr, 1.0f, 1.0f, nullptr, 0,
+                               out.data_ptr<float>(), ex.math_mode()));
+        return {std::move(out)};
+    }
+    if (w && w->kind == RocmExecutor::DeviceWeight::CsrA) {
+        need_f32(b, "MatMul input B");
+        if (b.ndim() != 2) throw std::invalid_argument("MatMul: a pruned first operand needs a 2-D second operand");
+        const int64_t M = a.shape()[0], N = b.shape()[1];
+        Tensor out({M, N}, DType::Float32);
+        pfr_check(pfr_spmm_csr(ex.ctx(), w->csr, b.data_ptr<float>(), N, out.data_ptr<float>(), ex.math_mode()));
+        return {std::move(out)};
+    }
+    throw std::runtime_error("MatMul: neither operand is a float32 2-D initializer; the rocm backend runs "
+                             "pruned-weight products only");
+}
+
+// Gemm with a pruned initializer B (math.cpp:377-438 semantics).
+std::vector<Tensor> rocm_gemm(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 2, "Gemm");
+    RocmExecutor& ex = exec();
+    const auto* w = ex.weight(ctx.node);
+    const Tensor& A = *in[0];
+    const Tensor& B = *in[1];
+    const Tensor* C = in.size() > 2 ? in[2] : nullptr;
+    if (A.ndim() < 2 || B.ndim() < 2) throw std::invalid_argument("Gemm input A/B must have at least 2 dimensions");
+    if (!w || w->kind != RocmExecutor::DeviceWeight::CsrB)
+        throw std::runtime_error("Gemm: B is not a float32 2-D initializer; the rocm backend runs pruned-weight "
+                                 "products only");
+    need_f32(A, "Gemm input A");
+    const float alpha = ctx.node->get_attr<float>("alpha", 1.0f);
+    const float beta = ctx.node->get_attr<float>("beta", 1.0f);
+    const int64_t ta = ctx.node->get_attr<int64_t>("transA", 0);
+    const int64_t tb = ctx.node->get_attr<int64_t>("transB", 0);
+    const int64_t M = ta ? A.shape()[1] : A.shape()[0];
+    const int64_t Ka = ta ? A.shape()[0] : A.shape()[1];
+    const int64_t Kb = tb ? B.shape()[1] : B.shape()[0];
+    const int64_t N = tb ? B.shape()[0] : B.shape()[1];
+    if (Ka != Kb)
+        throw std::invalid_argument("Gemm: incompatible dimensions - A has K=" + std::to_string(Ka) +
+                                    ", B has K=" + std::to_string(Kb));
+    Tensor out({M, N}, DType::Float32);
+    const float* c = nullptr;
+    int64_t c_size = 0;
+    if (C && C->num_elements() > 0) {
+        need_f32(*C, "Gemm input C");
+        c = C->data_ptr<float>();
+        c_size = C->num_elements();
+    }
+    pfr_check(pfr_gemm_csr(ex.ctx(), A.data_ptr<float>(), M, Ka, (int)ta, w->csr, alpha, beta, c, c_size,
+                           out.data_ptr<float>(), ex.math_mode()));
+    return {std::move(out)};
+}
+
+// QuantizedMatMul with a 2:4 int8 initializer A (quantized_ops.cpp:77-167):
+// out = (float)acc * (a_scale * b_scale), int32 accumulation.
+std::vector<Tensor> rocm_qmatmul(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 2, "QuantizedMatMul");
+    RocmExecutor& ex = exec();
+    const auto* w = ex.weight(ctx.node);
+    const Tensor& a = *in[0];
+    const Tensor& b = *in[1];
+    if ((a.dtype() != DType::Int8 && a.dtype() != DType::UInt8))
+        throw std::invalid_argument("QuantizedMatMul: input A must be Int8 or UInt8");
+    if ((b.dtype() != DType::Int8 && b.dtype() != DType::UInt8))
+        throw std::invalid_argument("QuantizedMatMul: input B must be Int8 or UInt8");
+    if (a.ndim() < 2 || b.ndim() < 2)
+        throw std::invalid_argument("QuantizedMatMul: inputs must have at least 2 dimensions");
+    const int64_t K = a.shape().back(), Kb = b.shape()[b.ndim() - 2];
+    if (K != Kb)
+        throw std::invalid_argument("QuantizedMatMul: inner dimensions must match (got " + std::to_string(K) +
+                                    " and " + std::to_string(Kb) + ")");
+    if (!w || w->kind != RocmExecutor::DeviceWeight::Sp24A || b.ndim() != 2)
+        throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D int8 initializer A that is 2:4 "
+                                 "sparse along K, zero points 0, and a 2-D B");
+    const float b_scale = ctx.node->get_attr<float>("b_scale", 1.0f);
+    const int64_t M = a.shape()[0], N = b.shape()[1];
+    Tensor out({M, N}, DType::Float32);
+    pfr_check(pfr_sp24_gemm_i8(ex.ctx(), w->sp24, static_cast<const int8_t*>(b.data()), N, b_scale,
+                               PFR_SP24_OUT_F32, 1.0f, 0, out.data()));
+    return {std::move(out)};
+}
+
+std::vector<Tensor> rocm_relu(const std::vector<const Tensor*>& in, const OpContext&) {
+    need_inputs(in, 1, "Relu");
+    const Tensor& x = *in[0];
+    need_f32(x, "Relu input");
+    Tensor out(x.shape(), x.dtype());
+    pfr_check(pfr_relu(exec().ctx(), x.data_ptr<float>(), x.num_elements(), out.data_ptr<float>()));
+    return {std::move(out)};
+}
+
+std::vector<Tensor> rocm_softmax(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 1, "Softmax");
+    const Tensor& x = *in[0];
+    need_f32(x, "Softmax input");
+    int64_t axis = ctx.node->get_attr<int64_t>("axis", -1);
+    const int64_t nd = (int64_t)x.ndim();
+    if (axis < -nd || axis >= nd)
+        throw std::invalid_argument("Softmax: axis " + std::to_string(axis) + " out of range for " +
+                                    std::to_string(nd) + "-D input");
+    if (axis < 0) axis += nd;
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= x.shape()[i];
+    for (int64_t i = axis + 1; i < nd; ++i) inner *= x.shape()[i];
+    Tensor out(x.shape(), x.dtype());
+    pfr_check(pfr_softmax(exec().ctx(), x.data_ptr<float>(), outer, x.shape()[axis], inner, out.data_ptr<float>()));
+    return {std::move(out)};
+}
+
+struct RocmOpsRegistrar {
+    RocmOpsRegistrar() {
+        auto& r = OperatorRegistry::instance();
+        r.register_op("rocm::MatMul", rocm_matmul);
+        r.register_op("rocm::Gemm", rocm_gemm);
+        r.register_op("rocm::QuantizedMatMul", rocm_qmatmul);
+        r.register_op("rocm::Relu", rocm_relu);
+        r.register_op("rocm::Softmax", rocm_softmax);
+    }
+};
+RocmOpsRegistrar registrar;
+
+}  // namespace
+}  // namespace pyflame_rt

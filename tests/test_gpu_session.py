@@ -1,0 +1,135 @@
+"""End-to-end sessions on the MI355X backend: the 784-512-10 MLP model
+written by the compiled reference, run with device="rocm", against the
+reference executor's outputs; plus MatMul / QuantizedMatMul graphs and the
+backend's error paths."""
+import gzip
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pyflamert_amd import pfm, session
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def mlp(tmp_path_factory):
+    p = tmp_path_factory.mktemp("m") / "mlp.pfm"
+    p.write_bytes(gzip.open(os.path.join(GOLD, "mlp_784_512_10.pfm.gz")).read())
+    return str(p)
+
+
+def test_mlp_against_reference_executor(mlp, golden, tmp_path):
+    g = golden("mlp.npz")
+    say("MLP 784-512-10 on device=rocm")
+    s = session.InferenceSession(mlp, session.SessionOptions(device="rocm"))
+    assert s.get_providers() == ["ROCMExecutionProvider"]
+    assert [i.name for i in s.get_inputs()] == ["x"] and s.get_inputs()[0].shape == [32, 784]
+    (y,) = s.run(None, {"x": g["x"]})
+    # Softmax uses the device expf: a few ulp from glibc's
+    assert np.abs(y - g["y"]).max() <= 4e-7
+    assert np.array_equal(np.argmax(y, 1), np.argmax(g["y"], 1))
+    # The pruned Gemm itself is bit-exact: expose h1 as a graph output.
+    m = pfm.load(mlp)
+    m["outputs"].append(("h1", 0, [32, 512]))
+    p2 = str(tmp_path / "mlp_h1.pfm")
+    pfm.save(m, p2)
+    s2 = session.InferenceSession(p2, session.SessionOptions(device="rocm"))
+    y2, h1 = s2.run(["y", "h1"], {"x": g["x"]})
+    assert np.array_equal(bits(h1), bits(g["h1"]))
+    assert np.array_equal(bits(y2), bits(y))
+    # relu and the second Gemm exactly as the oracle computes them from h1
+    a1 = O.orc_relu(h1)
+    w2, b2 = m["initializers"]["fc2.weight"], m["initializers"]["fc2.bias"]
+    z2 = O.orc_gemm(a1, w2, b2)
+    assert np.abs(y - O.orc_softmax(z2)).max() <= 4e-7
+    # fast mode: same graph with fused multiply-add sums
+    s3 = session.InferenceSession(mlp, session.SessionOptions(device="rocm", math_mode="fast"))
+    (y3,) = s3.run(None, {"x": g["x"]})
+    assert np.abs(y3 - g["y"]).max() <= 1e-5
+
+
+def test_kat_and_batched_matmul(tmp_path, golden):
+    k = golden("kat_matmul.npz")
+    say("MatMul KAT through a session")
+    m = {"name": "kat", "inputs": [("a", 0, [2, 3])], "outputs": [("c", 0, [2, 2])],
+         "initializers": {"b": k["b"]}, "nodes": [("matmul_0", "MatMul", ["a", "b"], ["c"], {})]}
+    p = str(tmp_path / "kat.pfm")
+    pfm.save(m, p)
+    (c,) = session.InferenceSession(p).run(None, {"a": k["a"]})
+    assert c.tolist() == [[22.0, 28.0], [49.0, 64.0]]
+    g = golden("matmul.npz")
+    a, b, ref = g["c0_a"], g["c0_b"], g["c0_out"]      # [3,4,5] x [5,6]
+    m = {"name": "bm", "inputs": [("a", 0, list(a.shape))], "outputs": [("c", 0, list(ref.shape))],
+         "initializers": {"w": b}, "nodes": [("mm", "MatMul", ["a", "w"], ["c"], {})]}
+    p = str(tmp_path / "bm.pfm")
+    pfm.save(m, p)
+    (c,) = session.InferenceSession(p).run(None, {"a": a})
+    assert np.array_equal(bits(c), bits(ref))
+    # pruned weight in the first position: Y = W . X
+    rng = np.random.default_rng(1)
+    W = rng.standard_normal((64, 48)).astype(np.float32)
+    W[rng.random(W.shape) < 0.9] = 0
+    X = rng.standard_normal((48, 7)).astype(np.float32)
+    m = {"name": "wx", "inputs": [("x", 0, [48, 7])], "outputs": [("y", 0, [64, 7])],
+         "initializers": {"w": W}, "nodes": [("mm", "MatMul", ["w", "x"], ["y"], {})]}
+    p = str(tmp_path / "wx.pfm")
+    pfm.save(m, p)
+    (y,) = session.InferenceSession(p).run(None, {"x": X})
+    assert np.array_equal(bits(y), bits(O.orc_matmul(W, X)))
+
+
+def test_quantized_matmul_24(tmp_path, golden):
+    """QuantizedMatMul(W int8 2:4 initializer, X int8) -> float, against the
+    reference op's output."""
+    g = golden("qmatmul.npz")
+    say("QuantizedMatMul with a 2:4 initializer")
+    wq, xq, ws = g["sp_wq"], g["sp_xq"], float(g["sp_ws"])
+    m = {"name": "q", "inputs": [("x", 7, list(xq.shape))], "outputs": [("y", 0, [wq.shape[0], xq.shape[1]])],
+         "initializers": {"w": wq},
+         "nodes": [("qmm", "QuantizedMatMul", ["w", "x"], ["y"], {"a_scale": ws, "b_scale": 0.05})]}
+    p = str(tmp_path / "q.pfm")
+    pfm.save(m, p)
+    (y,) = session.InferenceSession(p).run(None, {"x": xq})
+    ref = O.orc_cpu_quantized_matmul(wq, xq, np.float32(ws), np.float32(0.05))
+    assert np.array_equal(bits(y), bits(ref))
+    assert np.array_equal(bits(y), bits(g["sp_yf"]))
+
+
+def test_backend_errors(tmp_path):
+    say("rocm backend error paths")
+    base = {"name": "e", "inputs": [("a", 0, [2, 3]), ("b", 0, [3, 2])], "outputs": [("c", 0, [2, 2])],
+            "initializers": {}}
+    m = dict(base, nodes=[("conv", "Conv", ["a", "b"], ["c"], {})])
+    p = str(tmp_path / "conv.pfm")
+    pfm.save(m, p)
+    s = session.InferenceSession(p)
+    with pytest.raises(session.UnsupportedOperatorError, match="'Conv' is not supported by the 'rocm' backend"):
+        s.run(None, {"a": np.ones((2, 3), np.float32), "b": np.ones((3, 2), np.float32)})
+    m = dict(base, nodes=[("mm", "MatMul", ["a", "b"], ["c"], {})])
+    p = str(tmp_path / "act.pfm")
+    pfm.save(m, p)
+    s = session.InferenceSession(p)
+    with pytest.raises(session.BackendError, match=r"\[mm\] MatMul: neither operand"):
+        s.run(None, {"a": np.ones((2, 3), np.float32), "b": np.ones((3, 2), np.float32)})
+    with pytest.raises(session.PyFlameRTError, match="Missing required input 'b'"):
+        s.run(None, {"a": np.ones((2, 3), np.float32)})
+    with pytest.raises(session.PyFlameRTError, match="dimension 1 has size 4 but expected 3"):
+        s.run(None, {"a": np.ones((2, 4), np.float32), "b": np.ones((3, 2), np.float32)})
+    with pytest.raises(session.PyFlameRTError, match="has dtype int8 but expected float32"):
+        s.run(None, {"a": np.ones((2, 3), np.int8), "b": np.ones((3, 2), np.float32)})
+    name, ops = s.supported_ops()
+    assert name == "rocm" and {"MatMul", "Gemm", "QuantizedMatMul", "Relu", "Softmax"} <= set(ops)
