@@ -97,17 +97,30 @@ struct pfr_csr {
     int32_t* spmv_blocks = nullptr;  // [n_spmv_blocks + 1] first row of each
     int64_t n_spmv_blocks = 0;
     int32_t max_row_nnz = 0;
-    // Columns ascend within every row (the order to_sparse produces).  Only
-    // then is the K-chunk table valid and the LDS-tiled kernel usable.
+    // Columns ascend within every row (the order to_sparse produces).
     bool cols_sorted = false;
-    // chunk_ptr[r * (n_chunks + 1) + c]: first nnz of row r with column
-    // >= c * kChunkK (c = n_chunks gives the row end).
-    int32_t* chunk_ptr = nullptr;
-    int32_t n_chunks = 0;
+    // Sliced-ELL copy of a float32 weight for the column-slice kernel (null
+    // when the shape does not qualify).  Rows are reordered into slabs of
+    // kSellRows; K is cut into chunks of sell_kc rows.  For slab s and chunk
+    // c, sell_soff[s * (sell_nch + 1) + c] is the first int4 of its run of
+    // 8-step groups (the run ends at entry c + 1).  A group is 64 int4: entry
+    // 4*r + j holds steps 2j and 2j+1 of the slab's row r as {byte offset of
+    // the column's row in the chunk's LDS copy, value bits} twice.  Every
+    // run is a multiple of kSellStepPad steps; padding steps point at the
+    // zero row (offset sell_kc * 64, value +0).
+    int32_t* sell_perm = nullptr;  // [sell_nslab * kSellRows] row of each slab lane, -1 none
+    int32_t* sell_soff = nullptr;  // [sell_nslab * (sell_nch + 1)]
+    int4* sell_blk = nullptr;      // [sell_len + kSellTail]
+    int32_t sell_nslab = 0, sell_nch = 0, sell_kc = 0;
+    int64_t sell_len = 0;
 };
 
 namespace pfr {
-constexpr int kChunkK = 256;  // K rows of X staged per LDS chunk
+constexpr int kSellRows = 16;      // rows per slab (one wave: 4 lanes x 4 columns per row)
+constexpr int kSellCols = 16;      // columns of X per workgroup slice
+constexpr int kSellMaxKC = 2048;   // K rows per LDS chunk (2048 x 64 B = 128 KiB)
+constexpr int kSellStepPad = 16;   // steps per (slab, chunk) run are a multiple of this
+constexpr int kSellTail = 128;     // int4 after the last run, read by the unconditional prefetch
 }
 
 namespace pfr {

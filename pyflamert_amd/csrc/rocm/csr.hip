@@ -1,6 +1,11 @@
 // Device-resident CSR weights: upload from the reference's SparseTensor
 // arrays or from a dense zero-filled pruned weight, with the range checks the
-// reference leaves out, and the row-block table used by the vector kernel.
+// reference leaves out, the row-block table used by the vector kernel and the
+// sliced-ELL copy used by the column-slice kernel.
+#include <algorithm>
+#include <climits>
+#include <cstring>
+#include <numeric>
 #include <vector>
 
 #include "common.hpp"
@@ -28,7 +33,7 @@ T* dev_alloc_copy(const T* host, int64_t count, hipStream_t s) {
 void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
-                    (void*)w->chunk_ptr})
+                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -52,6 +57,87 @@ std::vector<int32_t> spmv_blocks(const std::vector<int32_t>& rowptr, int64_t M) 
     }
     starts.push_back((int32_t)M);
     return starts;
+}
+
+// Sliced-ELL copy (layout described at pfr_csr::sell_blk).  Each row keeps
+// its storage order inside a chunk and chunks are visited in order, so the
+// copy needs the chunk index to be non-decreasing along every row (always
+// true for one chunk, and for ascending columns).  Rows are ordered so that
+// the rows of a slab have similar counts in every chunk, which keeps the
+// padding to the slab maximum small: sorted by their chunk-0 count, then
+// within 8 buckets by their chunk-1 count, within 64 by chunk 2, and so on.
+void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
+                const float* vals, hipStream_t s) {
+    const int64_t M = w->M, K = w->K;
+    if (M == 0 || K == 0 || w->nnz == 0) return;
+    const int64_t kc = std::min<int64_t>(K, pfr::kSellMaxKC);
+    const int64_t nch = (K + kc - 1) / kc;
+    if (M * nch > (int64_t(1) << 26)) return;  // count table too large: keep the row kernels
+    for (int64_t r = 0; r < M; ++r)
+        for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
+            if (col[j] / kc < col[j - 1] / kc) return;
+    std::vector<int32_t> cnt((size_t)(M * nch), 0);
+    for (int64_t r = 0; r < M; ++r)
+        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cnt[(size_t)(r * nch + col[j] / kc)];
+    const int64_t R = pfr::kSellRows;
+    const int64_t nslab = (M + R - 1) / R;
+    std::vector<int32_t> order((size_t)M);
+    std::iota(order.begin(), order.end(), 0);
+    int64_t group = M;
+    for (int64_t c = 0; c < nch && group >= R; ++c) {
+        for (int64_t g0 = 0; g0 < M; g0 += group) {
+            const int64_t g1 = std::min(M, g0 + group);
+            std::stable_sort(order.begin() + g0, order.begin() + g1, [&](int32_t a, int32_t b) {
+                return cnt[(size_t)(a * nch + c)] > cnt[(size_t)(b * nch + c)];
+            });
+        }
+        group = std::max<int64_t>(R, (group / 8 + R - 1) / R * R);
+        if (group == R) break;
+    }
+    std::vector<int64_t> off((size_t)(nslab * nch + 1), 0);
+    for (int64_t sl = 0; sl < nslab; ++sl)
+        for (int64_t c = 0; c < nch; ++c) {
+            int32_t mx = 0;
+            for (int64_t i = sl * R; i < std::min(M, sl * R + R); ++i)
+                mx = std::max(mx, cnt[(size_t)(order[(size_t)i] * nch + c)]);
+            const int64_t steps = (mx + pfr::kSellStepPad - 1) / pfr::kSellStepPad * pfr::kSellStepPad;
+            off[(size_t)(sl * nch + c + 1)] = off[(size_t)(sl * nch + c)] + steps / 8 * 64;
+        }
+    const int64_t len = off.back();
+    if (len + pfr::kSellTail > INT32_MAX) return;
+    const int32_t pad_off = (int32_t)(kc * 64);
+    std::vector<int4> blk((size_t)(len + pfr::kSellTail));
+    for (auto& b : blk) b = make_int4(pad_off, 0, pad_off, 0);
+    std::vector<int32_t> perm((size_t)(nslab * R), -1);
+    std::vector<int32_t> t((size_t)nch);
+    for (int64_t i = 0; i < M; ++i) {
+        const int32_t row = order[(size_t)i];
+        perm[(size_t)i] = row;
+        const int64_t sl = i / R, r = i % R;
+        std::fill(t.begin(), t.end(), 0);
+        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
+            const int64_t c = col[j] / kc;
+            const int32_t step = t[(size_t)c]++;
+            int4& b = blk[(size_t)(off[(size_t)(sl * nch + c)] + (step / 8) * 64 + 4 * r + (step % 8) / 2)];
+            int32_t bits;
+            std::memcpy(&bits, &vals[j], 4);
+            const int32_t o = (int32_t)((col[j] - c * kc) * 64);
+            if (step % 2 == 0) { b.x = o; b.y = bits; } else { b.z = o; b.w = bits; }
+        }
+    }
+    std::vector<int32_t> soff((size_t)(nslab * (nch + 1)));
+    for (int64_t sl = 0; sl < nslab; ++sl)
+        for (int64_t c = 0; c <= nch; ++c)  // c == nch: end of the slab's last run
+            soff[(size_t)(sl * (nch + 1) + c)] = (int32_t)off[(size_t)(sl * nch + c)];
+    w->sell_perm = dev_alloc_copy(perm.data(), (int64_t)perm.size(), s);
+    w->sell_soff = dev_alloc_copy(soff.data(), (int64_t)soff.size(), s);
+    w->sell_blk = dev_alloc_copy(blk.data(), (int64_t)blk.size(), s);
+    w->sell_nslab = (int32_t)nslab;
+    w->sell_nch = (int32_t)nch;
+    w->sell_kc = (int32_t)kc;
+    w->sell_len = len;
+    // the host copies must outlive the asynchronous uploads
+    PFR_HIP(hipStreamSynchronize(s));
 }
 
 pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
@@ -83,20 +169,7 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
             for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
                 if (col[j] <= col[j - 1]) { sorted = false; break; }
         w->cols_sorted = sorted;
-        if (sorted && M > 0) {
-            const int64_t nc = (K + pfr::kChunkK - 1) / pfr::kChunkK;
-            w->n_chunks = (int32_t)nc;
-            std::vector<int32_t> cp((size_t)(M * (nc + 1)));
-            for (int64_t r = 0; r < M; ++r) {
-                int32_t j = rowptr[r];
-                for (int64_t c = 0; c <= nc; ++c) {
-                    const int64_t lim = c * pfr::kChunkK;
-                    while (j < rowptr[r + 1] && col[j] < lim) ++j;
-                    cp[(size_t)(r * (nc + 1) + c)] = (c == nc) ? rowptr[r + 1] : j;
-                }
-            }
-            w->chunk_ptr = dev_alloc_copy(cp.data(), (int64_t)cp.size(), s);
-        }
+        if (vdt == PFR_F32) build_sell(w, rowptr, col, static_cast<const float*>(vals), s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {

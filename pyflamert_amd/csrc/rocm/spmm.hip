@@ -6,6 +6,7 @@
 // sparse_tensor.cpp:500-510 / :543-548).  The whole file is compiled with
 // floating-point contraction off; fast mode asks for fmaf explicitly.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -16,6 +17,7 @@ namespace {
 constexpr int kWaves = 4;  // waves per 256-thread workgroup
 constexpr int kSpmvThreads = 512;  // threads of the vector kernel's workgroup
 constexpr int kSpmvCap = 4096;     // products staged per workgroup chunk (16 KB)
+constexpr int64_t kSellMinN = 16;  // column-slice kernel from this many columns on
 
 template <bool FAST>
 __device__ __forceinline__ float madd(float acc, float w, float x) {
@@ -205,6 +207,133 @@ __global__ __launch_bounds__(256) void k_scale(const float* __restrict__ A, int6
     if (i < n) out[i] = alpha * A[i];
 }
 
+template <int I, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < E) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, E>(f);
+    }
+}
+
+// Column-slice kernel over the sliced-ELL copy (layout at pfr_csr::sell_blk).
+// A workgroup of W waves owns W slabs (16 rows each) and one 16-column slice
+// of X.  For every K chunk it stages X[chunk rows, slice] (64 B per row) in
+// LDS, then each wave walks its slab: lane 4r+q accumulates columns 4q..4q+3
+// of slab row r.  The pairs of a step come from one int4 per lane per eight
+// steps, broadcast to the row's four lanes with quad_perm DPP (which the
+// compiler folds into the address add and the multiply).  Products are added
+// in the row's storage order, so strict mode matches the row kernels bit for
+// bit; padding steps add RN(+0 * +0) = +0, which leaves any sum unchanged
+// (an accumulator that starts at +0 never becomes -0 under RN addition).
+template <bool FAST, bool XVEC, int W>
+__global__ __launch_bounds__(64 * W) void k_spmm_sell(
+    int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ soff, const int4* __restrict__ blk, const float* __restrict__ X,
+    int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, int yvec,
+    const float* __restrict__ bias, int64_t c_size, float beta) {
+    extern __shared__ float4 xs[];  // [(kc + 1) * 4]: kc rows of 16 floats, then a zero row
+    constexpr int NT = 64 * W;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, q = lane & 3;
+    const int slab = __builtin_amdgcn_readfirstlane((int)blockIdx.x * W + (tid >> 6));
+    const int n0 = (int)blockIdx.y * pfr::kSellCols;
+    const char* xb = reinterpret_cast<const char*>(xs) + q * 16;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    if (tid < 4) xs[kc * 4 + tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int slots = kc * 4;
+    for (int c = 0; c < nch; ++c) {
+        if (c) __syncthreads();  // every wave is done with the previous chunk
+        const int k0 = c * kc;
+        const int rows = min(kc, K - k0);
+        for (int base = 0; base < slots; base += 8 * NT) {
+            float4 st[8];
+            if constexpr (XVEC) {
+                // unconditional loads from clamped addresses, selected afterwards,
+                // so the eight loads are in flight together
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int e = min(base + tid + i * NT, slots - 1);
+                    const int k = k0 + min(e >> 2, rows - 1);
+                    const int n = min(n0 + (e & 3) * 4, N - 4);
+                    st[i] = *reinterpret_cast<const float4*>(X + (int64_t)k * ldx + n);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = base + tid + i * NT;
+                if (e < slots) {
+                    const int kr = e >> 2, n = n0 + (e & 3) * 4;
+                    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (kr < rows) {
+                        const float* xr = X + (int64_t)(k0 + kr) * ldx;
+                        if constexpr (XVEC) {
+                            if (n < N) v = st[i];
+                        } else {
+                            if (n < N) v.x = xr[n];
+                            if (n + 1 < N) v.y = xr[n + 1];
+                            if (n + 2 < N) v.z = xr[n + 2];
+                            if (n + 3 < N) v.w = xr[n + 3];
+                        }
+                    }
+                    xs[e] = v;
+                }
+            }
+        }
+        __syncthreads();
+        if (slab < nslab) {
+            const int s0 = soff[slab * (nch + 1) + c], s1 = soff[slab * (nch + 1) + c + 1];
+            auto comp = [&](const int4 w) {
+                float4 xv[8];
+                static_for<0, 8>([&](auto tc) {
+                    constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;  // quad_perm [j,j,j,j]
+                    const int o = __builtin_amdgcn_mov_dpp((t & 1) ? w.z : w.x, ctrl, 0xF, 0xF, true);
+                    xv[t] = *reinterpret_cast<const float4*>(xb + o);
+                });
+                static_for<0, 8>([&](auto tc) {
+                    constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+                    const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
+                    a0 = madd<FAST>(a0, wv, xv[t].x);
+                    a1 = madd<FAST>(a1, wv, xv[t].y);
+                    a2 = madd<FAST>(a2, wv, xv[t].z);
+                    a3 = madd<FAST>(a3, wv, xv[t].w);
+                });
+            };
+            // groups of 8 steps, two per iteration (runs are a multiple of 16
+            // steps); the next group is always loaded one group ahead, past
+            // the run's end into the next run or the tail, and never used there
+            const int T = __builtin_amdgcn_readfirstlane((s1 - s0) / 64);
+            int p = s0 + lane;
+            int4 wa = blk[p], wb;
+            for (int t = 0; t < T; t += 2) {
+                wb = blk[p + 64];
+                asm volatile("" ::: "memory");  // keep the prefetch ahead of the LDS reads
+                comp(wa);
+                wa = blk[p + 128];
+                asm volatile("" ::: "memory");
+                comp(wb);
+                p += 128;
+            }
+        }
+    }
+    if (slab < nslab) {
+        const int row = perm[slab * pfr::kSellRows + r];
+        const int cn = n0 + q * 4;
+        if (row >= 0 && cn < N) {
+            float* yr = Y + (int64_t)row * ldy_r;
+            if (yvec && cn + 3 < N) {
+                *reinterpret_cast<float4*>(yr + cn) = make_float4(a0, a1, a2, a3);
+            } else {
+                const float a[4] = {a0, a1, a2, a3};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (cn + i < N) {
+                        const int64_t f = (int64_t)row * ldy_r + (int64_t)(cn + i) * ldy_c;
+                        Y[f] = bias_add(a[i], f, bias, c_size, beta);
+                    }
+            }
+        }
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int next_pow2(int n) {
@@ -214,6 +343,52 @@ int next_pow2(int n) {
 }
 
 
+// Column-slice kernel launch; false when the weight has no sliced-ELL copy.
+template <bool FAST, bool XVEC, int W>
+void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta) {
+    auto kern = k_spmm_sell<FAST, XVEC, W>;
+    const size_t lds = (size_t)(Wt->sell_kc + 1) * 64;
+    // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
+    static uint64_t allowed = 0;  // bit d: done on device d (< 64)
+    const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
+    if (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit)) {
+        PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        if (bit && lds == (size_t)(pfr::kSellMaxKC + 1) * 64) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
+    }
+    dim3 grid((unsigned)((Wt->sell_nslab + W - 1) / W), (unsigned)((N + pfr::kSellCols - 1) / pfr::kSellCols));
+    hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, ctx->stream, N, (int)Wt->K, Wt->sell_kc, Wt->sell_nch,
+                       Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, Wt->sell_blk, X, ldx, Y, ldy_r, ldy_c, yvec,
+                       bias, c_size, beta);
+}
+
+template <bool FAST, bool XVEC>
+void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta) {
+    // 16 waves per workgroup when that still gives a workgroup per CU,
+    // otherwise smaller workgroups to spread the slabs over more CUs
+    const int64_t slices = (N + pfr::kSellCols - 1) / pfr::kSellCols;
+    const int64_t wg16 = (Wt->sell_nslab + 15) / 16 * slices;
+    if (wg16 >= ctx->num_cu)
+        launch_sell_w<FAST, XVEC, 16>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+    else
+        launch_sell_w<FAST, XVEC, 4>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+}
+
+void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
+                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, bool fast) {
+    const bool xvec = (ldx % 4 == 0) && (N % 4 == 0) && aligned16(X);
+    const int yvec = (ldy_c == 1 && ldy_r % 4 == 0 && aligned16(Y) && bias == nullptr) ? 1 : 0;
+    if (fast) {
+        if (xvec) launch_sell_x<true, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        else launch_sell_x<true, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+    } else {
+        if (xvec) launch_sell_x<false, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        else launch_sell_x<false, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+    }
+}
+
 // Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
 void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
                  int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
@@ -222,7 +397,9 @@ void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int6
     if (M == 0 || N == 0) return;
     const float* val = static_cast<const float*>(W->val);
     hipStream_t s = ctx->stream;
-    if (N == 1) {
+    if (N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535) {
+        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast);
+    } else if (N == 1) {
         hipLaunchKernelGGL(k_spmv_wg, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
                            W->spmv_blocks, W->rowptr, W->col, val, X, ldx, Y, ldy_r, bias, c_size,
                            beta);

@@ -209,3 +209,63 @@ def test_device_pointer_variant(ctx, cfg_weight):
     ctx.synchronize()
     Y = dY[:, :256].cpu().numpy()
     assert bits_equal(Y, O.orc_csr_spmm(4096, 4096, ip, ix, v, X))
+
+
+def shuffle_within(ix, ip, block):
+    """Permute each row's columns inside every `block`-wide K range, keeping
+    the ranges in order (storage order then differs from column order)."""
+    rng = np.random.default_rng(5)
+    out = ix.copy()
+    for r in range(len(ip) - 1):
+        seg = out[ip[r]:ip[r + 1]]
+        for b in np.unique(seg // block):
+            m = np.nonzero(seg // block == b)[0]
+            seg[m] = seg[rng.permutation(m)]
+    return out
+
+
+def test_column_slice_layout_cases(ctx):
+    """The column-slice kernel (N >= 16): several K chunks, storage order
+    unsorted inside chunks, a weight that must fall back to the row kernels,
+    ragged column counts, unaligned leading dimensions, empty slabs, and
+    infinities in X."""
+    import torch
+
+    M, K = 16 * 21 + 3, 5000
+    ip, ix, v = workloads.csr_uniform(M, K, 0.08, 0.05, seed=21)
+    cnt = np.diff(ip)
+    cnt[16 * 4:16 * 6] = 0  # two slabs' worth of empty rows
+    ip = np.zeros(M + 1, np.int64)
+    np.cumsum(cnt, out=ip[1:])
+    rng = np.random.default_rng(8)
+    ix = np.concatenate([np.sort(rng.choice(K, c, replace=False)) for c in cnt]).astype(np.int64)
+    v = (rng.standard_normal(len(ix)) * 0.05).astype(np.float32)
+    cases = {"sorted": ix, "shuffled in chunks": shuffle_within(ix, ip, 2048),
+             "shuffled across chunks": shuffle_within(ix, ip, K)}
+    for name, cols in cases.items():
+        W = ctx.csr_upload(M, K, ip, cols, v)
+        for N in (16, 48, 50):
+            say(f"column slice: {name} N={N}")
+            X = rng.standard_normal((K, N)).astype(np.float32)
+            assert bits_equal(W.spmm(X), O.orc_csr_spmm(M, K, ip, cols, v, X)), (name, N)
+    # unaligned leading dimensions through the device-pointer entry
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    N = 37
+    X = rng.standard_normal((K, N + 3)).astype(np.float32)
+    dX = torch.from_numpy(X).cuda()
+    dY = torch.zeros((M, N + 5), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    say("column slice: ldx=40 ldy=42")
+    W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), ldx=N + 3, ldy=N + 5)
+    ctx.synchronize()
+    R = O.orc_csr_spmm(M, K, ip, ix, v, np.ascontiguousarray(X[:, :N]))
+    assert bits_equal(dY[:, :N].cpu().numpy(), R)
+    assert not dY[:, N:].cpu().numpy().any()  # columns past N untouched
+    # infinities: products inf and inf - inf = nan exactly where the oracle has them
+    X = rng.standard_normal((K, 32)).astype(np.float32)
+    X[rng.integers(0, K, 40), rng.integers(0, 32, 40)] = np.inf
+    say("column slice: infinities")
+    Y, R = W.spmm(X), O.orc_csr_spmm(M, K, ip, ix, v, X)
+    assert np.array_equal(np.isnan(Y), np.isnan(R))
+    fin = ~np.isnan(R)
+    assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
