@@ -25,11 +25,17 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (packed FMA)
+STRICT_VALU_CEILING_TFLOPS = 39.3  # one non-packed fp32 op per lane per clock, 256 CUs x 64 lanes x 2.4 GHz
 INT8_DENSE_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (the 2:4 instruction doubles K per issue)
 M = K = 4096
 DENSITY = 0.1
 N_MAIN = 256
 N_SETS = 16
+# HBM traffic of the main kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+# runs recorded in this summary (the line "traffic_bytes_per_launch: <int>"
+# for the kernel named on the line "kernel: <name>").
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "spmm_csr_sell_4096x4096x256_strict.md")
+MAIN_KERNEL = "k_spmm_sell"
 
 
 def csr_bytes(nnz, M, K, N):
@@ -60,6 +66,62 @@ def time_gpu(sets, N, steps, warmup, mode):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def time_host_entry(ctx, ip, ix, v, Xh, calls=20):
+    """The host-buffer entry point (pfr_spmm_csr: X copied in, Y copied out,
+    synchronised) on the same workload: the PCIe-inclusive rate a synchronous
+    OpFunc sees.  Reported beside `value`, never as it."""
+    import numpy as np
+
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    X = np.ascontiguousarray(Xh)
+    W.spmm(X)
+    ts = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        W.spmm(X)
+        ts.append(time.perf_counter() - t0)
+    W.free()
+    ms = float(np.median(ts)) * 1e3
+    res = {"ms_per_call": round(ms, 4),
+           "gflops": round(2.0 * len(v) * X.shape[1] / (ms * 1e-3) / 1e9, 1),
+           "note": "median of %d calls of the host entry point (X 4 MiB in, Y 4 MiB out over PCIe)" % calls}
+    log(f"host entry N=256: {res}")
+    return res
+
+
+def recorded_traffic():
+    """Bytes per launch of the main kernel measured by the profiler runs
+    described in TRAFFIC_FILE, or None when that record is absent."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    kern = val = None
+    for line in text.splitlines():
+        line = line.strip().strip("`")
+        if line.startswith("kernel:"):
+            kern = line.split(":", 1)[1].strip()
+        elif line.startswith("traffic_bytes_per_launch:"):
+            val = int(line.split(":", 1)[1].strip())
+    return val if kern == MAIN_KERNEL else None
+
+
+def calibrate_copy(mib):
+    """A plain streaming kernel of known size for counter calibration:
+    y = -x over `mib` MiB of float32 (reads and writes mib MiB each), 10 times."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "torch.neg float32", "bytes_read": n * 4, "bytes_written": n * 4,
+                      "launches": 10}), flush=True)
 
 
 def bench_sp24(ctx, args):
@@ -161,11 +223,18 @@ def main():
     ap.add_argument("--mode", default="strict", choices=["strict", "fast"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-main", action="store_true", help="time only the N=256 SpMM (profiler runs)")
+    ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
+                    help="run a copy-like kernel of MIB MiB for counter calibration and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs the path on "
               "a single MI355X and reports that GPU's throughput.", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     import numpy as np
     import torch
@@ -183,7 +252,7 @@ def main():
 
     extra = {}
     results = {}
-    for N in (N_MAIN, 64, 1):
+    for N in ((N_MAIN,) if args.only_main else (N_MAIN, 64, 1)):
         sets = []
         for s in range(N_SETS):
             W = ctx.csr_upload(M, K, ip, ix, v)
@@ -211,7 +280,9 @@ def main():
         del sets
         torch.cuda.empty_cache()
 
-    extra["sp24_i8"] = bench_sp24(ctx, args)
+    if not args.only_main:
+        extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)
+        extra["sp24_i8"] = bench_sp24(ctx, args)
 
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)
@@ -244,13 +315,16 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(),
         },
         "compute": {
             "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
             "fp32_valu_peak_tflops": FP32_VALU_PEAK_TFLOPS,
+            "strict_valu_ceiling_tflops": STRICT_VALU_CEILING_TFLOPS,
+            "frac_of_strict_ceiling": round(flops / (ms * 1e-3) / 1e12 / STRICT_VALU_CEILING_TFLOPS, 4),
             "note": "strict mode issues a separate v_mul_f32 and v_add_f32 per term (no FMA, no packed "
-                    "FP32): its VALU ceiling is 1/4 of the packed-FMA peak",
+                    "FP32), so each useful flop is one non-packed VALU lane-op: 256 CUs x 64 lanes x "
+                    "2.4 GHz = 39.3 TFLOP/s, 1/4 of the packed-FMA peak",
         },
         "parity": parity,
         "cpu_baseline": cpu,

@@ -7,7 +7,7 @@
  *
  * Every function restates one reference function line-for-line in its
  * numerics (loop order, rounding points, casts); the reference file:line is
- * given on each declaration.  Compiled with -std=c11 -O2 -ffp-contract=off
+ * given on each declaration.  Compiled with -std=c11 -O3 -ffp-contract=off
  * and no -march, like the reference's Release build (GCC, ISO mode, x86-64
  * baseline: SSE arithmetic, no FMA).
  *
