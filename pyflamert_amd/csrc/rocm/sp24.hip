@@ -40,8 +40,9 @@ struct pfr_sp24 {
 
 namespace {
 
-constexpr int kTileM = 128;  // rows per workgroup (4 waves x 32)
-constexpr int kTileN = 64;   // columns per workgroup
+constexpr int kTileM = 128;  // bf16 kernel: rows per workgroup (4 waves x 32)
+constexpr int kTileN = 64;   // bf16 kernel: columns per workgroup
+constexpr int kPadM = 256;   // packed weights pad M to this (the int8 tile height)
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -100,69 +101,247 @@ __device__ __forceinline__ int32_t f2i_trunc_x86(float r) {
     return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
 }
 
-// One wave computes 32 rows x 64 columns (2 x 4 tiles of 16x16); four waves
-// stack along M.  Operands come straight from global memory (A packed, B from
-// the transposed activation).
-template <int OUT>
-__global__ __launch_bounds__(256) void k_sp24_i8(
-    int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
-    const int8_t* __restrict__ XT, int64_t Kp, int M, int N, const float* __restrict__ sab,
-    float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy) {
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int mt0 = (int)blockIdx.x * (kTileM / 16) + 2 * w;
-    const int nt0 = (int)blockIdx.y * (kTileN / 16);
-    const int kb = l >> 4, c = l & 15;
-    v4i acc[2][4];
+// XT[n][k] (Np x Kp) = X[k][n] for int8, zero outside K x N.  A wave owns a
+// 64 x 64 block: lane (rg = l / 4, cg = l % 4) loads rows 4rg .. 4rg+3,
+// columns 16cg .. 16cg+15 (each load instruction covers 16 rows x 64
+// contiguous bytes), transposes each 4 x 4 byte square with v_perm_b32 and
+// stores dwords (each store instruction covers 4 XT rows x 64 bytes).
+__global__ __launch_bounds__(256) void k_transpose_i8(const int8_t* __restrict__ X, int64_t K, int64_t N,
+                                                      int64_t ldx, int vec, int8_t* __restrict__ XT,
+                                                      int64_t Kp, int64_t Np) {
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int rg = l >> 2, cg = l & 3;
+    const int64_t k = (int64_t)blockIdx.x * 64 + 4 * rg;
+    const int64_t n0 = ((int64_t)blockIdx.y * 4 + w) * 64 + 16 * cg;
+    if (n0 >= Np) return;
+    uint32_t r[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int row = 0; row < 4; ++row) {
+        const int64_t kk = k + row;
+        if (vec && kk < K && n0 + 16 <= N) {
+            const v4i v = *reinterpret_cast<const v4i*>(X + kk * ldx + n0);
+            r[row][0] = (uint32_t)v.x; r[row][1] = (uint32_t)v.y; r[row][2] = (uint32_t)v.z; r[row][3] = (uint32_t)v.w;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-    const v4i* a0p = A + ((int64_t)mt0 * nkt) * 64 + l;
-    const v4i* a1p = A + ((int64_t)(mt0 + 1) * nkt) * 64 + l;
-    const uint32_t* i0p = I + ((int64_t)mt0 * nkt) * 64 + l;
-    const uint32_t* i1p = I + ((int64_t)(mt0 + 1) * nkt) * 64 + l;
-    const int8_t* xb[4];
+            for (int g = 0; g < 4; ++g) {
+                uint32_t d = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xb[j] = XT + (int64_t)((nt0 + j) * 16 + c) * Kp + 16 * kb;
-    for (int kt = 0; kt < nkt; ++kt) {
-        const v4i a0 = a0p[(int64_t)kt * 64], a1 = a1p[(int64_t)kt * 64];
-        const int ix0 = (int)i0p[(int64_t)kt * 64], ix1 = (int)i1p[(int64_t)kt * 64];
-        v8i b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const v4i lo = *reinterpret_cast<const v4i*>(xb[j] + (int64_t)kt * 128);
-            const v4i hi = *reinterpret_cast<const v4i*>(xb[j] + (int64_t)kt * 128 + 64);
-            b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[0][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a0, b[j], acc[0][j], ix0, 0, 0);
-            acc[1][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a1, b[j], acc[1][j], ix1, 0, 0);
+                for (int b = 0; b < 4; ++b) {
+                    const int64_t n = n0 + 4 * g + b;
+                    if (kk < K && n < N) d |= (uint32_t)(uint8_t)X[kk * ldx + n] << (8 * b);
+                }
+                r[row][g] = d;
+            }
         }
     }
 #pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        // byte j of r[row][g] is X[k + row][n0 + 4g + j]; o[j] gathers it over row
+        const uint32_t lo01 = __builtin_amdgcn_perm(r[1][g], r[0][g], 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(r[1][g], r[0][g], 0x07030602u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(r[3][g], r[2][g], 0x05010400u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(r[3][g], r[2][g], 0x07030602u);
+        const uint32_t o[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                               __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                               __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                               __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint32_t*>(XT + (n0 + 4 * g + j) * Kp + k) = o[j];
+    }
+}
+
+// int8 2:4 GEMM, 256 x 128 outputs per workgroup of eight waves in a 4 x 2
+// grid, each owning 64 rows x 64 columns (4 x 4 tiles of 16 x 16, two waves
+// per SIMD).  A k step is 128 wide; its operands live in one of four LDS
+// stages:
+//   A values  [16 row blocks][64 lanes][16 B]   (the packed register order)
+//   A indices [16 row blocks][64 lanes] u32
+//   B         [128 columns][128 B]: the k bytes of one XT row, its 16-byte
+//             chunk c stored at position c ^ ((column >> 1) & 7), so the 16
+//             lanes of a ds_read_b128 group (16 consecutive columns, one
+//             chunk) hit 16 distinct 4-bank groups.
+// Stages are filled by direct-to-LDS loads (global_load_lds_dword[x4]: each
+// wave instruction writes its lanes' data contiguously) four steps ahead of
+// the MFMAs; each wave reads the next step's fragments into a second
+// register set while the MFMAs of the current step run; one barrier per
+// step.  nkt is a multiple of 4 (packed K is padded to 512), so the loop
+// unrolls over the four stages with each stage's address static, which lets
+// the compiler wait for only the oldest loads (vmcnt) instead of all of them.
+constexpr int kI8TileM = 256, kI8TileN = 128;
+constexpr int kLdsA = 16 * 64 * 16, kLdsI = 16 * 64 * 4, kLdsB = 128 * 128;
+constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
+
+#define PFR_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+template <int OUT>
+__global__ __launch_bounds__(512) void k_sp24_i8(
+    int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
+    const int8_t* __restrict__ XT, int64_t Kp, int M, int N, const float* __restrict__ ws, float xs,
+    float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn) {
+    __shared__ __attribute__((aligned(1024))) char st0[kStage];
+    __shared__ __attribute__((aligned(1024))) char st1[kStage];
+    __shared__ __attribute__((aligned(1024))) char st2[kStage];
+    __shared__ __attribute__((aligned(1024))) char st3[kStage];
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int wm = w >> 1, wn = w & 1;
+    const int kb = l >> 4, c = l & 15;
+    int mt, nt;
+    {
+        const int G = (int)gridDim.x, L = (int)blockIdx.x, xcd = L & 7, slot = L >> 3;
+        const int q = G >> 3, rem = G & 7;
+        const int T = xcd * q + min(xcd, rem) + slot;
+        mt = T / ntn;
+        nt = T % ntn;
+    }
+    const int64_t mb0 = (int64_t)mt * 16;
+    const int64_t n0 = (int64_t)nt * kI8TileN;
+    // every wave issues six direct-to-LDS loads per k step: A row blocks w and
+    // w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), XT rows
+    // 16w .. 16w + 15 (two 1 KiB runs of 8 rows)
+    const v4i* asrc = A + ((mb0 + w) * nkt) * 64 + l;
+    const int64_t a_rb8 = (int64_t)8 * nkt * 64;
+    const uint32_t* isrc = I + ((mb0 + 2 * w) * nkt) * 64 + l;
+    const int64_t i_rb1 = (int64_t)nkt * 64;
+    const v4i* bsrc[2];
+#pragma unroll
     for (int i = 0; i < 2; ++i) {
+        const int n = 16 * w + 8 * i + (l >> 3);
+        const int chunk = (l & 7) ^ ((n >> 1) & 7);
+        bsrc[i] = reinterpret_cast<const v4i*>(XT + (n0 + n) * Kp + 16 * chunk);
+    }
+    auto issue = [&](char* st, int s) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(asrc + i * a_rb8 + (int64_t)s * 64, PFR_LDS(st + (w + 8 * i) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(isrc + i * i_rb1 + (int64_t)s * 64, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * 8, PFR_LDS(st + kLdsA + kLdsI + (16 * w + 8 * i) * 128), 16, 0, 0);
+    };
+    int boff_lo[4], boff_hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = wn * 64 + 16 * j + c, sw = (n >> 1) & 7;
+        boff_lo[j] = kLdsA + kLdsI + n * 128 + 16 * (kb ^ sw);
+        boff_hi[j] = kLdsA + kLdsI + n * 128 + 16 * ((4 + kb) ^ sw);
+    }
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    struct Frag {
+        v4i a[4];
+        int ix[4];
+        v8i b[4];
+    };
+    auto fetch = [&](Frag& f, const char* st) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int n = (nt0 + j) * 16 + c;
+            const v4i lo = *reinterpret_cast<const v4i*>(st + boff_lo[j]);
+            const v4i hi = *reinterpret_cast<const v4i*>(st + boff_hi[j]);
+            f.b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f.a[i] = *reinterpret_cast<const v4i*>(st + ((wm * 4 + i) * 64 + l) * 16);
+            f.ix[i] = *reinterpret_cast<const int*>(st + kLdsA + ((wm * 4 + i) * 64 + l) * 4);
+        }
+    };
+    auto mma = [&](const Frag& f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(f.a[i], f.b[j], acc[i][j], f.ix[i], 0, 0);
+    };
+    // Step s: fragments of stage s are in registers (cur).  Wait for stage
+    // s+1's loads (vmcnt(12): stages s+2 and s+3 may still be in flight),
+    // barrier (every wave's stage s+1 loads have landed, and every wave has
+    // read stage s's fragments, so its LDS buffer is free), start the loads
+    // of stage s+4 into that buffer, read stage s+1's fragments into `nxt`
+    // while the MFMAs run on `cur`.
+    // vmcnt(12) and lgkmcnt(0): this wave's fragment reads of the previous
+    // step have completed before the barrier lets other waves refill a stage
+    constexpr int kWait12 = (12 & 0xF) | (7 << 4) | (0 << 8);
+    Frag fa, fb;
+    auto step = [&](Frag& cur, Frag& nxt, char* st_cur, char* st_next, int s) {
+        __builtin_amdgcn_s_waitcnt(kWait12);
+        __builtin_amdgcn_s_barrier();
+        issue(st_cur, min(s + 4, nkt - 1));  // past the end: reloads the last step, never read
+        fetch(nxt, st_next);
+        mma(cur);
+    };
+    issue(st0, 0);
+    issue(st1, min(1, nkt - 1));
+    issue(st2, min(2, nkt - 1));
+    issue(st3, min(3, nkt - 1));
+    __builtin_amdgcn_s_waitcnt((18 & 0xF) | ((18 >> 4) << 14) | (7 << 4) | (0xF << 8));  // stage 0 landed
+    __builtin_amdgcn_s_barrier();
+    fetch(fa, st0);
+    for (int s = 0; s < nkt; s += 4) {
+        step(fa, fb, st0, st1, s);
+        step(fb, fa, st1, st2, s + 1);
+        step(fa, fb, st2, st3, s + 2);
+        step(fb, fa, st3, st0, s + 3);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the trailing reloads have landed
+    __builtin_amdgcn_s_barrier();
+    if constexpr (OUT == PFR_SP24_OUT_I8) {
+        // requantise into an LDS tile [256][128] (stage 0), then store 16-byte row pieces
+        char* tile = st0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = (mt0 + i) * 16 + 4 * kb + r;
-                if (m >= M || n >= N) continue;
-                const int32_t v = acc[i][j][r];
-                const int64_t o = (int64_t)m * ldy + n;
-                if constexpr (OUT == PFR_SP24_OUT_I32) {
-                    static_cast<int32_t*>(Y)[o] = v;
-                } else {
-                    const float f = (float)v * sab[m];
-                    if constexpr (OUT == PFR_SP24_OUT_F32) {
-                        static_cast<float*>(Y)[o] = f;
-                    } else {
-                        const float prod = f * inv_out;
-                        int32_t q = (int32_t)((uint32_t)f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
-                        q = q < -128 ? -128 : (q > 127 ? 127 : q);
-                        static_cast<int8_t*>(Y)[o] = (int8_t)q;
-                    }
+                const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
+                const int m = (int)(mb0 * 16) + ml;
+                const float sab = m < M ? ws[m] * xs : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float f = (float)acc[i][j][r] * sab;
+                    const float prod = f * inv_out;
+                    int32_t q = (int32_t)((uint32_t)f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
+                    q = q < -128 ? -128 : (q > 127 ? 127 : q);
+                    tile[ml * 128 + wn * 64 + 16 * j + c] = (char)q;
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q16 = t + 512 * i, ml = q16 >> 3, cc = q16 & 7;
+            const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
+            if (m >= M) continue;
+            int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
+            const char* src = tile + ml * 128 + 16 * cc;
+            if (yvec && n + 16 <= N) {
+                *reinterpret_cast<v4i*>(yr + n) = *reinterpret_cast<const v4i*>(src);
+            } else {
+                for (int b = 0; b < 16 && n + b < N; ++b) yr[n + b] = src[b];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = (int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r;
+                if (m >= M) continue;
+                float sab = 1.0f;
+                if constexpr (OUT == PFR_SP24_OUT_F32) sab = ws[m] * xs;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t n = n0 + wn * 64 + 16 * j + c;
+                    if (n >= N) continue;
+                    const int32_t v = acc[i][j][r];
+                    const int64_t o = (int64_t)m * ldy + n;
+                    if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
+                    else static_cast<float*>(Y)[o] = (float)v * sab;
                 }
             }
         }
@@ -229,17 +408,10 @@ __global__ __launch_bounds__(256) void k_sp24_bf16(
         }
 }
 
-// s_ab[m] = w_scale[m] * x_scale, one rounding as on the host (quant_ops.cpp:435).
-__global__ __launch_bounds__(256) void k_scale_rows(const float* __restrict__ ws, float xs, int64_t M,
-                                                    float* __restrict__ out) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m < M) out[m] = ws[m] * xs;
-}
-
 // ---- host -----------------------------------------------------------------
 
 pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
-    const int64_t Mp = round_up(M, kTileM), Kp = round_up(K, 128), nkt = Kp / 128;
+    const int64_t Mp = round_up(M, kPadM), Kp = round_up(K, 512), nkt = Kp / 128;
     std::vector<int8_t> a((size_t)(Mp / 16 * nkt * 64 * 16), 0);
     std::vector<uint32_t> ix((size_t)(Mp / 16 * nkt * 64), 0);
     auto wat = [&](int64_t r, int64_t k) -> int8_t { return (r < M && k < K) ? W[r * K + k] : 0; };
@@ -293,7 +465,7 @@ pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
 bool bf16_nz(uint16_t b) { return (b & 0x7FFF) != 0; }
 
 pfr_sp24* pack_bf16(pfr_ctx* ctx, int64_t M, int64_t K, const uint16_t* W) {
-    const int64_t Mp = round_up(M, kTileM), Kp = round_up(K, 128), nkt = Kp / 64, nkp = nkt / 2;
+    const int64_t Mp = round_up(M, kPadM), Kp = round_up(K, 128), nkt = Kp / 64, nkp = nkt / 2;
     std::vector<uint16_t> a((size_t)(Mp / 16 * nkt * 64 * 8), 0);
     std::vector<uint32_t> ix((size_t)(Mp / 16 * nkp * 64), 0);
     auto wat = [&](int64_t r, int64_t k) -> uint16_t { return (r < M && k < K) ? W[r * K + k] : 0; };
@@ -366,37 +538,36 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     if (W->M == 0 || N == 0) return;
     pfr::require(X != nullptr && Y != nullptr, "null X/Y");
     float inv_out = 1.0f;
-    const float* sab = nullptr;
-    if (out_kind != PFR_SP24_OUT_I32) {
+    if (out_kind != PFR_SP24_OUT_I32)
         pfr::require(x_scale > 0.0f && std::isfinite(x_scale), "x_scale must be positive and finite");
-        // s_ab[m] = a_scale * b_scale with a = the weight (quant_ops.cpp:435).
-        float* d = static_cast<float*>(ctx->scratch[1].ensure(sizeof(float) * (size_t)W->M));
-        hipLaunchKernelGGL(k_scale_rows, dim3((unsigned)((W->M + 255) / 256)), dim3(256), 0, ctx->stream,
-                           W->w_scale, x_scale, W->M, d);
-        PFR_HIP(hipGetLastError());
-        sab = d;
-    }
     if (out_kind == PFR_SP24_OUT_I8) {
         pfr::require(out_scale > 0.0f && std::isfinite(out_scale), "output scale must be positive and finite");
         inv_out = 1.0f / out_scale;  // quant_ops.cpp:41
     }
-    const int64_t Np = round_up(N, kTileN);
-    const int8_t* xt = stage_xt(ctx, X, W->K, N, ldx, W->Kp, Np);
-    dim3 grid((unsigned)(W->Mp / kTileM), (unsigned)(Np / kTileN));
-    const int nkt = (int)(W->Kp / 128);
+    // XT: Np x Kp, zero padded (the kernel reads whole 128 x 128 tiles)
+    const int64_t Np = round_up(N, kI8TileN), Kp = W->Kp;
+    int8_t* xt = static_cast<int8_t*>(ctx->scratch[3].ensure((size_t)(Np * Kp)));
+    const int vec = (ldx % 16 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(k_transpose_i8, dim3((unsigned)(Kp / 64), (unsigned)((Np + 255) / 256)), dim3(256), 0,
+                       ctx->stream, X, W->K, N, ldx, vec, xt, Kp, Np);
+    PFR_HIP(hipGetLastError());
+    const int ntn = (int)(Np / kI8TileN);
+    dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
+    const int nkt = (int)(Kp / 128);
+    const int yvec = (ldy % 16 == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) ? 1 : 0;
     const v4i* A = static_cast<const v4i*>(W->a);
     switch (out_kind) {
         case PFR_SP24_OUT_I32:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I32>, grid, dim3(256), 0, ctx->stream, nkt, A, W->idx, xt,
-                               W->Kp, (int)W->M, (int)N, sab, inv_out, out_zp, Y, ldy);
+            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I32>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
+                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
             break;
         case PFR_SP24_OUT_F32:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_F32>, grid, dim3(256), 0, ctx->stream, nkt, A, W->idx, xt,
-                               W->Kp, (int)W->M, (int)N, sab, inv_out, out_zp, Y, ldy);
+            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_F32>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
+                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
             break;
         default:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I8>, grid, dim3(256), 0, ctx->stream, nkt, A, W->idx, xt,
-                               W->Kp, (int)W->M, (int)N, sab, inv_out, out_zp, Y, ldy);
+            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I8>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
+                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
     }
     PFR_HIP(hipGetLastError());
 }
