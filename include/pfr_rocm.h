@@ -100,7 +100,10 @@ int pfr_csr_free(pfr_csr* w);
 /* Y[M,N] = W[M,K] . X[K,N] (row-major, host).  N == 1 is the SpMV of
  * sparse_matvec (sparse_tensor.cpp:521-554).  Replaces sparse_matmul
  * (sparse_tensor.cpp:473-519) and MatMul with a pruned first operand
- * (math.cpp:268-374). */
+ * (math.cpp:268-374).  For int8 values each term uses the dequantised
+ * weight RN((float)q * row_scales[m]) (dequantize_tensor with zero point 0,
+ * quant_ops.cpp:182-196), so the result equals dequantize-then-sparse_matmul
+ * bit for bit in strict mode. */
 int pfr_spmm_csr(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N,
                  float* Y, int mode);
 /* Device variant.  X rows are ldx floats apart, Y rows ldy floats apart

@@ -29,6 +29,18 @@ __device__ __forceinline__ float madd(float acc, float w, float x) {
     }
 }
 
+// Weight of nonzero j of `row`: the float32 value, or for int8 values the
+// dequantised RN((float)q * scale[row]) of dequantize_tensor with zero point
+// 0 (quant_ops.cpp:182-196: ((float)q - 0.0f) * scale rounds once).
+template <bool I8>
+__device__ __forceinline__ float wval(const void* __restrict__ val, const float* __restrict__ rs, int j, int row) {
+    if constexpr (I8) {
+        return (float)static_cast<const int8_t*>(val)[j] * rs[row];
+    } else {
+        return static_cast<const float*>(val)[j];
+    }
+}
+
 // Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size].
 __device__ __forceinline__ float bias_add(float v, int64_t f, const float* __restrict__ bias,
                                           int64_t c_size, float beta) {
@@ -39,10 +51,10 @@ __device__ __forceinline__ float bias_add(float v, int64_t f, const float* __res
 
 // One wave per CSR row, lanes across the N columns (4 per lane when VEC).
 // Output element (row, c) goes to Y[row * ldy_r + c * ldy_c].
-template <bool FAST, bool VEC>
+template <bool FAST, bool VEC, bool I8>
 __global__ __launch_bounds__(256) void k_spmm_rows(
     int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
-    const float* __restrict__ val, const float* __restrict__ X, int64_t ldx,
+    const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
     int64_t c_size, float beta) {
     const int lane = threadIdx.x & 63;
@@ -61,7 +73,7 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     x[i] = *reinterpret_cast<const float4*>(xc + (int64_t)col[j + i] * ldx);
-                    w[i] = val[j + i];
+                    w[i] = wval<I8>(val, rs, j + i, row);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -72,7 +84,7 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
                 }
             }
             for (; j < end; ++j) {
-                const float w = val[j];
+                const float w = wval<I8>(val, rs, j, row);
                 const float4 x = *reinterpret_cast<const float4*>(xc + (int64_t)col[j] * ldx);
                 a0 = madd<FAST>(a0, w, x.x);
                 a1 = madd<FAST>(a1, w, x.y);
@@ -91,7 +103,7 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
         for (int c = lane; c < N; c += 64) {
             float a = 0.0f;
 #pragma unroll 4
-            for (int j = beg; j < end; ++j) a = madd<FAST>(a, val[j], X[(int64_t)col[j] * ldx + c]);
+            for (int j = beg; j < end; ++j) a = madd<FAST>(a, wval<I8>(val, rs, j, row), X[(int64_t)col[j] * ldx + c]);
             const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
             Y[f] = bias_add(a, f, bias, c_size, beta);
         }
@@ -99,10 +111,10 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
 }
 
 // NP lanes per row (NP = next power of two >= N, N < 64), 64 / NP rows per wave.
-template <int NP, bool FAST>
+template <int NP, bool FAST, bool I8>
 __global__ __launch_bounds__(256) void k_spmm_small(
     int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
-    const float* __restrict__ val, const float* __restrict__ X, int64_t ldx,
+    const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
     int64_t c_size, float beta) {
     constexpr int RPW = 64 / NP;
@@ -114,22 +126,25 @@ __global__ __launch_bounds__(256) void k_spmm_small(
     const int end = rowptr[row + 1];
     float a = 0.0f;
 #pragma unroll 4
-    for (int j = beg; j < end; ++j) a = madd<FAST>(a, val[j], X[(int64_t)col[j] * ldx + c]);
+    for (int j = beg; j < end; ++j) a = madd<FAST>(a, wval<I8>(val, rs, j, row), X[(int64_t)col[j] * ldx + c]);
     const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
     Y[f] = bias_add(a, f, bias, c_size, beta);
 }
 
 // SpMV.  One workgroup per row block (<= 64 rows, <= kSpmvCap nnz unless a
-// single longer row).  All kSpmvThreads threads form the products
-// RN(w * x[col]) over the block's contiguous nnz range with all loads in
-// flight at once, staging them in LDS; then lane g of wave 0 folds the
-// products of row r0 + g in storage order.  Longer blocks go in chunks.
+// single longer row).  All kSpmvThreads threads gather over the block's
+// contiguous nnz range with all loads in flight at once, staging in LDS
+// either the products RN(w * x[col]) (float values) or x[col] and the int8
+// value (int8 values: the product needs the row's scale); then lane g of
+// wave 0 folds row r0 + g in storage order.  Longer blocks go in chunks.
+template <bool I8>
 __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     const int32_t* __restrict__ blocks, const int32_t* __restrict__ rowptr,
-    const int32_t* __restrict__ col, const float* __restrict__ val, const float* __restrict__ x,
-    int64_t ldx, float* __restrict__ y, int64_t ldy_r, const float* __restrict__ bias,
-    int64_t c_size, float beta) {
+    const int32_t* __restrict__ col, const void* __restrict__ val, const float* __restrict__ rs,
+    const float* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy_r,
+    const float* __restrict__ bias, int64_t c_size, float beta) {
     __shared__ float P[kSpmvCap];
+    __shared__ int8_t Q[I8 ? kSpmvCap : 1];
     constexpr int kPer = kSpmvCap / kSpmvThreads;
     const int tid = threadIdx.x;
     const int r0 = blocks[blockIdx.x];
@@ -140,23 +155,31 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     const bool folder = tid < 64 && my_row < r1;
     const int my_beg = folder ? rowptr[my_row] : 0;
     const int my_end = folder ? rowptr[my_row + 1] : 0;
+    const float my_scale = (I8 && folder) ? rs[my_row] : 1.0f;
     float acc = 0.0f;
     for (int base = nb; base < ne; base += kSpmvCap) {
         const int cend = min(base + kSpmvCap, ne);
         int cl[kPer];
         float w[kPer];
+        int8_t q[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int j = base + tid + i * kSpmvThreads;
             cl[i] = j < cend ? col[j] : 0;
-            w[i] = j < cend ? val[j] : 0.0f;
+            if constexpr (I8) q[i] = j < cend ? static_cast<const int8_t*>(val)[j] : 0;
+            else w[i] = j < cend ? static_cast<const float*>(val)[j] : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int j = base + tid + i * kSpmvThreads;
             if (j < cend) {
                 const float xv = x[(int64_t)cl[i] * ldx];
-                P[j - base] = w[i] * xv;
+                if constexpr (I8) {
+                    P[j - base] = xv;
+                    Q[j - base] = q[i];
+                } else {
+                    P[j - base] = w[i] * xv;
+                }
             }
         }
         __syncthreads();
@@ -166,11 +189,26 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
             for (; p + 8 <= e; p += 8) {
                 float t[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) t[i] = P[p + i];
+                for (int i = 0; i < 8; ++i) {
+                    if constexpr (I8) {
+                        const float wv = (float)Q[p + i] * my_scale;
+                        t[i] = wv * P[p + i];
+                    } else {
+                        t[i] = P[p + i];
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) acc = acc + t[i];
             }
-            for (; p < e; ++p) acc = acc + P[p];
+            for (; p < e; ++p) {
+                if constexpr (I8) {
+                    const float wv = (float)Q[p] * my_scale;
+                    const float t = wv * P[p];
+                    acc = acc + t;
+                } else {
+                    acc = acc + P[p];
+                }
+            }
         }
         __syncthreads();
     }
@@ -389,32 +427,25 @@ void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t
     }
 }
 
-// Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
-void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
-                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
-                 bool fast) {
+// Row, small-N and vector kernels for one value type.
+template <bool FAST, bool I8>
+void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
+                        int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta) {
     const int M = (int)W->M;
-    if (M == 0 || N == 0) return;
-    const float* val = static_cast<const float*>(W->val);
     hipStream_t s = ctx->stream;
-    if (N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535) {
-        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast);
-    } else if (N == 1) {
-        hipLaunchKernelGGL(k_spmv_wg, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
-                           W->spmv_blocks, W->rowptr, W->col, val, X, ldx, Y, ldy_r, bias, c_size,
-                           beta);
+    const void* val = W->val;
+    const float* rs = W->row_scale;
+    if (N == 1) {
+        hipLaunchKernelGGL(k_spmv_wg<I8>, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
+                           W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta);
     } else if (N < 64) {
         const int np = next_pow2((int)N);
         const int rows_per_block = kWaves * (64 / np);
         const unsigned grid = (unsigned)((M + rows_per_block - 1) / rows_per_block);
-#define PFR_SMALL(NPV)                                                                          \
-    case NPV:                                                                                   \
-        if (fast)                                                                               \
-            hipLaunchKernelGGL((k_spmm_small<NPV, true>), dim3(grid), dim3(256), 0, s, M, (int)N, \
-                               W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta); \
-        else                                                                                    \
-            hipLaunchKernelGGL((k_spmm_small<NPV, false>), dim3(grid), dim3(256), 0, s, M, (int)N,\
-                               W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta); \
+#define PFR_SMALL(NPV)                                                                                \
+    case NPV:                                                                                         \
+        hipLaunchKernelGGL((k_spmm_small<NPV, FAST, I8>), dim3(grid), dim3(256), 0, s, M, (int)N,   \
+                           W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta); \
         break;
         switch (np) {
             PFR_SMALL(2)
@@ -431,29 +462,37 @@ void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int6
         const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
         const bool vec = (N % 4 == 0) && (ldx % 4 == 0) && ldy_c == 1 && (ldy_r % 4 == 0) &&
                          aligned16(X) && aligned16(Y);
-        if (vec) {
-            if (fast)
-                hipLaunchKernelGGL((k_spmm_rows<true, true>), dim3(grid), dim3(256), 0, s, M, (int)N,
-                                   W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-            else
-                hipLaunchKernelGGL((k_spmm_rows<false, true>), dim3(grid), dim3(256), 0, s, M, (int)N,
-                                   W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-        } else {
-            if (fast)
-                hipLaunchKernelGGL((k_spmm_rows<true, false>), dim3(grid), dim3(256), 0, s, M, (int)N,
-                                   W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-            else
-                hipLaunchKernelGGL((k_spmm_rows<false, false>), dim3(grid), dim3(256), 0, s, M, (int)N,
-                                   W->rowptr, W->col, val, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-        }
+        if (vec)
+            hipLaunchKernelGGL((k_spmm_rows<FAST, true, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
+                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else
+            hipLaunchKernelGGL((k_spmm_rows<FAST, false, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
+                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+    }
+}
+
+// Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
+void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
+                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
+                 bool fast) {
+    if (W->M == 0 || N == 0) return;
+    const bool i8 = W->vdt == PFR_I8;
+    if (!i8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535) {
+        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast);
+    } else if (i8) {
+        if (fast) launch_csr_kernels<true, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else launch_csr_kernels<false, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+    } else {
+        if (fast) launch_csr_kernels<true, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else launch_csr_kernels<false, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
     }
     PFR_HIP(hipGetLastError());
 }
 
 void check_csr(const pfr_csr* W) {
     pfr::require(W != nullptr, "null CSR handle");
-    if (W->vdt != PFR_F32)
-        throw pfr::Error(PFR_ERR_UNSUPPORTED, "this entry point takes float32 CSR values");
+    if (W->vdt != PFR_F32 && W->vdt != PFR_I8)
+        throw pfr::Error(PFR_ERR_UNSUPPORTED, "CSR values must be float32 or int8");
 }
 
 void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,

@@ -93,3 +93,28 @@ def sp24_int8_weight(M, K, seed):
     symmetric int8."""
     w = keep_top2_of_4(np.random.default_rng(seed).standard_normal((M, K), dtype=np.float32))
     return symmetric_int8_rows(w)
+
+
+def csr_int8_lognormal(M, K, mean_density, sigma, std, seed):
+    """int8 weight-only CSR: lognormal row lengths (csr_lognormal_rows), values
+    N(0, std) quantised per row, symmetric (scale = absmax / 127), entries
+    that round to 0 dropped (the dequantised weight's CSR would not hold
+    them).  Returns indptr, indices, int8 values, float32 row scales."""
+    ip, ix, v = csr_lognormal_rows(M, K, mean_density, sigma, std, seed)
+    rows = np.repeat(np.arange(M), np.diff(ip))
+    absmax = np.zeros(M, np.float32)
+    np.maximum.at(absmax, rows, np.abs(v))
+    scale = np.where(absmax > 0, absmax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    q = np.clip(round_half_away(v * inv[rows]), -127, 127).astype(np.int8)
+    keep = q != 0
+    counts = np.bincount(rows[keep], minlength=M)
+    ip2 = np.zeros(M + 1, np.int64)
+    np.cumsum(counts, out=ip2[1:])
+    return ip2, ix[keep], q[keep], scale
+
+
+def dequant_rows(ip, q, scale):
+    """float32 values RN((float)q * scale[row]) of an int8 CSR."""
+    rows = np.repeat(np.arange(len(ip) - 1), np.diff(ip))
+    return (q.astype(np.float32) * scale[rows]).astype(np.float32)

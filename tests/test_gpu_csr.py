@@ -269,3 +269,33 @@ def test_column_slice_layout_cases(ctx):
     assert np.array_equal(np.isnan(Y), np.isnan(R))
     fin = ~np.isnan(R)
     assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
+
+
+def test_int8_csr_dequant_fused(ctx):
+    """int8 CSR values with per-row scales: every product uses
+    RN((float)q * scale[row]), i.e. dequantize_tensor followed by the fp32
+    CSR kernels, bit for bit.  Skewed (lognormal) rows, N = 1 .. 100, and the
+    Gemm form with an int8 weight in the B position."""
+    ip, ix, q, sc = workloads.csr_int8_lognormal(1500, 2100, 0.3, 0.5, 0.02, seed=31)
+    vals = workloads.dequant_rows(ip, q, sc)
+    # the dequantised values are what the oracle's dequantize_tensor gives
+    dense_q = np.zeros((1500, 2100), np.int8)
+    dense_q[np.repeat(np.arange(1500), np.diff(ip)), ix] = q
+    dq = O.orc_dequantize(dense_q, sc, np.zeros(1500, np.int32), O.I8, (1, 1500, 2100))
+    assert np.array_equal(dq[dense_q != 0].view(np.uint32),
+                          vals.view(np.uint32)[np.argsort(np.repeat(np.arange(1500), np.diff(ip)) * 2100 + ix,
+                                                          kind="stable")])
+    W = ctx.csr_upload(1500, 2100, ip, ix, q, row_scales=sc)
+    rng = np.random.default_rng(4)
+    for N in (1, 2, 8, 64, 100):
+        say(f"int8 CSR N={N}")
+        X = rng.standard_normal((2100, N)).astype(np.float32)
+        Xa = X[:, 0] if N == 1 else X
+        assert bits_equal(W.spmm(Xa), O.orc_csr_spmm(1500, 2100, ip, ix, vals, Xa)), N
+    # Gemm form: Y = A . B with B = dequantised W^T (the CSR is of B^T)
+    A = rng.standard_normal((37, 2100)).astype(np.float32)
+    bias = rng.standard_normal(1500).astype(np.float32)
+    Bd = np.zeros((2100, 1500), np.float32)
+    Bd[ix, np.repeat(np.arange(1500), np.diff(ip))] = vals
+    say("int8 CSR Gemm form")
+    assert bits_equal(ctx.gemm_csr(A, W, 1.0, 1.0, bias), O.orc_gemm(A, Bd, bias, 1.0, 1.0))
