@@ -91,6 +91,167 @@ def time_host_entry(ctx, ip, ix, v, Xh, calls=20):
     return res
 
 
+def bench_mlp_session(cpu):
+    """MLP 784-512-10 (Gemm + Relu + Gemm + Softmax), weights N(0, 0.05)
+    magnitude-pruned to 90 %, biases zero, batch 32 U(0, 1), through
+    InferenceSession(device="rocm"): end-to-end microseconds per run()
+    (host tensors in and out, as the reference API hands them over)."""
+    import tempfile
+
+    import numpy as np
+
+    from pyflamert_amd import pfm, session
+
+    rng = np.random.default_rng(1234)
+
+    def pruned(shape):
+        w = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+        thr = np.partition(np.abs(w).ravel(), int(0.9 * w.size))[int(0.9 * w.size)]
+        return np.where(np.abs(w) > thr, w, np.float32(0)).astype(np.float32)
+
+    w1, w2 = pruned((784, 512)), pruned((512, 10))
+    model = {"name": "mlp", "inputs": [("x", 0, [32, 784])], "outputs": [("y", 0, [32, 10])],
+             "initializers": {"fc1.weight": w1, "fc1.bias": np.zeros(512, np.float32),
+                              "fc2.weight": w2, "fc2.bias": np.zeros(10, np.float32)},
+             "nodes": [("gemm1", "Gemm", ["x", "fc1.weight", "fc1.bias"], ["h1"], {"alpha": 1.0, "beta": 1.0}),
+                       ("relu1", "Relu", ["h1"], ["a1"], {}),
+                       ("gemm2", "Gemm", ["a1", "fc2.weight", "fc2.bias"], ["z2"], {"alpha": 1.0, "beta": 1.0}),
+                       ("softmax", "Softmax", ["z2"], ["y"], {"axis": -1})]}
+    x = rng.random((32, 784), dtype=np.float32)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "mlp.pfm")
+        pfm.save(model, path)
+        sess = session.InferenceSession(path, session.SessionOptions(device="rocm"))
+        for _ in range(10):
+            sess.run(None, {"x": x})
+        ts = []
+        for _ in range(200):
+            t0 = time.perf_counter()
+            sess.run(None, {"x": x})
+            ts.append(time.perf_counter() - t0)
+        sess.close()
+        res = {"us_per_run": round(float(np.median(ts)) * 1e6, 1),
+               "nnz": [int((w1 != 0).sum()), int((w2 != 0).sum())],
+               "flop_per_run": 2 * 32 * int((w1 != 0).sum() + (w2 != 0).sum())}
+        if cpu:
+            from oracle import oracle as O
+
+            if O.have_ref():
+                O.ref_run_pfm(path, "x", x, 320)
+                tc = []
+                for _ in range(20):
+                    t0 = time.perf_counter()
+                    O.ref_run_pfm(path, "x", x, 320)
+                    tc.append(time.perf_counter() - t0)
+                res["cpu_reference_us_per_run"] = round(float(np.median(tc)) * 1e6, 1)
+                res["cpu_note"] = ("reference CPUExecutor compiled from its sources, 1 thread, .pfm load + "
+                                   "execute per call")
+    log(f"MLP session: {res}")
+    return res
+
+
+def bench_bert_linears(ctx):
+    """BERT-base-shaped encoder's pruned linears: 12 layers x (4 x 768x768,
+    768x3072, 3072x768), 80 % uniform-random sparsity, 1024 tokens (batch 8 x
+    seq 128), Gemm form with bias (the rocm::Gemm kernel), strict.  Dense
+    attention stays on the reference path and is not timed.  Per-layer time
+    is the sum of one timed launch of each shape."""
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import workloads
+
+    T = 1024
+    shapes = {"qkvo_768x768": (768, 768, 4), "ffn_up_3072x768": (3072, 768, 1), "ffn_down_768x3072": (768, 3072, 1)}
+    res, layer_ms, nnz_layer = {}, 0.0, 0
+    for name, (out_f, in_f, count) in shapes.items():
+        ip, ix, v = workloads.csr_uniform(out_f, in_f, 0.2, 0.02, seed=out_f * 7 + in_f)
+        Ws = [ctx.csr_upload(out_f, in_f, ip, ix, v) for _ in range(4)]
+        A = torch.randn((T, in_f), dtype=torch.float32, device="cuda")
+        bias = torch.randn((out_f,), dtype=torch.float32, device="cuda")
+        Y = torch.empty((T, out_f), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+
+        def launch(i):
+            ctx.gemm_csr_dev(A.data_ptr(), T, in_f, Ws[i % 4], Y.data_ptr(), 1.0, 1.0, bias.data_ptr(), out_f)
+
+        for i in range(10):
+            launch(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(100):
+            launch(i)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / 100
+        res[name] = {"ms": round(ms, 5), "nnz": len(v), "gflops": round(2.0 * len(v) * T / (ms * 1e-3) / 1e9, 1)}
+        layer_ms += count * ms
+        nnz_layer += count * len(v)
+        for W in Ws:
+            W.free()
+    res["per_forward_ms"] = round(12 * layer_ms, 4)
+    res["tokens_per_s"] = round(T / (12 * layer_ms * 1e-3), 1)
+    res["gflops"] = round(2.0 * 12 * nnz_layer * T / (12 * layer_ms * 1e-3) / 1e9, 1)
+    log(f"BERT linears: {res}")
+    return res
+
+
+def bench_decode_int8(ctx):
+    """Llama-2-7B-shaped decode linear stack: 32 layers x (4 x 4096x4096,
+    2 x 11008x4096, 4096x11008), 70 % sparsity with lognormal (sigma 0.5) row
+    lengths, int8 weight-only with per-row scales (dequantisation fused),
+    fp32 activations, batch 1 and 8; fast mode (wave-parallel reassociated
+    sums, within 1e-5 normwise) and strict mode (bit-exact, storage-order
+    sums).  Per-step time is the sum over
+    the stack of one timed launch per shape (4 rotating copies each)."""
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import workloads
+
+    shapes = {"qkvo_4096x4096": (4096, 4096, 4), "gate_up_11008x4096": (11008, 4096, 2),
+              "down_4096x11008": (4096, 11008, 1)}
+    weights = {}
+    for name, (M_, K_, _) in shapes.items():
+        ip, ix, q, sc = workloads.csr_int8_lognormal(M_, K_, 0.3, 0.5, 0.02, seed=M_ + 3 * K_)
+        weights[name] = ([ctx.csr_upload(M_, K_, ip, ix, q, row_scales=sc) for _ in range(4)], len(q))
+    res = {}
+    for B, mode in ((1, "fast"), (8, "fast"), (1, "strict"), (8, "strict")):
+        step_ms, byts, flops = 0.0, 0, 0
+        per = {}
+        for name, (M_, K_, count) in shapes.items():
+            Ws, nnz = weights[name]
+            X = torch.randn((K_, B), dtype=torch.float32, device="cuda")
+            Y = torch.empty((M_, B), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            for i in range(10):
+                Ws[i % 4].spmm_dev(X.data_ptr(), B, Y.data_ptr(), mode=mode)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(100):
+                Ws[i % 4].spmm_dev(X.data_ptr(), B, Y.data_ptr(), mode=mode)
+            b.record()
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / 100
+            lb = nnz * 5 + 4 * (M_ + 1) + 4 * M_ + 4 * K_ * B + 4 * M_ * B
+            per[name] = {"ms": round(ms, 5), "nnz": nnz, "gbs": round(lb / (ms * 1e-3) / 1e9, 1)}
+            step_ms += 32 * count * ms
+            byts += 32 * count * lb
+            flops += 32 * count * 2 * nnz * B
+        res[f"batch{B}_{mode}"] = {"per_shape": per, "step_ms": round(step_ms, 4),
+                            "tokens_per_s": round(B / (step_ms * 1e-3), 1),
+                            "gbs": round(byts / (step_ms * 1e-3) / 1e9, 1),
+                            "hbm_frac": round(byts / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                            "gflops": round(flops / (step_ms * 1e-3) / 1e9, 1)}
+        log(f"decode int8 batch {B} {mode}: {res[f'batch{B}_{mode}']}")
+    for Ws, _ in weights.values():
+        for W in Ws:
+            W.free()
+    return res
+
+
 def recorded_traffic():
     """Bytes per launch of the main kernel measured by the profiler runs
     described in TRAFFIC_FILE, or None when that record is absent."""
@@ -283,6 +444,9 @@ def main():
     if not args.only_main:
         extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)
         extra["sp24_i8"] = bench_sp24(ctx, args)
+        extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
+        extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
+        extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
 
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)

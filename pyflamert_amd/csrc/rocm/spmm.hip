@@ -218,6 +218,77 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     }
 }
 
+// Fast mode, N <= 8: one wave per row, lane l takes the row's nonzeros
+// l, l + 64, ... (coalesced index and value streams).  Each lane issues the
+// loads of U nonzeros at once (indices clamped into the row, so every load
+// is unconditional and in flight together), then their X rows (two float4
+// per nonzero for NB = 8 when X rows are 16-byte aligned), then fused
+// multiply-adds into per-column partial sums, reduced across the wave at
+// the end.  The sum is reassociated, so this kernel serves the fast mode
+// only.
+template <int NB, bool I8, bool XV>
+__global__ __launch_bounds__(256) void k_spmv_fast(
+    int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+    const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
+    float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias, int64_t c_size,
+    float beta) {
+    constexpr int U = NB == 1 ? 16 : (NB <= 4 ? 8 : 4);
+    const int lane = threadIdx.x & 63;
+    const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kWaves + (int)(threadIdx.x >> 6));
+    if (row >= M) return;
+    const int beg = rowptr[row], end = rowptr[row + 1];
+    float acc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) acc[c] = 0.0f;
+    for (int base = beg; base < end; base += 64 * U) {
+        int cl[U];
+        float w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int jj = min(base + lane + 64 * u, end - 1);
+            cl[u] = col[jj];
+            w[u] = wval<I8>(val, rs, jj, row);
+        }
+        float xv[U][NB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float* xr = X + (int64_t)cl[u] * ldx;
+            if constexpr (XV && NB % 4 == 0) {
+#pragma unroll
+                for (int c = 0; c < NB; c += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(xr + c);
+                    xv[u][c] = v.x; xv[u][c + 1] = v.y; xv[u][c + 2] = v.z; xv[u][c + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < NB; ++c) xv[u][c] = c < N ? xr[c] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (base + lane + 64 * u < end) {
+#pragma unroll
+                for (int c = 0; c < NB; ++c) acc[c] = __builtin_fmaf(w[u], xv[u][c], acc[c]);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NB; ++c) {
+        float v = acc[c];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+        acc[c] = v;
+    }
+    if (lane < N && lane < NB) {
+        float v = acc[0];
+#pragma unroll
+        for (int c = 1; c < NB; ++c)
+            if (lane == c) v = acc[c];
+        const int64_t f = (int64_t)row * ldy_r + (int64_t)lane * ldy_c;
+        Y[f] = bias_add(v, f, bias, c_size, beta);
+    }
+}
+
 // At[k, i] = RN(alpha * A[i, k]) for A rows x cols (At cols x rows).
 __global__ __launch_bounds__(256) void k_transpose_scale(const float* __restrict__ A, int64_t rows,
                                                          int64_t cols, float alpha, int scale,
@@ -435,7 +506,22 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     hipStream_t s = ctx->stream;
     const void* val = W->val;
     const float* rs = W->row_scale;
-    if (N == 1) {
+    if (FAST && N <= 8) {
+        const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
+        const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);
+        if (N == 1)
+            hipLaunchKernelGGL((k_spmv_fast<1, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else if (N <= 4)
+            hipLaunchKernelGGL((k_spmv_fast<4, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else if (xv)
+            hipLaunchKernelGGL((k_spmv_fast<8, I8, true>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        else
+            hipLaunchKernelGGL((k_spmv_fast<8, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+    } else if (N == 1) {
         hipLaunchKernelGGL(k_spmv_wg<I8>, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
                            W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta);
     } else if (N < 64) {

@@ -292,6 +292,13 @@ def test_int8_csr_dequant_fused(ctx):
         X = rng.standard_normal((2100, N)).astype(np.float32)
         Xa = X[:, 0] if N == 1 else X
         assert bits_equal(W.spmm(Xa), O.orc_csr_spmm(1500, 2100, ip, ix, vals, Xa)), N
+    # fast mode (reassociated wave sums for N <= 8): normwise within 1e-5
+    for N in (1, 3, 8):
+        X = rng.standard_normal((2100, N)).astype(np.float32)
+        Xa = X[:, 0] if N == 1 else X
+        R = O.orc_csr_spmm(1500, 2100, ip, ix, vals, Xa)
+        Y = W.spmm(Xa, mode="fast")
+        assert np.abs(Y - R).max() <= 1e-5 * np.abs(R).max(), N
     # Gemm form: Y = A . B with B = dequantised W^T (the CSR is of B^T)
     A = rng.standard_normal((37, 2100)).astype(np.float32)
     bias = rng.standard_normal(1500).astype(np.float32)
