@@ -385,6 +385,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="time only the N=256 SpMM (profiler runs)")
+    ap.add_argument("--only-sp24", action="store_true", help="time only the 2:4 int8 GEMM (profiler runs)")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
                     help="run a copy-like kernel of MIB MiB for counter calibration and exit")
     args = ap.parse_args()
@@ -405,6 +406,10 @@ def main():
     torch.cuda.init()
     ctx = rocm.Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    if args.only_sp24:
+        print(json.dumps({"sp24_i8": bench_sp24(ctx, args)}), flush=True)
+        ctx.close()
+        return
 
     log("generating W 4096x4096 at 10% density ...")
     ip, ix, v = workloads.csr_uniform(M, K, DENSITY, 0.02, seed=1234)
