@@ -22,6 +22,7 @@
 
 #pragma clang fp contract(off)
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -174,10 +175,21 @@ constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 
 #define PFR_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <int OUT>
+// B source: XROW = false reads XT (Np x Kp, the transposed activation),
+// XROW = true reads the row-major activation X itself (K % 512 == 0,
+// N % 128 == 0, rows 16-byte aligned).  In the XROW form LDS holds the step's
+// 128 X rows (128 bytes each, 16-byte chunk c of row k at position
+// c ^ xrow_swizzle(k)) and the B fragments are assembled with
+// ds_read_b64_tr_b8: within each 16-lane group the sixteen 8-byte reads form
+// a 16 x 8 byte matrix S and lane t receives S[2i + t/8][t % 8], i = 0..7;
+// so source lane s pointing at row k0 + s/2, bytes 8(s % 2) of the column
+// chunk gives lane t the eight k values k0 .. k0+7 of column chunk + t.
+__device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((k >> 4) & 1) << 2); }
+
+template <int OUT, bool XROW>
 __global__ __launch_bounds__(512) void k_sp24_i8(
     int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
-    const int8_t* __restrict__ XT, int64_t Kp, int M, int N, const float* __restrict__ ws, float xs,
+    const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
     float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn) {
     __shared__ __attribute__((aligned(1024))) char st0[kStage];
     __shared__ __attribute__((aligned(1024))) char st1[kStage];
@@ -197,8 +209,8 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
     const int64_t mb0 = (int64_t)mt * 16;
     const int64_t n0 = (int64_t)nt * kI8TileN;
     // every wave issues six direct-to-LDS loads per k step: A row blocks w and
-    // w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), XT rows
-    // 16w .. 16w + 15 (two 1 KiB runs of 8 rows)
+    // w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), B rows
+    // 16w .. 16w + 15 of the step's tile (two 1 KiB runs of 8 rows)
     const v4i* asrc = A + ((mb0 + w) * nkt) * 64 + l;
     const int64_t a_rb8 = (int64_t)8 * nkt * 64;
     const uint32_t* isrc = I + ((mb0 + 2 * w) * nkt) * 64 + l;
@@ -207,9 +219,15 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int n = 16 * w + 8 * i + (l >> 3);
-        const int chunk = (l & 7) ^ ((n >> 1) & 7);
-        bsrc[i] = reinterpret_cast<const v4i*>(XT + (n0 + n) * Kp + 16 * chunk);
+        if constexpr (XROW) {
+            const int chunk = (l & 7) ^ xrow_swizzle(n);
+            bsrc[i] = reinterpret_cast<const v4i*>(B + (int64_t)n * ldb + n0 + 16 * chunk);
+        } else {
+            const int chunk = (l & 7) ^ ((n >> 1) & 7);
+            bsrc[i] = reinterpret_cast<const v4i*>(B + (n0 + n) * ldb + 16 * chunk);
+        }
     }
+    const int64_t b_step = XROW ? 128 * ldb / 16 : 8;  // v4i per k step
     auto issue = [&](char* st, int s) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -219,14 +237,23 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
             __builtin_amdgcn_global_load_lds(isrc + i * i_rb1 + (int64_t)s * 64, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * 8, PFR_LDS(st + kLdsA + kLdsI + (16 * w + 8 * i) * 128), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * b_step, PFR_LDS(st + kLdsA + kLdsI + (16 * w + 8 * i) * 128), 16, 0, 0);
     };
-    int boff_lo[4], boff_hi[4];
+    int boff_lo[4], boff_hi[4];  // XT form: the two 16-byte pieces of column n
+    // X-row form: transpose read r of this lane starts at row
+    // k_r = 16kb + 8(r & 1) + 64(r >> 1) + c/2, bytes 8(c % 2) of the chunk.
+    // xrow_swizzle(k_r) is the same for all four reads (bits 1-2 of k_r come
+    // from c/2, bit 4 from kb), and the rows differ by constants, so one base
+    // and one swizzle serve them all.
+    const int trk = kLdsA + kLdsI + (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
+    const int trf = xrow_swizzle(16 * kb + (c >> 1));
+    if constexpr (!XROW) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = wn * 64 + 16 * j + c, sw = (n >> 1) & 7;
-        boff_lo[j] = kLdsA + kLdsI + n * 128 + 16 * (kb ^ sw);
-        boff_hi[j] = kLdsA + kLdsI + n * 128 + 16 * ((4 + kb) ^ sw);
+        for (int j = 0; j < 4; ++j) {
+            const int n = wn * 64 + 16 * j + c, sw = (n >> 1) & 7;
+            boff_lo[j] = kLdsA + kLdsI + n * 128 + 16 * (kb ^ sw);
+            boff_hi[j] = kLdsA + kLdsI + n * 128 + 16 * ((4 + kb) ^ sw);
+        }
     }
     v4i acc[4][4];
 #pragma unroll
@@ -241,9 +268,20 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
     auto fetch = [&](Frag& f, const char* st) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const v4i lo = *reinterpret_cast<const v4i*>(st + boff_lo[j]);
-            const v4i hi = *reinterpret_cast<const v4i*>(st + boff_hi[j]);
-            f.b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            if constexpr (XROW) {
+                const int cj = wn * 4 + j;  // 16-column chunk of this fragment
+                v2i q[4];
+                const char* bp = st + trk + 16 * (cj ^ trf);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    q[r] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                        (__attribute__((address_space(3))) v2i*)(bp + 1024 * (r & 1) + 8192 * (r >> 1)));
+                f.b[j] = v8i{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
+            } else {
+                const v4i lo = *reinterpret_cast<const v4i*>(st + boff_lo[j]);
+                const v4i hi = *reinterpret_cast<const v4i*>(st + boff_hi[j]);
+                f.b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -544,31 +582,45 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
         pfr::require(out_scale > 0.0f && std::isfinite(out_scale), "output scale must be positive and finite");
         inv_out = 1.0f / out_scale;  // quant_ops.cpp:41
     }
-    // XT: Np x Kp, zero padded (the kernel reads whole 128 x 128 tiles)
-    const int64_t Np = round_up(N, kI8TileN), Kp = W->Kp;
-    int8_t* xt = static_cast<int8_t*>(ctx->scratch[3].ensure((size_t)(Np * Kp)));
-    const int vec = (ldx % 16 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0) ? 1 : 0;
-    hipLaunchKernelGGL(k_transpose_i8, dim3((unsigned)(Kp / 64), (unsigned)((Np + 255) / 256)), dim3(256), 0,
-                       ctx->stream, X, W->K, N, ldx, vec, xt, Kp, Np);
-    PFR_HIP(hipGetLastError());
-    const int ntn = (int)(Np / kI8TileN);
-    dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
+    const int64_t Kp = W->Kp;
     const int nkt = (int)(Kp / 128);
     const int yvec = (ldy % 16 == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) ? 1 : 0;
     const v4i* A = static_cast<const v4i*>(W->a);
-    switch (out_kind) {
-        case PFR_SP24_OUT_I32:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I32>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
-                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
-            break;
-        case PFR_SP24_OUT_F32:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_F32>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
-                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
-            break;
-        default:
-            hipLaunchKernelGGL(k_sp24_i8<PFR_SP24_OUT_I8>, grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, xt,
-                               Kp, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn);
+    // The kernel reads whole 128-column, 128-row B tiles.  X itself serves
+    // when those stay inside it and its rows are 16-byte aligned; otherwise
+    // it is transposed into a zero-padded XT (Np x Kp) first.
+    const bool xrow = W->K == Kp && N % kI8TileN == 0 && ldx % 16 == 0 &&
+                      (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    int64_t Np = N;
+    const int8_t* B = X;
+    int64_t ldb = ldx;
+    if (!xrow) {
+        Np = round_up(N, kI8TileN);
+        int8_t* xt = static_cast<int8_t*>(ctx->scratch[3].ensure((size_t)(Np * Kp)));
+        const int vec = (ldx % 16 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0) ? 1 : 0;
+        hipLaunchKernelGGL(k_transpose_i8, dim3((unsigned)(Kp / 64), (unsigned)((Np + 255) / 256)), dim3(256), 0,
+                           ctx->stream, X, W->K, N, ldx, vec, xt, Kp, Np);
+        PFR_HIP(hipGetLastError());
+        B = xt;
+        ldb = Kp;
     }
+    const int ntn = (int)(Np / kI8TileN);
+    dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
+#define PFR_SP24_LAUNCH(OUTK)                                                                              \
+    do {                                                                                                   \
+        if (xrow)                                                                                          \
+            hipLaunchKernelGGL((k_sp24_i8<OUTK, true>), grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, B, \
+                               ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
+        else                                                                                               \
+            hipLaunchKernelGGL((k_sp24_i8<OUTK, false>), grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, B, \
+                               ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
+    } while (0)
+    switch (out_kind) {
+        case PFR_SP24_OUT_I32: PFR_SP24_LAUNCH(PFR_SP24_OUT_I32); break;
+        case PFR_SP24_OUT_F32: PFR_SP24_LAUNCH(PFR_SP24_OUT_F32); break;
+        default: PFR_SP24_LAUNCH(PFR_SP24_OUT_I8);
+    }
+#undef PFR_SP24_LAUNCH
     PFR_HIP(hipGetLastError());
 }
 
