@@ -49,6 +49,12 @@ typedef enum pfr_dtype {
 
 typedef enum pfr_mode { PFR_MODE_STRICT = 0, PFR_MODE_FAST = 1 } pfr_mode;
 
+/* Activation fused into a product's epilogue (after the bias). */
+typedef enum pfr_act {
+    PFR_ACT_NONE = 0,
+    PFR_ACT_RELU = 1  /* cpu_relu, activation.cpp:45-60: std::max(0.0f, v) */
+} pfr_act;
+
 typedef struct pfr_ctx pfr_ctx;   /* one device + one stream + scratch */
 typedef struct pfr_csr pfr_csr;   /* device-resident CSR weight */
 typedef struct pfr_sp24 pfr_sp24; /* device-resident 2:4 compressed weight */
@@ -69,6 +75,18 @@ int pfr_rocm_destroy(pfr_ctx* ctx);
 int pfr_ctx_get_stream(pfr_ctx* ctx, void** stream);
 int pfr_ctx_set_stream(pfr_ctx* ctx, void* stream);
 int pfr_synchronize(pfr_ctx* ctx);
+
+/* Device buffers for callers that keep activations on the GPU between
+ * nodes (the executor's device-resident plan; the reference's Tensor storage,
+ * src/tensor.cpp:31-49, is host memory only).  pfr_copy_to_device enqueues
+ * on the context's stream (the host source must stay valid until the stream
+ * reaches the copy, e.g. until a later pfr_copy_to_host or
+ * pfr_synchronize); pfr_copy_to_host waits for the stream.  pfr_dev_free
+ * waits for the stream before freeing. */
+int pfr_dev_alloc(pfr_ctx* ctx, int64_t bytes, void** out);
+int pfr_dev_free(pfr_ctx* ctx, void* p);
+int pfr_copy_to_device(pfr_ctx* ctx, void* dst, const void* src, int64_t bytes);
+int pfr_copy_to_host(pfr_ctx* ctx, void* dst, const void* src, int64_t bytes);
 
 /* ---- CSR weights (reference: pruning::SparseTensor, sparse_tensor.hpp:19-132) */
 
@@ -111,6 +129,13 @@ int pfr_spmm_csr(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N,
 int pfr_spmm_csr_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X,
                      int64_t N, int64_t ldx, float* Y, int64_t ldy, int mode);
 
+/* pfr_spmm_csr_dev with an activation fused into the epilogue: the node
+ * pair MatMul(W, X) -> Relu (math.cpp:268-374 then activation.cpp:45-60) in
+ * one pass, bit-identical to the two nodes in strict mode. */
+int pfr_spmm_csr_act_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X,
+                         int64_t N, int64_t ldx, float* Y, int64_t ldy,
+                         int mode, int act);
+
 /* Gemm with the weight in the B position (cpu_gemm, math.cpp:377-438):
  *   Y[Mb, Nf] = alpha * op(A)[Mb, K] . B[K, Nf] + beta * C[(i*Nf+j) % c_size]
  * where BT is the CSR of op(B)^T (Nf x K, from pfr_csr_from_dense with
@@ -124,6 +149,14 @@ int pfr_gemm_csr(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
 int pfr_gemm_csr_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
                      int transA, const pfr_csr* BT, float alpha, float beta,
                      const float* C, int64_t c_size, float* Y, int mode);
+
+/* pfr_gemm_csr_dev with an activation fused after the bias: the node pair
+ * Gemm -> Relu (math.cpp:377-438 then activation.cpp:45-60) in one pass,
+ * bit-identical to the two nodes in strict mode. */
+int pfr_gemm_csr_act_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
+                         int transA, const pfr_csr* BT, float alpha, float beta,
+                         const float* C, int64_t c_size, float* Y, int mode,
+                         int act);
 
 /* ---- 2:4 structured weights (sparse MFMA, gfx950 smfmac) ------------------- */
 

@@ -30,9 +30,13 @@ typedef struct pfr_session pfr_session;
 
 const char* pfr_session_last_error(void);
 /* device: "rocm" (other reference devices are rejected by this runtime).
- * math_mode: 0 strict (bit-exact fp32), 1 fast (FMA). */
+ * math_mode: 0 strict (bit-exact fp32), 1 fast (FMA).
+ * optimization_level: the reference's OptLevel (types.hpp:119-124).  0 None
+ * runs node by node through the rocm:: OpFuncs; 1 Basic runs the
+ * device-resident plan; 2 Extended (the reference's default) and 3 All add
+ * operator fusion (Relu into the preceding pruned product). */
 int pfr_session_create(const char* model_path, const char* device, int strict_math_mode, int math_mode,
-                       int device_id, pfr_session** out);
+                       int device_id, int optimization_level, pfr_session** out);
 int pfr_session_destroy(pfr_session* s);
 int pfr_session_io_count(pfr_session* s, int* n_inputs, int* n_outputs);
 /* Name, DType code and shape (-1 = dynamic, at most 16 dims) of input or
@@ -48,6 +52,11 @@ int pfr_session_result(pfr_session* s, int index, int* dtype, int64_t* shape, in
 /* Backend identity and the op types it runs ("rocm::" kernels), newline
  * separated into buf (NUL-terminated, truncated to cap). */
 int pfr_session_supported_ops(pfr_session* s, char* buf, int64_t cap);
+/* After a run: *device_resident = 1 when the model runs as a device-resident
+ * plan (graph inputs copied to the GPU once, activations kept there between
+ * nodes, a Relu that is a product's only consumer fused into the product),
+ * with *steps its kernel launches; 0 and 0 when it runs node by node. */
+int pfr_session_device_plan(pfr_session* s, int* device_resident, int* steps);
 
 /* Host-side model utilities (no device needed).  pfr_model_describe loads
  * and validates a .pfm with this runtime's loader and writes a JSON summary

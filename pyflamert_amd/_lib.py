@@ -23,6 +23,7 @@ PFR_ERR_NO_DEVICE = 4
 
 PFR_F32, PFR_BF16, PFR_I32, PFR_I8, PFR_U8 = 0, 2, 5, 7, 8
 MODE_STRICT, MODE_FAST = 0, 1
+ACT_NONE, ACT_RELU = 0, 1
 SP24_OUT_I32, SP24_OUT_F32, SP24_OUT_I8 = 0, 1, 2
 
 _P = C.c_void_p
@@ -41,14 +42,20 @@ SIGNATURES = {
     "pfr_ctx_get_stream": (_INT, [_P, _PP]),
     "pfr_ctx_set_stream": (_INT, [_P, _P]),
     "pfr_synchronize": (_INT, [_P]),
+    "pfr_dev_alloc": (_INT, [_P, _I64, _PP]),
+    "pfr_dev_free": (_INT, [_P, _P]),
+    "pfr_copy_to_device": (_INT, [_P, _P, _P, _I64]),
+    "pfr_copy_to_host": (_INT, [_P, _P, _P, _I64]),
     "pfr_csr_upload": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _PP]),
     "pfr_csr_from_dense": (_INT, [_P, _P, _I64, _I64, _INT, _F, _PP]),
     "pfr_csr_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
     "pfr_csr_free": (_INT, [_P]),
     "pfr_spmm_csr": (_INT, [_P, _P, _P, _I64, _P, _INT]),
     "pfr_spmm_csr_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64, _INT]),
+    "pfr_spmm_csr_act_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64, _INT, _INT]),
     "pfr_gemm_csr": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
     "pfr_gemm_csr_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
+    "pfr_gemm_csr_act_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT, _INT]),
     "pfr_sp24_pack": (_INT, [_P, _I64, _I64, _P, _INT, _P, _I64, _PP]),
     "pfr_sp24_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_INT)]),
     "pfr_sp24_free": (_INT, [_P]),

@@ -91,4 +91,40 @@ int pfr_synchronize(pfr_ctx* ctx) {
     });
 }
 
+int pfr_dev_alloc(pfr_ctx* ctx, int64_t bytes, void** out) {
+    return pfr::guarded([&] {
+        pfr::require(out != nullptr, "null output pointer");
+        *out = nullptr;
+        pfr::require(bytes >= 0, "negative size");
+        pfr::bind(ctx);
+        PFR_HIP(hipMalloc(out, (size_t)(bytes > 0 ? bytes : 4)));
+    });
+}
+
+int pfr_dev_free(pfr_ctx* ctx, void* p) {
+    return pfr::guarded([&] {
+        if (!p) return;
+        pfr::bind(ctx);
+        PFR_HIP(hipStreamSynchronize(ctx->stream));  // no kernel may still use it
+        PFR_HIP(hipFree(p));
+    });
+}
+
+int pfr_copy_to_device(pfr_ctx* ctx, void* dst, const void* src, int64_t bytes) {
+    return pfr::guarded([&] {
+        pfr::require(bytes >= 0 && (bytes == 0 || (dst && src)), "bad copy");
+        pfr::bind(ctx);
+        if (bytes) PFR_HIP(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream));
+    });
+}
+
+int pfr_copy_to_host(pfr_ctx* ctx, void* dst, const void* src, int64_t bytes) {
+    return pfr::guarded([&] {
+        pfr::require(bytes >= 0 && (bytes == 0 || (dst && src)), "bad copy");
+        pfr::bind(ctx);
+        if (bytes) PFR_HIP(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
 }  // extern "C"

@@ -41,12 +41,17 @@ __device__ __forceinline__ float wval(const void* __restrict__ val, const float*
     }
 }
 
-// Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size].
+// Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size],
+// then optionally a fused Relu (activation.cpp:45-60: std::max(0.0f, v), which
+// is (0 < v) ? v : +0, so -0 and NaN give +0).
 __device__ __forceinline__ float bias_add(float v, int64_t f, const float* __restrict__ bias,
-                                          int64_t c_size, float beta) {
-    if (bias == nullptr) return v;
-    const float t = beta * bias[f % c_size];
-    return v + t;
+                                          int64_t c_size, float beta, int act) {
+    if (bias != nullptr) {
+        const float t = beta * bias[f % c_size];
+        v = v + t;
+    }
+    if (act == PFR_ACT_RELU) v = (0.0f < v) ? v : 0.0f;
+    return v;
 }
 
 // One wave per CSR row, lanes across the N columns (4 per lane when VEC).
@@ -56,7 +61,7 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
     int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
-    int64_t c_size, float beta) {
+    int64_t c_size, float beta, int act) {
     const int lane = threadIdx.x & 63;
     const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kWaves + (int)(threadIdx.x >> 6));
     if (row >= M) return;
@@ -93,10 +98,10 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
             }
             const int64_t f = (int64_t)row * ldy_r + c0;  // ldy_c == 1 here
             float4 o;
-            o.x = bias_add(a0, f, bias, c_size, beta);
-            o.y = bias_add(a1, f + 1, bias, c_size, beta);
-            o.z = bias_add(a2, f + 2, bias, c_size, beta);
-            o.w = bias_add(a3, f + 3, bias, c_size, beta);
+            o.x = bias_add(a0, f, bias, c_size, beta, act);
+            o.y = bias_add(a1, f + 1, bias, c_size, beta, act);
+            o.z = bias_add(a2, f + 2, bias, c_size, beta, act);
+            o.w = bias_add(a3, f + 3, bias, c_size, beta, act);
             *reinterpret_cast<float4*>(Y + f) = o;
         }
     } else {
@@ -105,7 +110,7 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
 #pragma unroll 4
             for (int j = beg; j < end; ++j) a = madd<FAST>(a, wval<I8>(val, rs, j, row), X[(int64_t)col[j] * ldx + c]);
             const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
-            Y[f] = bias_add(a, f, bias, c_size, beta);
+            Y[f] = bias_add(a, f, bias, c_size, beta, act);
         }
     }
 }
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(256) void k_spmm_small(
     int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
-    int64_t c_size, float beta) {
+    int64_t c_size, float beta, int act) {
     constexpr int RPW = 64 / NP;
     const int lane = threadIdx.x & 63;
     const int g = lane / NP, c = lane % NP;
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(256) void k_spmm_small(
 #pragma unroll 4
     for (int j = beg; j < end; ++j) a = madd<FAST>(a, wval<I8>(val, rs, j, row), X[(int64_t)col[j] * ldx + c]);
     const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
-    Y[f] = bias_add(a, f, bias, c_size, beta);
+    Y[f] = bias_add(a, f, bias, c_size, beta, act);
 }
 
 // SpMV.  One workgroup per row block (<= 64 rows, <= kSpmvCap nnz unless a
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     const int32_t* __restrict__ blocks, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ col, const void* __restrict__ val, const float* __restrict__ rs,
     const float* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy_r,
-    const float* __restrict__ bias, int64_t c_size, float beta) {
+    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
     __shared__ float P[kSpmvCap];
     __shared__ int8_t Q[I8 ? kSpmvCap : 1];
     constexpr int kPer = kSpmvCap / kSpmvThreads;
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     }
     if (folder) {
         const int64_t f = (int64_t)my_row * ldy_r;
-        y[f] = bias_add(acc, f, bias, c_size, beta);
+        y[f] = bias_add(acc, f, bias, c_size, beta, act);
     }
 }
 
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
     int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias, int64_t c_size,
-    float beta) {
+    float beta, int act) {
     constexpr int U = NB == 1 ? 16 : (NB <= 4 ? 8 : 4);
     const int lane = threadIdx.x & 63;
     const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kWaves + (int)(threadIdx.x >> 6));
@@ -285,7 +290,7 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
         for (int c = 1; c < NB; ++c)
             if (lane == c) v = acc[c];
         const int64_t f = (int64_t)row * ldy_r + (int64_t)lane * ldy_c;
-        Y[f] = bias_add(v, f, bias, c_size, beta);
+        Y[f] = bias_add(v, f, bias, c_size, beta, act);
     }
 }
 
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_sell(
     int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ soff, const int4* __restrict__ blk, const float* __restrict__ X,
     int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, int yvec,
-    const float* __restrict__ bias, int64_t c_size, float beta) {
+    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
     extern __shared__ float4 xs[];  // [(kc + 1) * 4]: kc rows of 16 floats, then a zero row
     constexpr int NT = 64 * W;
     const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, q = lane & 3;
@@ -429,6 +434,12 @@ __global__ __launch_bounds__(64 * W) void k_spmm_sell(
         if (row >= 0 && cn < N) {
             float* yr = Y + (int64_t)row * ldy_r;
             if (yvec && cn + 3 < N) {
+                if (act == PFR_ACT_RELU) {
+                    a0 = (0.0f < a0) ? a0 : 0.0f;
+                    a1 = (0.0f < a1) ? a1 : 0.0f;
+                    a2 = (0.0f < a2) ? a2 : 0.0f;
+                    a3 = (0.0f < a3) ? a3 : 0.0f;
+                }
                 *reinterpret_cast<float4*>(yr + cn) = make_float4(a0, a1, a2, a3);
             } else {
                 const float a[4] = {a0, a1, a2, a3};
@@ -436,7 +447,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_sell(
                 for (int i = 0; i < 4; ++i)
                     if (cn + i < N) {
                         const int64_t f = (int64_t)row * ldy_r + (int64_t)(cn + i) * ldy_c;
-                        Y[f] = bias_add(a[i], f, bias, c_size, beta);
+                        Y[f] = bias_add(a[i], f, bias, c_size, beta, act);
                     }
             }
         }
@@ -455,7 +466,7 @@ int next_pow2(int n) {
 // Column-slice kernel launch; false when the weight has no sliced-ELL copy.
 template <bool FAST, bool XVEC, int W>
 void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta) {
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
     auto kern = k_spmm_sell<FAST, XVEC, W>;
     const size_t lds = (size_t)(Wt->sell_kc + 1) * 64;
     // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
@@ -469,39 +480,39 @@ void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
     dim3 grid((unsigned)((Wt->sell_nslab + W - 1) / W), (unsigned)((N + pfr::kSellCols - 1) / pfr::kSellCols));
     hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, ctx->stream, N, (int)Wt->K, Wt->sell_kc, Wt->sell_nch,
                        Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, Wt->sell_blk, X, ldx, Y, ldy_r, ldy_c, yvec,
-                       bias, c_size, beta);
+                       bias, c_size, beta, act);
 }
 
 template <bool FAST, bool XVEC>
 void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta) {
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
     // 16 waves per workgroup when that still gives a workgroup per CU,
     // otherwise smaller workgroups to spread the slabs over more CUs
     const int64_t slices = (N + pfr::kSellCols - 1) / pfr::kSellCols;
     const int64_t wg16 = (Wt->sell_nslab + 15) / 16 * slices;
     if (wg16 >= ctx->num_cu)
-        launch_sell_w<FAST, XVEC, 16>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        launch_sell_w<FAST, XVEC, 16>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
     else
-        launch_sell_w<FAST, XVEC, 4>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        launch_sell_w<FAST, XVEC, 4>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
 }
 
 void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, bool fast) {
+                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, bool fast, int act) {
     const bool xvec = (ldx % 4 == 0) && (N % 4 == 0) && aligned16(X);
     const int yvec = (ldy_c == 1 && ldy_r % 4 == 0 && aligned16(Y) && bias == nullptr) ? 1 : 0;
     if (fast) {
-        if (xvec) launch_sell_x<true, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
-        else launch_sell_x<true, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        if (xvec) launch_sell_x<true, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
+        else launch_sell_x<true, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
     } else {
-        if (xvec) launch_sell_x<false, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
-        else launch_sell_x<false, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta);
+        if (xvec) launch_sell_x<false, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
+        else launch_sell_x<false, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
     }
 }
 
 // Row, small-N and vector kernels for one value type.
 template <bool FAST, bool I8>
 void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
-                        int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta) {
+                        int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
     const int M = (int)W->M;
     hipStream_t s = ctx->stream;
     const void* val = W->val;
@@ -511,19 +522,19 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
         const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);
         if (N == 1)
             hipLaunchKernelGGL((k_spmv_fast<1, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else if (N <= 4)
             hipLaunchKernelGGL((k_spmv_fast<4, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else if (xv)
             hipLaunchKernelGGL((k_spmv_fast<8, I8, true>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else
             hipLaunchKernelGGL((k_spmv_fast<8, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else if (N == 1) {
         hipLaunchKernelGGL(k_spmv_wg<I8>, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
-                           W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta);
+                           W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta, act);
     } else if (N < 64) {
         const int np = next_pow2((int)N);
         const int rows_per_block = kWaves * (64 / np);
@@ -531,7 +542,7 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
 #define PFR_SMALL(NPV)                                                                                \
     case NPV:                                                                                         \
         hipLaunchKernelGGL((k_spmm_small<NPV, FAST, I8>), dim3(grid), dim3(256), 0, s, M, (int)N,   \
-                           W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta); \
+                           W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act); \
         break;
         switch (np) {
             PFR_SMALL(2)
@@ -550,27 +561,27 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
                          aligned16(X) && aligned16(Y);
         if (vec)
             hipLaunchKernelGGL((k_spmm_rows<FAST, true, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
-                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else
             hipLaunchKernelGGL((k_spmm_rows<FAST, false, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
-                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     }
 }
 
 // Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
 void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
                  int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
-                 bool fast) {
+                 bool fast, int act) {
     if (W->M == 0 || N == 0) return;
     const bool i8 = W->vdt == PFR_I8;
     if (!i8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535) {
-        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast);
+        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast, act);
     } else if (i8) {
-        if (fast) launch_csr_kernels<true, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-        else launch_csr_kernels<false, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        if (fast) launch_csr_kernels<true, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        else launch_csr_kernels<false, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else {
-        if (fast) launch_csr_kernels<true, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
-        else launch_csr_kernels<false, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta);
+        if (fast) launch_csr_kernels<true, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        else launch_csr_kernels<false, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     }
     PFR_HIP(hipGetLastError());
 }
@@ -581,19 +592,26 @@ void check_csr(const pfr_csr* W) {
         throw pfr::Error(PFR_ERR_UNSUPPORTED, "CSR values must be float32 or int8");
 }
 
+void check_act(int act) {
+    pfr::require(act == PFR_ACT_NONE || act == PFR_ACT_RELU, "unknown activation");
+}
+
 void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
-              int64_t ldy, int mode) {
+              int64_t ldy, int mode, int act = PFR_ACT_NONE) {
     check_csr(W);
     pfr::require(N >= 0 && N < INT32_MAX, "bad column count");
     pfr::require(ldx >= N && ldy >= N, "leading dimension smaller than N");
     pfr::require(mode == PFR_MODE_STRICT || mode == PFR_MODE_FAST, "unknown mode");
     pfr::require((X && Y) || W->M * N == 0, "null X/Y");
-    launch_spmm(ctx, W, X, N, ldx, Y, ldy, 1, nullptr, 0, 0.0f, mode == PFR_MODE_FAST);
+    check_act(act);
+    launch_spmm(ctx, W, X, N, ldx, Y, ldy, 1, nullptr, 0, 0.0f, mode == PFR_MODE_FAST, act);
 }
 
 void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, const pfr_csr* BT,
-              float alpha, float beta, const float* C, int64_t c_size, float* Y, int mode) {
+              float alpha, float beta, const float* C, int64_t c_size, float* Y, int mode,
+              int act = PFR_ACT_NONE) {
     check_csr(BT);
+    check_act(act);
     pfr::require(Mb >= 0 && Mb < INT32_MAX, "bad row count");
     pfr::require(BT->K == K, "Gemm: incompatible dimensions - A has K=" + std::to_string(K) +
                                  ", B has K=" + std::to_string(BT->K));
@@ -627,7 +645,7 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     }
     // Output (feature j, batch i) -> Y[i * Nf + j]: the flat index the bias
     // modulo uses in cpu_gemm.
-    launch_spmm(ctx, BT, At, Mb, Mb, Y, 1, Nf, C, c_size, beta, mode == PFR_MODE_FAST);
+    launch_spmm(ctx, BT, At, Mb, Mb, Y, 1, Nf, C, c_size, beta, mode == PFR_MODE_FAST, act);
 }
 
 }  // namespace
@@ -666,6 +684,23 @@ int pfr_gemm_csr_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int tr
     return pfr::guarded([&] {
         pfr::bind(ctx);
         gemm_dev(ctx, A, Mb, K, transA, BT, alpha, beta, C, c_size, Y, mode);
+    });
+}
+
+int pfr_spmm_csr_act_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx,
+                         float* Y, int64_t ldy, int mode, int act) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        spmm_dev(ctx, W, X, N, ldx, Y, ldy, mode, act);
+    });
+}
+
+int pfr_gemm_csr_act_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA,
+                         const pfr_csr* BT, float alpha, float beta, const float* C, int64_t c_size,
+                         float* Y, int mode, int act) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        gemm_dev(ctx, A, Mb, K, transA, BT, alpha, beta, C, c_size, Y, mode, act);
     });
 }
 

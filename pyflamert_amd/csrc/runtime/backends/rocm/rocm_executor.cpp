@@ -1,5 +1,6 @@
 #include "rocm_executor.hpp"
 
+#include <algorithm>
 #include <stdexcept>
 #include <unordered_set>
 
@@ -17,6 +18,26 @@ struct CurrentGuard {
 };
 
 bool is_f32_matrix(const Tensor& t) { return t.dtype() == DType::Float32 && t.ndim() == 2; }
+
+int64_t numel(const std::vector<int64_t>& shape) {
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    return n;
+}
+
+void need_f32(DType d, const char* what) {
+    if (d != DType::Float32) throw std::invalid_argument(std::string(what) + " must be float32, got " + dtype_name(d));
+}
+
+// Waits for the context's stream when a plan run leaves early, so that no
+// queued copy still reads a host input after execute returns.
+struct StreamDrain {
+    pfr_ctx* ctx;
+    bool armed = true;
+    ~StreamDrain() {
+        if (armed) pfr_synchronize(ctx);
+    }
+};
 }  // namespace
 
 void pfr_check(int status) {
@@ -26,8 +47,8 @@ void pfr_check(int status) {
     throw std::runtime_error(msg);
 }
 
-RocmExecutor::RocmExecutor(int device, bool strict_math_mode, int math_mode)
-    : strict_math_mode_(strict_math_mode), math_mode_(math_mode) {
+RocmExecutor::RocmExecutor(int device, bool strict_math_mode, int math_mode, OptLevel opt)
+    : strict_math_mode_(strict_math_mode), math_mode_(math_mode), opt_(opt) {
     const int st = pfr_rocm_init(device, &ctx_);
     if (st != PFR_OK) throw BackendError(std::string("cannot initialise ROCm device: ") + pfr_last_error());
 }
@@ -43,7 +64,27 @@ void RocmExecutor::release_weights() {
         if (kv.second.sp24) pfr_sp24_free(kv.second.sp24);
     }
     weights_.clear();
+    for (auto& kv : constants_) pfr_dev_free(ctx_, kv.second.p);
+    constants_.clear();
+    for (auto& kv : bufs_) pfr_dev_free(ctx_, kv.second.p);
+    bufs_.clear();
+    plan_.clear();
+    fused_away_.clear();
+    plan_ok_ = false;
     prepared_for_ = nullptr;
+}
+
+void* RocmExecutor::device_buffer(const std::string& name, int64_t bytes) {
+    DevBuf& b = bufs_[name];
+    const int64_t need = std::max<int64_t>(bytes, 256);
+    if (b.cap < need) {
+        if (b.p) pfr_check(pfr_dev_free(ctx_, b.p));
+        b.p = nullptr;
+        b.cap = 0;
+        pfr_check(pfr_dev_alloc(ctx_, need, &b.p));
+        b.cap = need;
+    }
+    return b.p;
 }
 
 RocmExecutor* RocmExecutor::current() { return t_current; }
@@ -111,7 +152,285 @@ void RocmExecutor::prepare(const Graph& graph) {
         }
         if (w.kind != DeviceWeight::None) weights_[n.get()] = w;
     }
+    build_plan(graph);
     prepared_for_ = &graph;
+}
+
+// The device-resident plan: one step per node in topological order, each a
+// device entry point; a product whose output feeds exactly one node, a Relu,
+// and is not a graph output takes that Relu into its epilogue (PFR_ACT_RELU;
+// the Relu then runs at the product's position, which its single input
+// allows).  Any node without a device kernel leaves plan_ok_ false.
+void RocmExecutor::build_plan(const Graph& graph) {
+    plan_.clear();
+    fused_away_.clear();
+    plan_ok_ = false;
+    if (opt_ == OptLevel::None) return;
+    const auto order = graph.topological_sort();
+    std::unordered_map<std::string, int> uses;
+    for (const auto& n : order)
+        for (const auto& nm : n->inputs()) ++uses[nm];
+    std::unordered_set<std::string> graph_outs;
+    for (const auto& o : graph.outputs()) graph_outs.insert(o.name);
+
+    std::vector<PlanStep> steps;
+    for (const auto& np : order) {
+        const Node* n = np.get();
+        if (n->outputs().size() != 1) return;
+        const DeviceWeight* w = weight(n);
+        const std::string& op = n->op_type();
+        PlanStep st{PlanStep::Relu, n, false, n->outputs()[0]};
+        if (op == "Gemm" && w && w->kind == DeviceWeight::CsrB)
+            st.op = PlanStep::Gemm;
+        else if (op == "MatMul" && w && w->kind == DeviceWeight::CsrB)
+            st.op = PlanStep::MatMulB;
+        else if (op == "MatMul" && w && w->kind == DeviceWeight::CsrA)
+            st.op = PlanStep::MatMulA;
+        else if (op == "QuantizedMatMul" && w && w->kind == DeviceWeight::Sp24A)
+            st.op = PlanStep::QMatMul;
+        else if (op == "Relu" && n->inputs().size() == 1)
+            st.op = PlanStep::Relu;
+        else if (op == "Softmax" && n->inputs().size() == 1)
+            st.op = PlanStep::Softmax;
+        else
+            return;
+        steps.push_back(st);
+    }
+
+    std::vector<bool> dropped(steps.size(), false);
+    for (auto& st : steps) {
+        if (opt_ == OptLevel::Basic) break;
+        if (st.op != PlanStep::Gemm && st.op != PlanStep::MatMulB && st.op != PlanStep::MatMulA) continue;
+        const std::string prod = st.out;
+        if (uses[prod] != 1 || graph_outs.count(prod)) continue;
+        for (size_t j = 0; j < steps.size(); ++j) {
+            if (dropped[j] || steps[j].op != PlanStep::Relu || steps[j].node->inputs()[0] != prod) continue;
+            st.fuse_relu = true;
+            st.out = steps[j].out;
+            dropped[j] = true;
+            fused_away_.insert(prod);
+            break;
+        }
+    }
+
+    // Initializers a step reads as an activation (biases, or a constant
+    // operand of Relu/Softmax) go to the device once; the pruned operand of a
+    // product is already a device weight.
+    for (size_t i = 0; i < steps.size(); ++i) {
+        if (dropped[i]) continue;
+        const PlanStep& st = steps[i];
+        const auto& in = st.node->inputs();
+        const int weight_slot = (st.op == PlanStep::Gemm || st.op == PlanStep::MatMulB)   ? 1
+                                : (st.op == PlanStep::MatMulA || st.op == PlanStep::QMatMul) ? 0
+                                                                                             : -1;
+        for (size_t k = 0; k < in.size(); ++k) {
+            if ((int)k == weight_slot || constants_.count(in[k])) continue;
+            auto t = graph.get_initializer(in[k]);
+            if (!t) continue;
+            const Tensor& src = t->get();
+            DevTensor d;
+            d.shape = src.shape();
+            d.dtype = src.dtype();
+            const int64_t bytes = (int64_t)src.size_bytes();
+            pfr_check(pfr_dev_alloc(ctx_, std::max<int64_t>(bytes, 256), &d.p));
+            constants_[in[k]] = d;
+            if (bytes) pfr_check(pfr_copy_to_device(ctx_, d.p, src.data(), bytes));
+        }
+        plan_.push_back(st);
+    }
+    pfr_check(pfr_synchronize(ctx_));
+    plan_ok_ = true;
+}
+
+// Runs the plan: graph inputs to the device, every step on the context's
+// stream with no host round trip, requested outputs back.  Shape and dtype
+// checks and their texts are those of the rocm:: OpFuncs.
+std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
+                                               const std::unordered_map<std::string, Tensor>& input_feed,
+                                               const std::vector<std::string>& names) {
+    StreamDrain drain{ctx_};
+    std::unordered_map<std::string, DevTensor> live(constants_);
+    for (const auto& kv : input_feed) {
+        const Tensor& t = kv.second;
+        const int64_t bytes = (int64_t)t.size_bytes();
+        DevTensor d;
+        d.p = device_buffer(kv.first, bytes);
+        d.shape = t.shape();
+        d.dtype = t.dtype();
+        if (bytes) pfr_check(pfr_copy_to_device(ctx_, d.p, t.data(), bytes));
+        live[kv.first] = d;
+    }
+
+    for (const PlanStep& st : plan_) {
+        const Node* n = st.node;
+        const auto& in = n->inputs();
+        auto act_in = [&](size_t i) -> const DevTensor& {
+            auto it = live.find(in[i]);
+            if (it == live.end()) throw BackendError("Input tensor '" + in[i] + "' not found", n->name());
+            return it->second;
+        };
+        auto init_in = [&](size_t i) -> const Tensor& { return graph.get_initializer(in[i])->get(); };
+        auto need_inputs = [&](size_t k, const char* op) {
+            if (in.size() < k)
+                throw std::invalid_argument(std::string(op) + ": expected at least " + std::to_string(k) +
+                                            " inputs, got " + std::to_string(in.size()));
+        };
+        const int act = st.fuse_relu ? PFR_ACT_RELU : PFR_ACT_NONE;
+        DevTensor out;
+        out.dtype = DType::Float32;
+        try {
+            switch (st.op) {
+            case PlanStep::Gemm: {
+                // math.cpp:377-438; the same checks as rocm::Gemm.
+                need_inputs(2, "Gemm");
+                const DevTensor& A = act_in(0);
+                const Tensor& B = init_in(1);
+                const DevTensor* C = in.size() > 2 ? &act_in(2) : nullptr;
+                if (A.shape.size() < 2 || B.ndim() < 2)
+                    throw std::invalid_argument("Gemm input A/B must have at least 2 dimensions");
+                need_f32(A.dtype, "Gemm input A");
+                const float alpha = n->get_attr<float>("alpha", 1.0f);
+                const float beta = n->get_attr<float>("beta", 1.0f);
+                const int64_t ta = n->get_attr<int64_t>("transA", 0);
+                const int64_t tb = n->get_attr<int64_t>("transB", 0);
+                const int64_t M = ta ? A.shape[1] : A.shape[0];
+                const int64_t Ka = ta ? A.shape[0] : A.shape[1];
+                const int64_t Kb = tb ? B.shape()[1] : B.shape()[0];
+                const int64_t N = tb ? B.shape()[0] : B.shape()[1];
+                if (Ka != Kb)
+                    throw std::invalid_argument("Gemm: incompatible dimensions - A has K=" + std::to_string(Ka) +
+                                                ", B has K=" + std::to_string(Kb));
+                const float* c = nullptr;
+                int64_t c_size = 0;
+                if (C && numel(C->shape) > 0) {
+                    need_f32(C->dtype, "Gemm input C");
+                    c = static_cast<const float*>(C->p);
+                    c_size = numel(C->shape);
+                }
+                out.shape = {M, N};
+                out.p = device_buffer(st.out, M * N * 4);
+                pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), M, Ka, (int)ta,
+                                               weight(n)->csr, alpha, beta, c, c_size, static_cast<float*>(out.p),
+                                               math_mode_, act));
+                break;
+            }
+            case PlanStep::MatMulB:
+            case PlanStep::MatMulA: {
+                // math.cpp:268-374; the same checks as rocm::MatMul.
+                need_inputs(2, "MatMul");
+                const bool wb = st.op == PlanStep::MatMulB;
+                const std::vector<int64_t> as = wb ? act_in(0).shape : init_in(0).shape();
+                const std::vector<int64_t> bs = wb ? init_in(1).shape() : act_in(1).shape;
+                if (as.size() < 2 || bs.size() < 2)
+                    throw std::invalid_argument("MatMul: inputs must have at least 2 dimensions");
+                const int64_t Ka = as.back(), Kb = bs[bs.size() - 2];
+                if (Ka != Kb)
+                    throw std::invalid_argument("MatMul: incompatible dimensions - A has inner dim " +
+                                                std::to_string(Ka) + ", B has inner dim " + std::to_string(Kb));
+                if (wb) {
+                    const DevTensor& A = act_in(0);
+                    need_f32(A.dtype, "MatMul input A");
+                    const int64_t N = bs[1];
+                    out.shape.assign(as.begin(), as.end() - 1);
+                    const int64_t rows = numel(out.shape);
+                    out.shape.push_back(N);
+                    out.p = device_buffer(st.out, rows * N * 4);
+                    pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), rows, Ka, 0, weight(n)->csr,
+                                                   1.0f, 1.0f, nullptr, 0, static_cast<float*>(out.p), math_mode_,
+                                                   act));
+                } else {
+                    const DevTensor& B = act_in(1);
+                    need_f32(B.dtype, "MatMul input B");
+                    if (bs.size() != 2)
+                        throw std::invalid_argument("MatMul: a pruned first operand needs a 2-D second operand");
+                    const int64_t M = as[0], N = bs[1];
+                    out.shape = {M, N};
+                    out.p = device_buffer(st.out, M * N * 4);
+                    pfr_check(pfr_spmm_csr_act_dev(ctx_, weight(n)->csr, static_cast<const float*>(B.p), N, N,
+                                                   static_cast<float*>(out.p), N, math_mode_, act));
+                }
+                break;
+            }
+            case PlanStep::QMatMul: {
+                // quantized_ops.cpp:77-167; the same checks as rocm::QuantizedMatMul.
+                need_inputs(2, "QuantizedMatMul");
+                const Tensor& a = init_in(0);
+                const DevTensor& b = act_in(1);
+                if (b.dtype != DType::Int8 && b.dtype != DType::UInt8)
+                    throw std::invalid_argument("QuantizedMatMul: input B must be Int8 or UInt8");
+                if (b.shape.size() < 2)
+                    throw std::invalid_argument("QuantizedMatMul: inputs must have at least 2 dimensions");
+                const int64_t K = a.shape().back(), Kb = b.shape[b.shape.size() - 2];
+                if (K != Kb)
+                    throw std::invalid_argument("QuantizedMatMul: inner dimensions must match (got " +
+                                                std::to_string(K) + " and " + std::to_string(Kb) + ")");
+                if (b.shape.size() != 2)
+                    throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D int8 initializer A that "
+                                             "is 2:4 sparse along K, zero points 0, and a 2-D B");
+                const float b_scale = n->get_attr<float>("b_scale", 1.0f);
+                const int64_t M = a.shape()[0], N = b.shape[1];
+                out.shape = {M, N};
+                out.p = device_buffer(st.out, M * N * 4);
+                pfr_check(pfr_sp24_gemm_i8_dev(ctx_, weight(n)->sp24, static_cast<const int8_t*>(b.p), N, N, b_scale,
+                                               PFR_SP24_OUT_F32, 1.0f, 0, out.p, N));
+                break;
+            }
+            case PlanStep::Relu: {
+                // activation.cpp:45-60.
+                const DevTensor& x = act_in(0);
+                need_f32(x.dtype, "Relu input");
+                out.shape = x.shape;
+                out.p = device_buffer(st.out, numel(x.shape) * 4);
+                pfr_check(pfr_relu_dev(ctx_, static_cast<const float*>(x.p), numel(x.shape),
+                                       static_cast<float*>(out.p)));
+                break;
+            }
+            case PlanStep::Softmax: {
+                // activation.cpp:157-237.
+                const DevTensor& x = act_in(0);
+                need_f32(x.dtype, "Softmax input");
+                int64_t axis = n->get_attr<int64_t>("axis", -1);
+                const int64_t nd = (int64_t)x.shape.size();
+                if (axis < -nd || axis >= nd)
+                    throw std::invalid_argument("Softmax: axis " + std::to_string(axis) + " out of range for " +
+                                                std::to_string(nd) + "-D input");
+                if (axis < 0) axis += nd;
+                int64_t outer = 1, inner = 1;
+                for (int64_t i = 0; i < axis; ++i) outer *= x.shape[i];
+                for (int64_t i = axis + 1; i < nd; ++i) inner *= x.shape[i];
+                out.shape = x.shape;
+                out.p = device_buffer(st.out, numel(x.shape) * 4);
+                pfr_check(pfr_softmax_dev(ctx_, static_cast<const float*>(x.p), outer, x.shape[axis], inner,
+                                          static_cast<float*>(out.p)));
+                break;
+            }
+            }
+        } catch (const BackendError&) {
+            throw;
+        } catch (const std::exception& e) {
+            throw BackendError(e.what(), n->name());
+        }
+        live[st.out] = out;
+    }
+
+    std::vector<Tensor> results;
+    results.reserve(names.size());
+    for (const auto& nm : names) {
+        auto it = live.find(nm);
+        if (it == live.end()) throw BackendError("Output tensor '" + nm + "' not found");
+        const DevTensor& d = it->second;
+        Tensor t(d.shape, d.dtype);
+        const int64_t bytes = (int64_t)t.size_bytes();
+        try {
+            if (bytes) pfr_check(pfr_copy_to_host(ctx_, t.data(), d.p, bytes));
+        } catch (const std::exception& e) {
+            throw BackendError(e.what());
+        }
+        results.push_back(std::move(t));
+    }
+    pfr_check(pfr_synchronize(ctx_));
+    drain.armed = false;
+    return results;
 }
 
 std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unordered_map<std::string, Tensor>& input_feed,
@@ -119,6 +438,15 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
     validate_inputs(graph, input_feed);
     prepare(graph);
     CurrentGuard guard(this);
+    std::vector<std::string> names = output_names;
+    if (names.empty())
+        for (const auto& o : graph.outputs()) names.push_back(o.name);
+    bool on_device = plan_ok_;
+    for (const auto& nm : names)
+        if (fused_away_.count(nm)) on_device = false;  // an intermediate the fused plan never writes
+    last_on_device_ = on_device;
+    if (on_device) return execute_plan(graph, input_feed, names);
+
     std::unordered_map<std::string, const Tensor*> view;
     std::unordered_map<std::string, Tensor> produced;
     for (const auto& kv : input_feed) view[kv.first] = &kv.second;
@@ -152,9 +480,6 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
             view[nm] = &produced[nm];
         }
     }
-    std::vector<std::string> names = output_names;
-    if (names.empty())
-        for (const auto& o : graph.outputs()) names.push_back(o.name);
     std::vector<Tensor> results;
     for (const auto& nm : names) {
         auto it = produced.find(nm);

@@ -9,12 +9,23 @@
 //    are converted once, on the first run of a graph, into device-resident
 //    CSR or 2:4-compressed operands kept by the executor per node; the rocm
 //    kernels find them through RocmExecutor::current();
-//  * inputs and initializers are not deep-copied on every run.
+//  * inputs and initializers are not deep-copied on every run;
+//  * from OptLevel::Basic up, a graph whose every node has a device kernel
+//    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, Relu, Softmax) runs as a
+//    device-resident plan:
+//    graph inputs are copied to the GPU once per run, the remaining
+//    initializers once per graph, activations stay in device buffers
+//    between nodes, from OptLevel::Extended up a Gemm/MatMul whose only
+//    consumer is a Relu runs with the Relu fused into its epilogue (the
+//    reference's Extended level adds operator fusion, types.hpp:119-124), and
+//    only the requested outputs come back to the host.  Other graphs, and
+//    OptLevel::None, run node by node through the host OpFuncs.
 #pragma once
 
 #include <memory>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "pfr_rocm.h"
 #include "pyflame_rt/backend.hpp"
@@ -30,7 +41,10 @@ public:
         pfr_sp24* sp24 = nullptr;  // Sp24A: 2:4-compressed int8 A
     };
 
-    explicit RocmExecutor(int device = 0, bool strict_math_mode = false, int math_mode = PFR_MODE_STRICT);
+    // opt: None runs node by node through the OpFuncs; Basic adds the
+    // device-resident plan; Extended and All also fuse Relu into products.
+    explicit RocmExecutor(int device = 0, bool strict_math_mode = false, int math_mode = PFR_MODE_STRICT,
+                          OptLevel opt = OptLevel::Extended);
     ~RocmExecutor() override;
 
     const std::string& name() const override { return name_; }
@@ -44,17 +58,50 @@ public:
     pfr_ctx* ctx() const { return ctx_; }
     int math_mode() const { return math_mode_; }
     const DeviceWeight* weight(const Node* node) const;
+    // True when the last run went through the device-resident plan.
+    bool device_plan() const { return last_on_device_; }
+    // Kernel launches of the plan (a fused pair counts once).
+    size_t device_plan_steps() const { return plan_.size(); }
 
 private:
+    // One kernel launch of the device plan.
+    struct PlanStep {
+        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax } op;
+        const Node* node;
+        bool fuse_relu = false;  // the following Relu runs in this step's epilogue
+        std::string out;         // tensor the step writes (the Relu's output when fused)
+    };
+    // A tensor held in device memory while a plan runs.
+    struct DevTensor {
+        void* p = nullptr;
+        std::vector<int64_t> shape;
+        DType dtype = DType::Float32;
+    };
+    struct DevBuf {
+        void* p = nullptr;
+        int64_t cap = 0;
+    };
+
     void prepare(const Graph& graph);
+    void build_plan(const Graph& graph);
     void release_weights();
+    void* device_buffer(const std::string& name, int64_t bytes);
+    std::vector<Tensor> execute_plan(const Graph& graph, const std::unordered_map<std::string, Tensor>& input_feed,
+                                     const std::vector<std::string>& names);
 
     std::string name_ = "rocm";
     pfr_ctx* ctx_ = nullptr;
     bool strict_math_mode_;
     int math_mode_;
+    OptLevel opt_;
     const Graph* prepared_for_ = nullptr;
     std::unordered_map<const Node*, DeviceWeight> weights_;
+    bool plan_ok_ = false;
+    bool last_on_device_ = false;
+    std::vector<PlanStep> plan_;
+    std::unordered_set<std::string> fused_away_;           // product outputs a fused Relu consumes
+    std::unordered_map<std::string, DevTensor> constants_;  // non-weight initializers, uploaded once
+    std::unordered_map<std::string, DevBuf> bufs_;          // graph inputs and activations, by name
 };
 
 // Throws the C ABI's last error as std::invalid_argument / std::runtime_error.

@@ -8,6 +8,7 @@
 #include "pyflame_rt/errors.hpp"
 #include "pyflame_rt/pyflame_format.hpp"
 #include "pyflame_rt/session.hpp"
+#include "../backends/rocm/rocm_executor.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -65,7 +66,7 @@ extern "C" {
 const char* pfr_session_last_error(void) { return g_err.c_str(); }
 
 int pfr_session_create(const char* path, const char* device, int strict_math_mode, int math_mode, int device_id,
-                       pfr_session** out) {
+                       int optimization_level, pfr_session** out) {
     return guard([&] {
         if (!out || !path || !device) throw PyFlameRTError("null argument");
         *out = nullptr;
@@ -74,6 +75,10 @@ int pfr_session_create(const char* path, const char* device, int strict_math_mod
         o.strict_math_mode = strict_math_mode != 0;
         o.rocm_math_mode = math_mode;
         o.rocm_device_id = device_id;
+        if (optimization_level < 0 || optimization_level > 3)
+            throw PyFlameRTError("optimization_level must be 0 (None) .. 3 (All), got " +
+                                 std::to_string(optimization_level));
+        o.optimization_level = static_cast<OptLevel>(optimization_level);
         auto s = std::make_unique<pfr_session>();
         s->sess = std::make_unique<InferenceSession>(path, o);
         *out = s.release();
@@ -265,6 +270,15 @@ int pfr_session_supported_ops(pfr_session* s, char* buf, int64_t cap) {
         const size_t n = std::min((size_t)cap - 1, r.size());
         std::memcpy(buf, r.data(), n);
         buf[n] = '\0';
+    });
+}
+
+int pfr_session_device_plan(pfr_session* s, int* device_resident, int* steps) {
+    return guard([&] {
+        if (!s || !device_resident || !steps) throw PyFlameRTError("null argument");
+        auto* ex = dynamic_cast<RocmExecutor*>(&s->sess->backend());
+        *device_resident = ex && ex->device_plan() ? 1 : 0;
+        *steps = *device_resident ? (int)ex->device_plan_steps() : 0;
     });
 }
 

@@ -28,7 +28,7 @@ InferenceSession::InferenceSession(const std::string& model_path, SessionOptions
         throw PyFlameRTError("Device '" + options_.device +
                              "' is not provided by this runtime; it runs device='rocm' (MI355X)");
     backend_ = std::make_unique<RocmExecutor>(options_.rocm_device_id, options_.strict_math_mode,
-                                              options_.rocm_math_mode);
+                                              options_.rocm_math_mode, options_.optimization_level);
 }
 
 InferenceSession::~InferenceSession() = default;

@@ -119,9 +119,13 @@ class Context:
         return Y
 
     def gemm_csr_dev(self, A_ptr, Mb, K, BT, Y_ptr, alpha=1.0, beta=1.0, C_ptr=None, c_size=0,
-                     transA=False, mode="strict"):
-        check(self._lib.pfr_gemm_csr_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
-                                         alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode]))
+                     transA=False, mode="strict", relu=False):
+        if relu:
+            check(self._lib.pfr_gemm_csr_act_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
+                                                 alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode], _lib.ACT_RELU))
+        else:
+            check(self._lib.pfr_gemm_csr_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
+                                             alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode]))
 
 
 class CsrWeight:
@@ -157,9 +161,13 @@ class CsrWeight:
         check(self.ctx._lib.pfr_spmm_csr(self.ctx.handle, self.handle, _ptr(X), N, _ptr(Y), _MODES[mode]))
         return Y
 
-    def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict"):
-        check(self.ctx._lib.pfr_spmm_csr_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
-                                             ldy or N, _MODES[mode]))
+    def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict", relu=False):
+        if relu:
+            check(self.ctx._lib.pfr_spmm_csr_act_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
+                                                     ldy or N, _MODES[mode], _lib.ACT_RELU))
+        else:
+            check(self.ctx._lib.pfr_spmm_csr_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
+                                                 ldy or N, _MODES[mode]))
 
 
 _SP24_OUT = {"i32": SP24_OUT_I32, "f32": SP24_OUT_F32, "i8": SP24_OUT_I8}

@@ -22,13 +22,14 @@ _I64 = C.c_int64
 _INT = C.c_int
 _SIGS = {
     "pfr_session_last_error": (C.c_char_p, []),
-    "pfr_session_create": (_INT, [C.c_char_p, C.c_char_p, _INT, _INT, _INT, C.POINTER(_P)]),
+    "pfr_session_create": (_INT, [C.c_char_p, C.c_char_p, _INT, _INT, _INT, _INT, C.POINTER(_P)]),
     "pfr_session_destroy": (_INT, [_P]),
     "pfr_session_io_count": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT)]),
     "pfr_session_io_info": (_INT, [_P, _INT, _INT, C.POINTER(C.c_char_p), C.POINTER(_INT), _P, C.POINTER(_INT)]),
     "pfr_session_run": (_INT, [_P, _INT, _P, _P, _P, _P, _P, _INT, _P, C.POINTER(_INT)]),
     "pfr_session_result": (_INT, [_P, _INT, C.POINTER(_INT), _P, C.POINTER(_INT), C.POINTER(_P)]),
     "pfr_session_supported_ops": (_INT, [_P, C.c_char_p, _I64]),
+    "pfr_session_device_plan": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT)]),
     "pfr_model_describe": (_INT, [C.c_char_p, C.c_char_p, _I64, C.POINTER(_I64)]),
     "pfr_model_resave": (_INT, [C.c_char_p, C.c_char_p]),
 }
@@ -96,6 +97,10 @@ class SessionOptions:
     strict_math_mode: bool = False
     math_mode: str = "strict"    # "strict": bit-exact fp32 sums; "fast": FMA
     device_id: int = 0
+    # OptLevel (types.hpp:119-124): 0 None = node by node through the host
+    # OpFuncs, 1 Basic = device-resident plan, 2 Extended (default) and 3 All
+    # = plan + Relu fused into the pruned product before it
+    optimization_level: int = 2
 
 
 @dataclass
@@ -125,7 +130,8 @@ class InferenceSession:
         h = _P()
         mode = {"strict": 0, "fast": 1}[options.math_mode]
         _check(L.pfr_session_create(str(model_path).encode(), options.device.encode(),
-                                    int(options.strict_math_mode), mode, options.device_id, C.byref(h)))
+                                    int(options.strict_math_mode), mode, options.device_id,
+                                    int(options.optimization_level), C.byref(h)))
         self._h = h
         self._L = L
 
@@ -167,6 +173,14 @@ class InferenceSession:
         _check(self._L.pfr_session_supported_ops(self._h, buf, len(buf)))
         lines = buf.value.decode().split("\n")
         return lines[0], lines[1:]
+
+    def device_plan(self):
+        """(device_resident, kernel_steps) of the last run: whether the graph
+        ran with activations kept on the GPU (Relu fused into a product that
+        feeds only it), and how many launches that plan makes."""
+        res, steps = C.c_int(), C.c_int()
+        _check(self._L.pfr_session_device_plan(self._h, C.byref(res), C.byref(steps)))
+        return bool(res.value), steps.value
 
     def run(self, output_names, input_feed):
         names = list(input_feed)

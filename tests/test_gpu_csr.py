@@ -306,3 +306,78 @@ def test_int8_csr_dequant_fused(ctx):
     Bd[ix, np.repeat(np.arange(1500), np.diff(ip))] = vals
     say("int8 CSR Gemm form")
     assert bits_equal(ctx.gemm_csr(A, W, 1.0, 1.0, bias), O.orc_gemm(A, Bd, bias, 1.0, 1.0))
+
+
+def relu_ref(y):
+    """activation.cpp:45-60: std::max(0.0f, v) = (0 < v) ? v : +0, so -0 and
+    NaN map to +0."""
+    return np.where(y > 0, y, np.float32(0)).astype(np.float32)
+
+
+def test_fused_relu_epilogue(ctx, cfg_weight):
+    """The Relu fused into the product epilogue (PFR_ACT_RELU) equals the
+    product followed by a separate Relu, bit for bit, on every kernel the
+    dispatch picks: the small-N and vector SpMV forms, the row kernels and
+    the column-slice kernel, in both math modes; infinities and NaNs in the
+    sums included."""
+    import torch
+
+    ip, ix, v = cfg_weight
+    W = ctx.csr_upload(4096, 4096, ip, ix, v)
+    rng = np.random.default_rng(8)
+    for N in (1, 3, 8, 40, 256):
+        X = rng.standard_normal((4096, N)).astype(np.float32)
+        X[0, :] = np.inf
+        X[1, :] = -np.inf
+        dX = torch.from_numpy(X).cuda()
+        dY = torch.empty((4096, N), dtype=torch.float32, device="cuda")
+        for mode in ("strict", "fast"):
+            say(f"fused relu spmm N={N} {mode}")
+            W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode)
+            ctx.synchronize()
+            plain = dY.cpu().numpy()
+            W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode, relu=True)
+            ctx.synchronize()
+            fused = dY.cpu().numpy()
+            assert np.isnan(plain).any() and (plain < 0).any()
+            assert bits_equal(fused, relu_ref(plain)), (N, mode, first_diff(fused, relu_ref(plain)))
+            if mode == "strict":
+                ref = O.orc_csr_spmm(4096, 4096, ip, ix, v, X)
+                assert bits_equal(fused, relu_ref(ref)), (N, first_diff(fused, relu_ref(ref)))
+    # Gemm form with bias and beta: Y = relu(alpha * A . B + beta * C)
+    B = np.zeros((600, 700), np.float32)
+    m = rng.random((600, 700)) < 0.2
+    B[m] = rng.standard_normal(int(m.sum())).astype(np.float32) * 0.1
+    BT = ctx.csr_from_dense(B, transpose=True)
+    bias = rng.standard_normal(700).astype(np.float32)
+    dC = torch.from_numpy(bias).cuda()
+    for Mb in (1, 5, 32, 200):
+        A = rng.standard_normal((Mb, 600)).astype(np.float32)
+        dA = torch.from_numpy(A).cuda()
+        dY = torch.empty((Mb, 700), dtype=torch.float32, device="cuda")
+        for mode in ("strict", "fast"):
+            say(f"fused relu gemm Mb={Mb} {mode}")
+            ctx.gemm_csr_dev(dA.data_ptr(), Mb, 600, BT, dY.data_ptr(), 0.5, 2.0, dC.data_ptr(), 700, mode=mode)
+            ctx.synchronize()
+            plain = dY.cpu().numpy()
+            ctx.gemm_csr_dev(dA.data_ptr(), Mb, 600, BT, dY.data_ptr(), 0.5, 2.0, dC.data_ptr(), 700, mode=mode,
+                             relu=True)
+            ctx.synchronize()
+            fused = dY.cpu().numpy()
+            assert bits_equal(fused, relu_ref(plain)), (Mb, mode)
+            if mode == "strict":
+                ref = O.orc_gemm(A, B, bias, 0.5, 2.0)
+                assert bits_equal(fused, relu_ref(ref)), (Mb, first_diff(fused, relu_ref(ref)))
+    # int8 CSR weight (dequantisation and Relu both in the kernel)
+    ip8, ix8, q, sc = workloads.csr_int8_lognormal(900, 1000, 0.2, 0.5, 0.02, seed=3)
+    W8 = ctx.csr_upload(900, 1000, ip8, ix8, q, row_scales=sc)
+    vals = workloads.dequant_rows(ip8, q, sc)
+    for N in (1, 8, 64):
+        X = rng.standard_normal((1000, N)).astype(np.float32)
+        dX = torch.from_numpy(X).cuda()
+        dY = torch.empty((900, N), dtype=torch.float32, device="cuda")
+        say(f"fused relu int8 spmm N={N}")
+        W8.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), relu=True)
+        ctx.synchronize()
+        ref = relu_ref(O.orc_csr_spmm(900, 1000, ip8, ix8, vals, X))
+        assert bits_equal(dY.cpu().numpy(), ref), N

@@ -39,6 +39,8 @@ def test_mlp_against_reference_executor(mlp, golden, tmp_path):
     assert s.get_providers() == ["ROCMExecutionProvider"]
     assert [i.name for i in s.get_inputs()] == ["x"] and s.get_inputs()[0].shape == [32, 784]
     (y,) = s.run(None, {"x": g["x"]})
+    # device-resident plan: Gemm+Relu fused, Gemm, Softmax
+    assert s.device_plan() == (True, 3)
     # Softmax uses the device expf: a few ulp from glibc's
     assert np.abs(y - g["y"]).max() <= 4e-7
     assert np.array_equal(np.argmax(y, 1), np.argmax(g["y"], 1))
@@ -49,8 +51,16 @@ def test_mlp_against_reference_executor(mlp, golden, tmp_path):
     pfm.save(m, p2)
     s2 = session.InferenceSession(p2, session.SessionOptions(device="rocm"))
     y2, h1 = s2.run(["y", "h1"], {"x": g["x"]})
+    assert s2.device_plan() == (True, 4)  # h1 is an output: the Relu runs on its own
     assert np.array_equal(bits(h1), bits(g["h1"]))
     assert np.array_equal(bits(y2), bits(y))
+    # OptLevel None: node by node through the host OpFuncs; Basic: the
+    # device-resident plan without fusion.  Same bits either way.
+    for lvl, plan in ((0, (False, 0)), (1, (True, 4))):
+        sl = session.InferenceSession(mlp, session.SessionOptions(device="rocm", optimization_level=lvl))
+        (yl,) = sl.run(None, {"x": g["x"]})
+        assert sl.device_plan() == plan, lvl
+        assert np.array_equal(bits(yl), bits(y)), lvl
     # relu and the second Gemm exactly as the oracle computes them from h1
     a1 = O.orc_relu(h1)
     w2, b2 = m["initializers"]["fc2.weight"], m["initializers"]["fc2.bias"]
@@ -60,6 +70,9 @@ def test_mlp_against_reference_executor(mlp, golden, tmp_path):
     s3 = session.InferenceSession(mlp, session.SessionOptions(device="rocm", math_mode="fast"))
     (y3,) = s3.run(None, {"x": g["x"]})
     assert np.abs(y3 - g["y"]).max() <= 1e-5
+    s4 = session.InferenceSession(mlp, session.SessionOptions(device="rocm", math_mode="fast", optimization_level=0))
+    (y4,) = s4.run(None, {"x": g["x"]})
+    assert np.array_equal(bits(y4), bits(y3))
 
 
 def test_kat_and_batched_matmul(tmp_path, golden):
@@ -107,6 +120,81 @@ def test_quantized_matmul_24(tmp_path, golden):
     ref = O.orc_cpu_quantized_matmul(wq, xq, np.float32(ws), np.float32(0.05))
     assert np.array_equal(bits(y), bits(ref))
     assert np.array_equal(bits(y), bits(g["sp_yf"]))
+
+
+def run_levels(m, tmp_path, feed, inter):
+    """Run model dict m at OptLevel Extended (device-resident plan with Relu
+    fused), Basic (plan, no fusion) and None (node by node through the host
+    OpFuncs): all three give the same bits.  inter lists (name, shape) of
+    intermediates, returned from a copy of the model that exposes them as
+    graph outputs (which keeps their Relu unfused)."""
+    p = str(tmp_path / (m["name"] + ".pfm"))
+    pfm.save(m, p)
+    runs = []
+    for lvl in (2, 1, 0):
+        s = session.InferenceSession(p, session.SessionOptions(optimization_level=lvl))
+        runs.append((s.run(None, feed), s.device_plan()))
+    for outs, _ in runs[1:]:
+        for a, b in zip(runs[0][0], outs):
+            assert a.shape == b.shape and np.array_equal(bits(a), bits(b))
+    assert runs[2][1] == (False, 0)
+    m2 = dict(m, name=m["name"] + "_x", outputs=list(m["outputs"]) + [(n, 0, sh) for n, sh in inter])
+    p2 = str(tmp_path / (m2["name"] + ".pfm"))
+    pfm.save(m2, p2)
+    s = session.InferenceSession(p2)
+    res = s.run([n for n, *_ in m2["outputs"]], feed)
+    for a, b in zip(runs[0][0], res):
+        assert np.array_equal(bits(a), bits(b))
+    return runs[0][0], res[len(m["outputs"]):], runs[0][1], runs[1][1]
+
+
+def test_device_plan_graphs(tmp_path, golden):
+    """Graphs of pruned MatMuls in both operand positions, batched MatMul,
+    fused and unfused Relu, Softmax over axis 0 and a 2:4 QuantizedMatMul
+    run on the device-resident plan: the same bits as the node-by-node run,
+    the products bit-exact against the oracle."""
+    rng = np.random.default_rng(21)
+
+    def pruned(shape, keep):
+        w = rng.standard_normal(shape).astype(np.float32)
+        w[rng.random(shape) >= keep] = 0
+        return w
+
+    W1, W2 = pruned((48, 64), 0.2), pruned((30, 10), 0.5)
+    x = rng.standard_normal((10, 48)).astype(np.float32)
+    m = {"name": "g1", "inputs": [("x", 0, [10, 48])], "outputs": [("y", 0, [30, 64])],
+         "initializers": {"w1": W1, "w2": W2},
+         "nodes": [("mm1", "MatMul", ["x", "w1"], ["h"], {}), ("r1", "Relu", ["h"], ["a"], {}),
+                   ("mm2", "MatMul", ["w2", "a"], ["z"], {}), ("r2", "Relu", ["z"], ["r"], {}),
+                   ("sm", "Softmax", ["r"], ["y"], {"axis": 0})]}
+    say("device plan: MatMul(x,W)+Relu, MatMul(W,a)+Relu, Softmax(axis 0)")
+    (y,), (h, z), plan, basic = run_levels(m, tmp_path, {"x": x}, [("h", [10, 64]), ("z", [30, 64])])
+    assert plan == (True, 3) and basic == (True, 5)
+    assert np.array_equal(bits(h), bits(O.orc_matmul(x, W1)))
+    z_ref = O.orc_matmul(W2, O.orc_relu(h))
+    assert np.array_equal(bits(z), bits(z_ref))
+    assert np.abs(y - O.orc_softmax(O.orc_relu(z_ref), axis=0)).max() <= 4e-7
+
+    xb = rng.standard_normal((2, 5, 48)).astype(np.float32)
+    m = {"name": "g2", "inputs": [("x", 0, [2, 5, 48])], "outputs": [("y", 0, [2, 5, 64])],
+         "initializers": {"w1": W1},
+         "nodes": [("mm", "MatMul", ["x", "w1"], ["h"], {}), ("r", "Relu", ["h"], ["y"], {})]}
+    say("device plan: batched MatMul + Relu")
+    (y,), (h,), plan, basic = run_levels(m, tmp_path, {"x": xb}, [("h", [2, 5, 64])])
+    assert plan == (True, 1) and basic == (True, 2) and y.shape == (2, 5, 64)
+    assert np.array_equal(bits(y), bits(O.orc_relu(O.orc_matmul(xb, W1))))
+
+    g = golden("qmatmul.npz")
+    wq, xq, ws = g["sp_wq"], g["sp_xq"], float(g["sp_ws"])
+    m = {"name": "g3", "inputs": [("x", 7, list(xq.shape))], "outputs": [("y", 0, [wq.shape[0], xq.shape[1]])],
+         "initializers": {"w": wq},
+         "nodes": [("qmm", "QuantizedMatMul", ["w", "x"], ["q"], {"a_scale": ws, "b_scale": 0.05}),
+                   ("r", "Relu", ["q"], ["y"], {})]}
+    say("device plan: QuantizedMatMul 2:4 + Relu")
+    (y,), (q,), plan, basic = run_levels(m, tmp_path, {"x": xq}, [("q", [wq.shape[0], xq.shape[1]])])
+    assert plan == (True, 2) and basic == (True, 2)
+    assert np.array_equal(bits(q), bits(g["sp_yf"]))
+    assert np.array_equal(bits(y), bits(O.orc_relu(g["sp_yf"])))
 
 
 def test_backend_errors(tmp_path):
