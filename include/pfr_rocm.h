@@ -101,6 +101,13 @@ int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz,
                    const int64_t* indptr, const int64_t* indices,
                    const void* values, pfr_dtype values_dtype,
                    const float* row_scales, pfr_csr** out);
+/* pfr_csr_upload with int32 column indices: the form a sparse .pfm record
+ * keeps in memory (no reference counterpart; the reference has no sparse
+ * on-disk form, pyflame_format.cpp:168-176), uploaded without widening. */
+int pfr_csr_upload_i32(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz,
+                       const int64_t* indptr, const int32_t* indices,
+                       const void* values, pfr_dtype values_dtype,
+                       const float* row_scales, pfr_csr** out);
 /* Build the CSR of a dense, zero-filled pruned weight the way
  * to_sparse(dense, threshold, CSR) does (sparse_tensor.cpp:560-610: keeps
  * |v| > threshold, columns ascending).  dense is rows x cols, row-major,

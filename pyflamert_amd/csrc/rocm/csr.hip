@@ -182,9 +182,11 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
 
 extern "C" {
 
-int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_t* indptr,
-                   const int64_t* indices, const void* values, pfr_dtype values_dtype,
-                   const float* row_scales, pfr_csr** out) {
+extern "C++" {
+namespace {
+template <class IDX>
+int csr_upload_any(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_t* indptr, const IDX* indices,
+                   const void* values, pfr_dtype values_dtype, const float* row_scales, pfr_csr** out) {
     return pfr::guarded([&] {
         pfr::require(out != nullptr, "null output handle");
         *out = nullptr;
@@ -207,7 +209,7 @@ int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_
         }
         std::vector<int32_t> cl((size_t)nnz);
         for (int64_t j = 0; j < nnz; ++j) {
-            int64_t c = indices[j];
+            const int64_t c = indices[j];
             pfr::require(c >= 0 && c < K, "CSR column index " + std::to_string(c) +
                                               " out of range [0, " + std::to_string(K) + ")");
             cl[(size_t)j] = (int32_t)c;
@@ -219,6 +221,20 @@ int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_
         *out = build(ctx, M, K, rp, cl, values, values_dtype,
                      values_dtype == PFR_I8 ? row_scales : nullptr);
     });
+}
+}  // namespace
+}  // extern "C++"
+
+int pfr_csr_upload(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_t* indptr,
+                   const int64_t* indices, const void* values, pfr_dtype values_dtype,
+                   const float* row_scales, pfr_csr** out) {
+    return csr_upload_any(ctx, M, K, nnz, indptr, indices, values, values_dtype, row_scales, out);
+}
+
+int pfr_csr_upload_i32(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz, const int64_t* indptr,
+                       const int32_t* indices, const void* values, pfr_dtype values_dtype,
+                       const float* row_scales, pfr_csr** out) {
+    return csr_upload_any(ctx, M, K, nnz, indptr, indices, values, values_dtype, row_scales, out);
 }
 
 int pfr_csr_from_dense(pfr_ctx* ctx, const float* dense, int64_t rows, int64_t cols, int transpose,

@@ -1,6 +1,7 @@
 #include "rocm_executor.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <stdexcept>
 #include <unordered_set>
 
@@ -27,6 +28,62 @@ int64_t numel(const std::vector<int64_t>& shape) {
 
 void need_f32(DType d, const char* what) {
     if (d != DType::Float32) throw std::invalid_argument(std::string(what) + " must be float32, got " + dtype_name(d));
+}
+
+// CSR of a sparse record's transpose (cols x rows); within each new row the
+// source rows come in ascending order, so indices stay ascending.  A
+// per-row scale becomes a per-column one and the reverse.
+SparseInitializer csr_transpose(const SparseInitializer& s) {
+    SparseInitializer t;
+    t.format = SparseInitializer::Csr;
+    t.dtype = s.dtype;
+    t.rows = s.cols;
+    t.cols = s.rows;
+    t.scales = s.scales;
+    t.scale_axis = s.scales.size() > 1 ? 1 - s.scale_axis : 0;
+    const size_t es = dtype_size(s.dtype);
+    const int64_t nnz = s.nnz();
+    t.indptr.assign((size_t)t.rows + 1, 0);
+    for (int64_t j = 0; j < nnz; ++j) ++t.indptr[(size_t)s.indices[(size_t)j] + 1];
+    for (int64_t c = 0; c < t.rows; ++c) t.indptr[(size_t)c + 1] += t.indptr[(size_t)c];
+    t.indices.resize((size_t)nnz);
+    t.values.resize((size_t)nnz * es);
+    std::vector<int64_t> next(t.indptr.begin(), t.indptr.end() - 1);
+    for (int64_t r = 0; r < s.rows; ++r)
+        for (int64_t j = s.indptr[(size_t)r]; j < s.indptr[(size_t)r + 1]; ++j) {
+            const int64_t d = next[(size_t)s.indices[(size_t)j]]++;
+            t.indices[(size_t)d] = (int32_t)r;
+            std::memcpy(&t.values[(size_t)d * es], &s.values[(size_t)j * es], es);
+        }
+    return t;
+}
+
+// Uploads a CSR record (or, with transpose, its transpose) as a device
+// weight whose rows are output channels.  int8 values keep the in-kernel
+// dequantisation when their scale is per tensor or per device row; a scale
+// along the reduction dimension is applied on the host instead, giving the
+// same float weights RN((float)q * scale).
+pfr_csr* upload_sparse_csr(pfr_ctx* ctx, const SparseInitializer& src, bool transpose) {
+    SparseInitializer tmp;
+    const SparseInitializer& s = transpose ? (tmp = csr_transpose(src)) : src;
+    pfr_csr* w = nullptr;
+    if (s.dtype == DType::Float32) {
+        pfr_check(pfr_csr_upload_i32(ctx, s.rows, s.cols, s.nnz(), s.indptr.data(), s.indices.data(),
+                                     s.values.data(), PFR_F32, nullptr, &w));
+        return w;
+    }
+    if (s.scales.size() == 1 || s.scale_axis == 0) {
+        std::vector<float> rs = s.scales.size() == 1 ? std::vector<float>((size_t)s.rows, s.scales[0]) : s.scales;
+        pfr_check(pfr_csr_upload_i32(ctx, s.rows, s.cols, s.nnz(), s.indptr.data(), s.indices.data(),
+                                     s.values.data(), PFR_I8, rs.data(), &w));
+        return w;
+    }
+    std::vector<float> v((size_t)s.nnz());
+    for (size_t j = 0; j < v.size(); ++j)
+        v[j] = (float)(int8_t)s.values[j] * s.scales[(size_t)s.indices[j]];
+    pfr_check(pfr_csr_upload_i32(ctx, s.rows, s.cols, s.nnz(), s.indptr.data(), s.indices.data(), v.data(),
+                                 PFR_F32, nullptr, &w));
+    return w;
 }
 
 // Waits for the context's stream when a plan run leaves early, so that no
@@ -70,8 +127,42 @@ void RocmExecutor::release_weights() {
     bufs_.clear();
     plan_.clear();
     fused_away_.clear();
+    sparse_views_.clear();
+    sparse_dense_.clear();
     plan_ok_ = false;
     prepared_for_ = nullptr;
+}
+
+const Tensor& RocmExecutor::weight_tensor(const Graph& graph, const std::string& name) const {
+    auto t = graph.get_initializer(name);
+    if (t) return t->get();
+    auto it = sparse_views_.find(name);
+    if (it == sparse_views_.end()) throw BackendError("Initializer '" + name + "' not found");
+    return it->second;
+}
+
+const Tensor& RocmExecutor::initializer_value(const Graph& graph, const std::string& name) {
+    auto t = graph.get_initializer(name);
+    if (t) return t->get();
+    auto it = sparse_dense_.find(name);
+    if (it != sparse_dense_.end()) return it->second;
+    const SparseInitializer* s = graph.get_sparse_initializer(name);
+    if (!s) throw BackendError("Initializer '" + name + "' not found");
+    return sparse_dense_.emplace(name, s->to_dense()).first->second;
+}
+
+// Shape-only views of the sparse initializers that feed a prepared weight
+// slot (the OpFuncs read only the weight's shape and type; the values are on
+// the device).
+void RocmExecutor::prepare_sparse_views(const Graph& graph) {
+    for (const auto& kv : weights_) {
+        const Node* n = kv.first;
+        const int slot = kv.second.kind == DeviceWeight::CsrB ? 1 : 0;
+        const std::string& nm = n->inputs()[(size_t)slot];
+        const SparseInitializer* s = graph.get_sparse_initializer(nm);
+        if (s && !sparse_views_.count(nm))
+            sparse_views_.emplace(nm, Tensor(nullptr, {s->rows, s->cols}, s->logical_dtype()));
+    }
 }
 
 void* RocmExecutor::device_buffer(const std::string& name, int64_t bytes) {
@@ -121,9 +212,32 @@ void RocmExecutor::prepare(const Graph& graph) {
             auto t = graph.get_initializer(in[i]);
             return t ? &t->get() : nullptr;
         };
+        auto sparse = [&](size_t i) -> const SparseInitializer* {
+            return i < in.size() ? graph.get_sparse_initializer(in[i]) : nullptr;
+        };
+        auto csr_rec = [&](size_t i) { return sparse(i) && sparse(i)->format == SparseInitializer::Csr; };
         DeviceWeight w;
         try {
-            if (n->op_type() == "Gemm" && init(1) && is_f32_matrix(*init(1))) {
+            if (n->op_type() == "Gemm" && csr_rec(1)) {
+                // B stored K x N (transB 0) or N x K: the device weight is op(B)^T
+                const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
+                w.csr = upload_sparse_csr(ctx_, *sparse(1), !tb);
+                w.kind = DeviceWeight::CsrB;
+            } else if (n->op_type() == "MatMul" && csr_rec(1)) {
+                w.csr = upload_sparse_csr(ctx_, *sparse(1), true);
+                w.kind = DeviceWeight::CsrB;
+            } else if (n->op_type() == "MatMul" && csr_rec(0) && !init(1) && !sparse(1)) {
+                w.csr = upload_sparse_csr(ctx_, *sparse(0), false);
+                w.kind = DeviceWeight::CsrA;
+            } else if (n->op_type() == "QuantizedMatMul" && sparse(0) &&
+                       sparse(0)->format == SparseInitializer::Nm24 &&
+                       n->get_attr<int64_t>("a_zero_point", 0) == 0 && n->get_attr<int64_t>("b_zero_point", 0) == 0) {
+                // expanded for the packer only; the record is 2:4 by construction
+                const Tensor A = sparse(0)->to_dense();
+                const float a_scale = n->get_attr<float>("a_scale", 1.0f);
+                pfr_check(pfr_sp24_pack(ctx_, A.shape()[0], A.shape()[1], A.data(), PFR_I8, &a_scale, 1, &w.sp24));
+                w.kind = DeviceWeight::Sp24A;
+            } else if (n->op_type() == "Gemm" && init(1) && is_f32_matrix(*init(1))) {
                 const Tensor& B = *init(1);
                 const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
                 pfr_check(pfr_csr_from_dense(ctx_, B.data_ptr<float>(), B.shape()[0], B.shape()[1], tb ? 0 : 1, 0.0f,
@@ -152,6 +266,7 @@ void RocmExecutor::prepare(const Graph& graph) {
         }
         if (w.kind != DeviceWeight::None) weights_[n.get()] = w;
     }
+    prepare_sparse_views(graph);
     build_plan(graph);
     prepared_for_ = &graph;
 }
@@ -224,10 +339,8 @@ void RocmExecutor::build_plan(const Graph& graph) {
                                 : (st.op == PlanStep::MatMulA || st.op == PlanStep::QMatMul) ? 0
                                                                                              : -1;
         for (size_t k = 0; k < in.size(); ++k) {
-            if ((int)k == weight_slot || constants_.count(in[k])) continue;
-            auto t = graph.get_initializer(in[k]);
-            if (!t) continue;
-            const Tensor& src = t->get();
+            if ((int)k == weight_slot || constants_.count(in[k]) || !graph.has_initializer(in[k])) continue;
+            const Tensor& src = initializer_value(graph, in[k]);
             DevTensor d;
             d.shape = src.shape();
             d.dtype = src.dtype();
@@ -269,7 +382,7 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
             if (it == live.end()) throw BackendError("Input tensor '" + in[i] + "' not found", n->name());
             return it->second;
         };
-        auto init_in = [&](size_t i) -> const Tensor& { return graph.get_initializer(in[i])->get(); };
+        auto init_in = [&](size_t i) -> const Tensor& { return weight_tensor(graph, in[i]); };
         auto need_inputs = [&](size_t k, const char* op) {
             if (in.size() < k)
                 throw std::invalid_argument(std::string(op) + ": expected at least " + std::to_string(k) +
@@ -417,6 +530,10 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
     results.reserve(names.size());
     for (const auto& nm : names) {
         auto it = live.find(nm);
+        if (it == live.end() && graph.has_initializer(nm)) {
+            results.push_back(initializer_value(graph, nm).clone());  // a weight asked for as an output
+            continue;
+        }
         if (it == live.end()) throw BackendError("Output tensor '" + nm + "' not found");
         const DevTensor& d = it->second;
         Tensor t(d.shape, d.dtype);
@@ -458,8 +575,17 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
         if (!op) throw UnsupportedOperatorError(node->op_type(), name_);
         std::vector<const Tensor*> ins;
         ins.reserve(node->inputs().size());
-        for (const auto& nm : node->inputs()) {
+        const DeviceWeight* w = weight(node.get());
+        const int wslot = !w ? -1 : (w->kind == DeviceWeight::CsrB ? 1 : 0);
+        for (size_t i = 0; i < node->inputs().size(); ++i) {
+            const std::string& nm = node->inputs()[i];
             auto it = view.find(nm);
+            if (it == view.end() && graph.get_sparse_initializer(nm)) {
+                // the prepared weight slot gets the shape-only view, any other
+                // use the expanded tensor
+                ins.push_back((int)i == wslot ? &sparse_views_.at(nm) : &initializer_value(graph, nm));
+                continue;
+            }
             if (it == view.end()) throw BackendError("Input tensor '" + nm + "' not found", node->name());
             ins.push_back(it->second);
         }
@@ -490,8 +616,13 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
             continue;
         }
         auto v = view.find(nm);
-        if (v == view.end()) throw BackendError("Output tensor '" + nm + "' not found");
-        results.push_back(v->second->clone());
+        if (v != view.end()) {
+            results.push_back(v->second->clone());
+        } else if (graph.get_sparse_initializer(nm)) {
+            results.push_back(initializer_value(graph, nm).clone());
+        } else {
+            throw BackendError("Output tensor '" + nm + "' not found");
+        }
     }
     return results;
 }

@@ -8,7 +8,9 @@
 //  * pruned weights (initializers feeding MatMul / Gemm / QuantizedMatMul)
 //    are converted once, on the first run of a graph, into device-resident
 //    CSR or 2:4-compressed operands kept by the executor per node; the rocm
-//    kernels find them through RocmExecutor::current();
+//    kernels find them through RocmExecutor::current().  A sparse
+//    initializer (a CSR or 2:4 record of a version-2 .pfm) is uploaded from
+//    its compressed form, never expanded to a dense host tensor;
 //  * inputs and initializers are not deep-copied on every run;
 //  * from OptLevel::Basic up, a graph whose every node has a device kernel
 //    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, Relu, Softmax) runs as a
@@ -83,7 +85,14 @@ private:
     };
 
     void prepare(const Graph& graph);
+    void prepare_sparse_views(const Graph& graph);
     void build_plan(const Graph& graph);
+    // The weight operand's host-side tensor: a dense initializer, or for a
+    // sparse one a data-less view with its logical shape and type.
+    const Tensor& weight_tensor(const Graph& graph, const std::string& name) const;
+    // A non-weight use of an initializer: the dense one, or a sparse one
+    // expanded once (sparse_dense_).
+    const Tensor& initializer_value(const Graph& graph, const std::string& name);
     void release_weights();
     void* device_buffer(const std::string& name, int64_t bytes);
     std::vector<Tensor> execute_plan(const Graph& graph, const std::unordered_map<std::string, Tensor>& input_feed,
@@ -102,6 +111,8 @@ private:
     std::unordered_set<std::string> fused_away_;           // product outputs a fused Relu consumes
     std::unordered_map<std::string, DevTensor> constants_;  // non-weight initializers, uploaded once
     std::unordered_map<std::string, DevBuf> bufs_;          // graph inputs and activations, by name
+    std::unordered_map<std::string, Tensor> sparse_views_;  // sparse weights: shape-only views
+    std::unordered_map<std::string, Tensor> sparse_dense_;  // sparse initializers used as plain tensors
 };
 
 // Throws the C ABI's last error as std::invalid_argument / std::runtime_error.

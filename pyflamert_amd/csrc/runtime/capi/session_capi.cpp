@@ -226,7 +226,20 @@ int pfr_model_describe(const char* path, char* buf, int64_t cap, int64_t* needed
             o << (i ? "," : "") << jstr(names[i]) << ":{\"dtype\":" << (int)t.dtype() << ",\"shape\":" << sh
               << "],\"nnz\":" << count_nonzero_bytes(t) << "}";
         }
-        o << "},\"nodes\":[";
+        o << "},\"sparse_initializers\":{";
+        std::vector<std::string> sn;
+        for (const auto& kv : g->sparse_initializers()) sn.push_back(kv.first);
+        std::sort(sn.begin(), sn.end());
+        for (size_t i = 0; i < sn.size(); ++i) {
+            const SparseInitializer& s = g->sparse_initializers().at(sn[i]);
+            o << (i ? "," : "") << jstr(sn[i]) << ":{\"format\":"
+              << (s.format == SparseInitializer::Csr ? "\"csr\"" : "\"2:4\"") << ",\"dtype\":" << (int)s.dtype
+              << ",\"shape\":[" << s.rows << "," << s.cols << "],\"nnz\":" << s.nnz()
+              << ",\"stored_bytes\":" << s.stored_bytes() << ",\"scales\":" << s.scales.size()
+              << ",\"scale_axis\":" << s.scale_axis << "}";
+        }
+        o << "},\"total_initializer_bytes\":" << g->total_initializer_bytes();
+        o << ",\"nodes\":[";
         auto order = g->topological_sort();
         for (size_t i = 0; i < order.size(); ++i) {
             const Node& n = *order[i];

@@ -4,6 +4,17 @@
 // dtype, dims, u64 byte count + raw little-endian data), nodes (name, op,
 // inputs, outputs, attributes typed 0 int64 / 1 float / 2 string /
 // 3 int64[] / 4 float[] / 255 skipped).  Strings are u64 length + bytes.
+//
+// Version 2 (this runtime; the reference loader rejects it as an unsupported
+// version, pyflame_format.cpp:406-409) appends after the nodes a section of
+// sparse initializers (SparseInitializer, graph.hpp): u64 count, then per
+// record name, u32 format (1 CSR, 2 2:4), u32 stored value dtype, i64 rows,
+// i64 cols and
+//   CSR: u64 nnz, u32 index width (2: uint16, 4: int32), indptr (rows + 1)
+//        x int64, indices nnz x width, values nnz x dtype size, u32 scale
+//        axis, u64 scale count, scales x float32;
+//   2:4: values rows x cols/2 int8, positions rows x cols/4 bytes.
+// A graph without sparse initializers is written as version 1.
 #pragma once
 
 #include <cstdint>
@@ -28,7 +39,7 @@ struct DeserializationLimits {
 class PyFlameFormat {
 public:
     static constexpr char MAGIC[4] = {'P', 'F', 'M', '\0'};
-    static constexpr uint32_t VERSION = 1;
+    static constexpr uint32_t VERSION = 2;
     static std::unique_ptr<Graph> load(const std::string& path);
     static void save(const Graph& graph, const std::string& path);
 };

@@ -109,7 +109,8 @@ const Node* Graph::get_node(const std::string& name) const {
 }
 
 void Graph::add_initializer(const std::string& name, Tensor t) {
-    if (initializers_.size() >= limits_.max_initializers && !initializers_.count(name))
+    if (sparse_.count(name)) throw std::runtime_error("Initializer '" + name + "' is already a sparse initializer");
+    if (initializers_.size() + sparse_.size() >= limits_.max_initializers && !initializers_.count(name))
         throw std::runtime_error("Graph initializer limit exceeded: max " +
                                  std::to_string(limits_.max_initializers) + " initializers allowed");
     size_t base = init_bytes_;
@@ -120,6 +121,27 @@ void Graph::add_initializer(const std::string& name, Tensor t) {
                                  std::to_string(limits_.max_initializer_bytes / (1024 * 1024)) + " MB allowed");
     init_bytes_ = base + t.size_bytes();
     initializers_[name] = std::move(t);
+}
+
+void Graph::add_sparse_initializer(const std::string& name, SparseInitializer s) {
+    if (initializers_.count(name)) throw std::runtime_error("Initializer '" + name + "' is already a dense initializer");
+    if (initializers_.size() + sparse_.size() >= limits_.max_initializers && !sparse_.count(name))
+        throw std::runtime_error("Graph initializer limit exceeded: max " +
+                                 std::to_string(limits_.max_initializers) + " initializers allowed");
+    s.validate(name);
+    size_t base = init_bytes_;
+    auto it = sparse_.find(name);
+    if (it != sparse_.end()) base -= it->second.stored_bytes();
+    if (base + s.stored_bytes() > limits_.max_initializer_bytes)
+        throw std::runtime_error("Graph initializer memory limit exceeded: max " +
+                                 std::to_string(limits_.max_initializer_bytes / (1024 * 1024)) + " MB allowed");
+    init_bytes_ = base + s.stored_bytes();
+    sparse_[name] = std::move(s);
+}
+
+const SparseInitializer* Graph::get_sparse_initializer(const std::string& name) const {
+    auto it = sparse_.find(name);
+    return it == sparse_.end() ? nullptr : &it->second;
 }
 
 std::optional<std::reference_wrapper<const Tensor>> Graph::get_initializer(const std::string& name) const {
@@ -169,6 +191,7 @@ std::vector<std::string> Graph::validate() const {
     std::unordered_set<std::string> avail;
     for (const auto& i : inputs_) avail.insert(i.name);
     for (const auto& kv : initializers_) avail.insert(kv.first);
+    for (const auto& kv : sparse_) avail.insert(kv.first);
     std::vector<std::shared_ptr<Node>> sorted;
     try {
         sorted = topological_sort();

@@ -1,5 +1,6 @@
-// .pfm v1 reader and writer (format described in pyflame_format.hpp).  Every
-// read is length-checked against DeserializationLimits before allocating.
+// .pfm v1/v2 reader and writer (format described in pyflame_format.hpp).
+// Every read is length-checked against DeserializationLimits before
+// allocating.
 #include "pyflame_rt/pyflame_format.hpp"
 
 #include <algorithm>
@@ -133,6 +134,59 @@ std::shared_ptr<Node> rd_node(std::istream& is) {
     return node;
 }
 
+// Bulk read of n elements of T into v, after the byte count is checked.
+template <class T>
+void rd_array(std::istream& is, std::vector<T>& v, uint64_t n, const std::string& what) {
+    if (n > DeserializationLimits::MAX_TENSOR_DATA_SIZE / sizeof(T))
+        throw InvalidModelError("Data size exceeds limit: " + what);
+    v.resize((size_t)n);
+    if (n) read_exact(is, v.data(), (size_t)n * sizeof(T), what.c_str());
+}
+
+std::pair<std::string, SparseInitializer> rd_sparse(std::istream& is) {
+    std::string name = rd_string(is);
+    SparseInitializer s;
+    const uint32_t fmt = rd<uint32_t>(is, "uint32");
+    if (fmt != SparseInitializer::Csr && fmt != SparseInitializer::Nm24)
+        throw InvalidModelError("Unknown sparse format " + std::to_string(fmt) + " for tensor '" + name + "'");
+    s.format = static_cast<SparseInitializer::Format>(fmt);
+    s.dtype = rd_dtype(is, " in sparse tensor '" + name + "'");
+    s.rows = rd<int64_t>(is, "int64");
+    s.cols = rd<int64_t>(is, "int64");
+    if (s.rows < 0 || s.cols < 0 || s.rows > DeserializationLimits::MAX_DIMENSION_SIZE ||
+        s.cols > DeserializationLimits::MAX_DIMENSION_SIZE)
+        throw InvalidModelError("Invalid dimensions in sparse tensor '" + name + "'");
+    if (s.format == SparseInitializer::Csr) {
+        const uint64_t nnz = rd<uint64_t>(is, "uint64");
+        if (nnz > (uint64_t)DeserializationLimits::MAX_TOTAL_ELEMENTS)
+            throw InvalidModelError("Sparse tensor '" + name + "' has too many nonzeros: " + std::to_string(nnz));
+        const uint32_t ib = rd<uint32_t>(is, "uint32");
+        if (ib != 2 && ib != 4)
+            throw InvalidModelError("Sparse tensor '" + name + "': index width must be 2 or 4 bytes");
+        rd_array(is, s.indptr, (uint64_t)s.rows + 1, "sparse indptr");
+        if (ib == 2) {
+            std::vector<uint16_t> c16;
+            rd_array(is, c16, nnz, "sparse indices");
+            s.indices.assign(c16.begin(), c16.end());
+        } else {
+            rd_array(is, s.indices, nnz, "sparse indices");
+        }
+        if (!validate_dtype_value((uint32_t)s.dtype) || dtype_size(s.dtype) > 4)
+            throw InvalidModelError("Sparse tensor '" + name + "': unsupported value type");
+        rd_array(is, s.values, nnz * dtype_size(s.dtype), "sparse values");
+        s.scale_axis = rd<uint32_t>(is, "uint32");
+        const uint64_t ns = rd_count(is, DeserializationLimits::MAX_ARRAY_COUNT * 100,
+                                     "Too many scales in sparse tensor '" + name + "'");
+        rd_array(is, s.scales, ns, "sparse scales");
+    } else {
+        if (s.cols % 4)
+            throw InvalidModelError("Sparse tensor '" + name + "': 2:4 needs cols divisible by 4");
+        rd_array(is, s.values, (uint64_t)s.rows * (uint64_t)(s.cols / 2), "2:4 values");
+        rd_array(is, s.positions, (uint64_t)s.rows * (uint64_t)(s.cols / 4), "2:4 positions");
+    }
+    return {name, std::move(s)};
+}
+
 template <class T>
 void wr(std::ostream& os, T v) {
     os.write(reinterpret_cast<const char*>(&v), sizeof(T));
@@ -150,6 +204,39 @@ void wr_info(std::ostream& os, const TensorInfo& i) {
     for (const auto& d : i.shape) wr<int64_t>(os, d ? *d : -1);
 }
 
+template <class T>
+void wr_array(std::ostream& os, const std::vector<T>& v) {
+    os.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
+}
+
+// Column indices go to disk as uint16 when every index fits (cols <= 65536).
+void wr_sparse(std::ostream& os, const std::string& name, const SparseInitializer& s) {
+    wr_string(os, name);
+    wr<uint32_t>(os, s.format);
+    wr<uint32_t>(os, static_cast<uint32_t>(s.dtype));
+    wr<int64_t>(os, s.rows);
+    wr<int64_t>(os, s.cols);
+    if (s.format == SparseInitializer::Csr) {
+        wr<uint64_t>(os, (uint64_t)s.indices.size());
+        const bool narrow = s.cols <= 65536;
+        wr<uint32_t>(os, narrow ? 2 : 4);
+        wr_array(os, s.indptr);
+        if (narrow) {
+            std::vector<uint16_t> c16(s.indices.begin(), s.indices.end());
+            wr_array(os, c16);
+        } else {
+            wr_array(os, s.indices);
+        }
+        wr_array(os, s.values);
+        wr<uint32_t>(os, s.scale_axis);
+        wr<uint64_t>(os, s.scales.size());
+        wr_array(os, s.scales);
+    } else {
+        wr_array(os, s.values);
+        wr_array(os, s.positions);
+    }
+}
+
 }  // namespace
 
 std::unique_ptr<Graph> PyFlameFormat::load(const std::string& path) {
@@ -160,6 +247,7 @@ std::unique_ptr<Graph> PyFlameFormat::load(const std::string& path) {
     if (std::memcmp(magic, MAGIC, 4) != 0) throw InvalidModelError("Invalid magic bytes", path);
     const uint32_t version = rd<uint32_t>(f, "uint32");
     if (version > VERSION) throw InvalidModelError("Unsupported version: " + std::to_string(version), path);
+    if (version == 0) throw InvalidModelError("Unsupported version: 0", path);
     auto g = std::make_unique<Graph>(rd_string(f));
     const uint64_t ni = rd_count(f, DeserializationLimits::MAX_ARRAY_COUNT, "Too many graph inputs");
     for (uint64_t i = 0; i < ni; ++i) g->add_input(rd_info(f));
@@ -172,6 +260,19 @@ std::unique_ptr<Graph> PyFlameFormat::load(const std::string& path) {
     }
     const uint64_t nn = rd_count(f, DeserializationLimits::MAX_NODES, "Too many nodes");
     for (uint64_t i = 0; i < nn; ++i) g->add_node(rd_node(f));
+    if (version >= 2) {
+        const uint64_t ns = rd_count(f, DeserializationLimits::MAX_ARRAY_COUNT, "Too many sparse initializers");
+        for (uint64_t i = 0; i < ns; ++i) {
+            auto sp = rd_sparse(f);
+            try {
+                g->add_sparse_initializer(sp.first, std::move(sp.second));
+            } catch (const InvalidModelError&) {
+                throw;
+            } catch (const std::exception& e) {
+                throw InvalidModelError(e.what(), path);
+            }
+        }
+    }
     if (f.fail()) throw InvalidModelError("Stream read failed: end of file");
     return g;
 }
@@ -180,7 +281,10 @@ void PyFlameFormat::save(const Graph& g, const std::string& path) {
     std::ofstream f(path, std::ios::binary);
     if (!f) throw InvalidModelError("Cannot create file", path);
     f.write(MAGIC, 4);
-    wr<uint32_t>(f, VERSION);
+    // A model without sparse initializers stays version 1, readable by the
+    // reference loader.
+    const bool sparse = !g.sparse_initializers().empty();
+    wr<uint32_t>(f, sparse ? VERSION : 1u);
     wr_string(f, g.name());
     wr<uint64_t>(f, g.inputs().size());
     for (const auto& i : g.inputs()) wr_info(f, i);
@@ -230,6 +334,13 @@ void PyFlameFormat::save(const Graph& g, const std::string& path) {
                 wr<uint32_t>(f, 255);
             }
         }
+    }
+    if (sparse) {
+        std::vector<std::string> sn;
+        for (const auto& kv : g.sparse_initializers()) sn.push_back(kv.first);
+        std::sort(sn.begin(), sn.end());
+        wr<uint64_t>(f, sn.size());
+        for (const auto& n : sn) wr_sparse(f, n, g.sparse_initializers().at(n));
     }
     if (!f) throw InvalidModelError("Write failed", path);
 }

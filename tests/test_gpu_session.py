@@ -221,3 +221,79 @@ def test_backend_errors(tmp_path):
         s.run(None, {"a": np.ones((2, 3), np.int8), "b": np.ones((3, 2), np.float32)})
     name, ops = s.supported_ops()
     assert name == "rocm" and {"MatMul", "Gemm", "QuantizedMatMul", "Relu", "Softmax"} <= set(ops)
+
+
+def test_sparse_record_sessions(mlp, golden, tmp_path):
+    """Version-2 .pfm models whose pruned weights are sparse records run
+    without a dense copy and give the results of the dense models: the MLP
+    with CSR weights (same bits as the dense file), int8 CSR weights in
+    both operand positions with per-row, per-column and per-tensor scales
+    (bit-exact against the oracle on the dequantised matrix), Gemm with
+    transB, a 2:4 record under QuantizedMatMul, and a record used as a plain
+    tensor."""
+    g = golden("mlp.npz")
+    m = pfm.load(mlp)
+    inits = dict(m["initializers"])
+    sp = {k: pfm.csr_record(inits.pop(k)) for k in ("fc1.weight", "fc2.weight")}
+    ms = dict(m, initializers=inits, sparse_initializers=sp)
+    p = str(tmp_path / "mlp_sparse.pfm")
+    pfm.save(ms, p)
+    assert os.path.getsize(p) < os.path.getsize(mlp) / 3
+    say("MLP with CSR records")
+    for lvl in (2, 0):
+        s = session.InferenceSession(p, session.SessionOptions(optimization_level=lvl))
+        (y,) = s.run(None, {"x": g["x"]})
+        s_dense = session.InferenceSession(mlp, session.SessionOptions(optimization_level=lvl))
+        (yd,) = s_dense.run(None, {"x": g["x"]})
+        assert np.array_equal(bits(y), bits(yd)), lvl
+
+    rng = np.random.default_rng(12)
+    M, K, N = 96, 200, 5
+    q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    q[rng.random(q.shape) < 0.7] = 0
+    ip = np.concatenate([[0], np.cumsum((q != 0).sum(1))]).astype(np.int64)
+    ix = np.nonzero(q)[1].astype(np.int32)
+    x = rng.standard_normal((K, N)).astype(np.float32)
+    xt = rng.standard_normal((N, M)).astype(np.float32)
+    bias = rng.standard_normal(K).astype(np.float32)
+    for scales, axis, tag in ((rng.random(M) + 0.01, 0, "row"), (rng.random(K) + 0.01, 1, "col"),
+                              (np.array([0.02]), 0, "tensor")):
+        rec = pfm.csr_record_int8((M, K), ip, ix, q[q != 0], scales.astype(np.float32), axis)
+        Wd = pfm.record_to_dense(rec)
+        say(f"int8 CSR record, scales per {tag}: W.x, x.W, Gemm transB")
+        mm = {"name": "q", "inputs": [("x", 0, [K, N]), ("xt", 0, [N, M])],
+              "outputs": [("y", 0, [M, N]), ("z", 0, [N, K]), ("u", 0, [N, M])],
+              "initializers": {"bias": bias}, "sparse_initializers": {"w": rec},
+              "nodes": [("wx", "MatMul", ["w", "x"], ["y"], {}),
+                        ("xw", "MatMul", ["xt", "w"], ["z0"], {}), ("r", "Relu", ["z0"], ["z"], {}),
+                        ("gm", "Gemm", ["x", "w", "bias"], ["u0"], {"transA": 1, "transB": 1, "alpha": 0.5}),
+                        ("r2", "Relu", ["u0"], ["u"], {})]}
+        pq = str(tmp_path / f"q_{tag}.pfm")
+        pfm.save(mm, pq)
+        for lvl in (2, 0):
+            s = session.InferenceSession(pq, session.SessionOptions(optimization_level=lvl))
+            y, z, u = s.run(None, {"x": x, "xt": xt})
+            assert np.array_equal(bits(y), bits(O.orc_matmul(Wd, x))), (tag, lvl)
+            assert np.array_equal(bits(z), bits(O.orc_relu(O.orc_matmul(xt, Wd)))), (tag, lvl)
+            ref_u = O.orc_relu(O.orc_gemm(x, Wd, bias, 0.5, 1.0, transA=1, transB=1))
+            assert np.array_equal(bits(u), bits(ref_u)), (tag, lvl)
+
+    gq = golden("qmatmul.npz")
+    wq, xq, ws = gq["sp_wq"], gq["sp_xq"], float(gq["sp_ws"])
+    rec24 = pfm.nm24_record(wq)
+    assert np.array_equal(pfm.record_to_dense(rec24), wq)
+    f = rng.standard_normal((6, 8)).astype(np.float32)
+    f[f < 0] = 0
+    m24 = {"name": "q24", "inputs": [("x", 7, list(xq.shape))],
+           "outputs": [("y", 0, [wq.shape[0], xq.shape[1]]), ("fr", 0, [6, 8])],
+           "initializers": {}, "sparse_initializers": {"w": rec24, "f": pfm.csr_record(f)},
+           "nodes": [("qmm", "QuantizedMatMul", ["w", "x"], ["y"], {"a_scale": ws, "b_scale": 0.05}),
+                     ("rf", "Relu", ["f"], ["fr"], {})]}
+    p24 = str(tmp_path / "q24.pfm")
+    pfm.save(m24, p24)
+    say("2:4 record under QuantizedMatMul; a record as a plain tensor")
+    for lvl in (2, 0):
+        s = session.InferenceSession(p24, session.SessionOptions(optimization_level=lvl))
+        y, fr = s.run(None, {"x": xq})
+        assert np.array_equal(bits(y), bits(gq["sp_yf"])), lvl
+        assert np.array_equal(bits(fr), bits(f)), lvl

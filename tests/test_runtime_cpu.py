@@ -98,7 +98,8 @@ def test_corrupt_files(tmp_path, mlp_path):
     cases = {
         "magic.pfm": (b"XFM\0" + raw[4:], "Invalid magic"),
         "trunc.pfm": (raw[: len(raw) // 2], "Incomplete read"),
-        "version.pfm": (raw[:4] + (2).to_bytes(4, "little") + raw[8:], "Unsupported version"),
+        "version.pfm": (raw[:4] + (3).to_bytes(4, "little") + raw[8:], "Unsupported version"),
+        "v2nosparse.pfm": (raw[:4] + (2).to_bytes(4, "little") + raw[8:], "Incomplete read"),
     }
     for name, (data, msg) in cases.items():
         p = tmp_path / name
@@ -147,3 +148,125 @@ def test_session_without_gpu_raises_backend_error(mlp_path):
         pytest.skip("a device is visible")
     with pytest.raises(session.BackendError, match="cannot initialise ROCm device"):
         session.InferenceSession(mlp_path, session.SessionOptions(device="rocm"))
+
+
+def sparse_model(rng):
+    """A graph with every sparse record form: float32 CSR, int8 CSR with
+    per-row, per-column and per-tensor scales, and a 2:4 int8 record."""
+    f = rng.standard_normal((40, 24)).astype(np.float32)
+    f[rng.random(f.shape) < 0.8] = 0
+    q = rng.integers(-127, 128, (30, 70000 // 1000)).astype(np.int8)
+    q[rng.random(q.shape) < 0.7] = 0
+    ip = np.concatenate([[0], np.cumsum((q != 0).sum(1))]).astype(np.int64)
+    ix = np.nonzero(q)[1].astype(np.int32)
+    qv = q[q != 0]
+    wide = np.zeros((3, 70000), np.float32)  # cols > 65535: int32 indices on disk
+    wide[0, [5, 69999]] = [1.5, -2.0]
+    wide[2, 65536] = 3.0
+    d24 = rng.integers(-100, 100, (8, 32)).astype(np.int8)
+    g = d24.reshape(8, 8, 4)
+    for r in range(8):
+        for k in range(8):
+            g[r, k, rng.permutation(4)[: 2 + (k % 3 == 0)]] = 0
+    recs = {
+        "f32": pfm.csr_record(f),
+        "i8_row": pfm.csr_record_int8(q.shape, ip, ix, qv, rng.random(30).astype(np.float32) + 0.01, 0),
+        "i8_col": pfm.csr_record_int8(q.shape, ip, ix, qv, rng.random(70).astype(np.float32) + 0.01, 1),
+        "i8_one": pfm.csr_record_int8(q.shape, ip, ix, qv, [0.25], 0),
+        "wide": pfm.csr_record(wide),
+        "w24": pfm.nm24_record(g.reshape(8, 32)),
+    }
+    nodes = [("mm", "MatMul", ["a", "f32"], ["y"], {})]
+    return {"name": "sp", "inputs": [("a", 0, [2, 40])], "outputs": [("y", 0, [2, 24])],
+            "initializers": {"dense_b": np.ones((2, 2), np.float32)}, "sparse_initializers": recs,
+            "nodes": nodes}
+
+
+def test_sparse_records_roundtrip(tmp_path):
+    """Version-2 sparse initializers: the C++ loader reads what the Python
+    writer wrote, reports them, counts their stored bytes against the
+    initializer limit, and writes the same bytes back; a model without them
+    stays version 1."""
+    rng = np.random.default_rng(3)
+    m = sparse_model(rng)
+    p = write(tmp_path, "sp.pfm", m)
+    raw = open(p, "rb").read()
+    assert raw[4:8] == (2).to_bytes(4, "little")
+    d = session.describe_model(p)
+    sp = d["sparse_initializers"]
+    assert sorted(sp) == sorted(m["sparse_initializers"])
+    stored = 16  # the dense 2x2 float32 initializer
+    for name, rec in m["sparse_initializers"].items():
+        rows, cols = rec["shape"]
+        assert sp[name]["shape"] == [rows, cols]
+        dense = pfm.record_to_dense(rec)
+        if rec["format"] == "csr":
+            nnz = len(rec["values"])
+            assert sp[name]["format"] == "csr" and sp[name]["nnz"] == nnz
+            b = 8 * (rows + 1) + 4 * nnz + rec["values"].nbytes + 4 * len(rec.get("scales", []))
+        else:
+            assert sp[name]["format"] == "2:4" and sp[name]["nnz"] == int(np.count_nonzero(dense))
+            b = rows * cols // 2 + rows * cols // 4
+        assert sp[name]["stored_bytes"] == b
+        stored += b
+    assert d["total_initializer_bytes"] == stored
+    out = str(tmp_path / "sp2.pfm")
+    session.resave_model(p, out)
+    assert open(out, "rb").read() == raw
+    back = pfm.load(out)
+    for name, rec in m["sparse_initializers"].items():
+        assert np.array_equal(pfm.record_to_dense(back["sparse_initializers"][name]), pfm.record_to_dense(rec))
+    # the wide record keeps int32 indices on disk, the others uint16
+    assert int(np.max(back["sparse_initializers"]["wide"]["indices"])) == 69999
+    dense_only = dict(m, sparse_initializers={})
+    p1 = write(tmp_path, "d.pfm", dense_only)
+    assert open(p1, "rb").read()[4:8] == (1).to_bytes(4, "little")
+    session.resave_model(p1, str(tmp_path / "d2.pfm"))
+    assert open(str(tmp_path / "d2.pfm"), "rb").read()[4:8] == (1).to_bytes(4, "little")
+
+
+def test_sparse_record_validation(tmp_path):
+    """Malformed sparse records are rejected at load with the tensor named."""
+    rng = np.random.default_rng(4)
+    f = rng.standard_normal((5, 6)).astype(np.float32)
+    f[rng.random(f.shape) < 0.5] = 0
+    f[:, 0] = 1.0
+    f[:, 5] = 2.0
+    base = pfm.csr_record(f)
+
+    def check(rec, msg, name="w"):
+        m = {"name": "v", "inputs": [], "outputs": [], "initializers": {}, "nodes": [],
+             "sparse_initializers": {name: rec}}
+        p = write(tmp_path, "bad.pfm", m)
+        with pytest.raises(session.InvalidModelError, match=msg):
+            session.describe_model(p)
+
+    r = dict(base, indices=base["indices"].copy())
+    r["indices"][1], r["indices"][0] = r["indices"][0], r["indices"][1]
+    check(r, "Sparse initializer 'w': column indices must ascend within row 0")
+    r = dict(base, indices=base["indices"].copy())
+    r["indices"][-1] = 6
+    check(r, "column index 6 out of range")
+    r = dict(base, indptr=base["indptr"].copy())
+    r["indptr"][2] = r["indptr"][3] + 1
+    check(r, "indptr must be non-decreasing")
+    r = dict(base, indptr=base["indptr"].copy())
+    r["indptr"][0] = 1
+    check(r, "indptr")
+    q = pfm.csr_record_int8((5, 6), base["indptr"], base["indices"], np.ones(len(base["values"]), np.int8),
+                            np.ones(4, np.float32), 0)
+    check(q, "int8 values need 1 scale or one per row")
+    q["scales"] = np.array([1, 1, -1, 1, 1], np.float32)
+    check(q, "scales must be positive and finite")
+    w24 = pfm.nm24_record(np.zeros((2, 8), np.int8))
+    w24["positions"] = w24["positions"].copy()
+    w24["positions"][1, 1] = 1 | (1 << 2)  # both kept slots at offset 1
+    check(w24, "2:4 group 3 has invalid positions")
+    with pytest.raises(ValueError, match="more than 2 nonzeros"):
+        pfm.nm24_record(np.ones((1, 4), np.int8))
+    # a sparse record whose name is also a dense initializer
+    m = {"name": "v", "inputs": [], "outputs": [], "initializers": {"w": f}, "nodes": [],
+         "sparse_initializers": {"w": base}}
+    p = write(tmp_path, "dup.pfm", m)
+    with pytest.raises(session.InvalidModelError, match="already a dense initializer"):
+        session.describe_model(p)
