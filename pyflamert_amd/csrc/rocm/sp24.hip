@@ -169,7 +169,14 @@ __global__ __launch_bounds__(256) void k_transpose_i8(const int8_t* __restrict__
 // step.  nkt is a multiple of 4 (packed K is padded to 512), so the loop
 // unrolls over the four stages with each stage's address static, which lets
 // the compiler wait for only the oldest loads (vmcnt) instead of all of them.
+// The last four steps, peeled from the loop, have no stage left to load; they
+// issue the same loads with every lane pointed at one address (one 64-byte
+// request per instruction) into the stage just consumed, so the count of
+// loads per step stays fixed for the vmcnt waits.  (Any branch or select
+// around the loop's loads makes the compiler wait for all of them before
+// every LDS read.)
 constexpr int kI8TileM = 256, kI8TileN = 128;
+constexpr int kI8Waves = 8, kI8Threads = 64 * kI8Waves;
 constexpr int kLdsA = 16 * 64 * 16, kLdsI = 16 * 64 * 4, kLdsB = 128 * 128;
 constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 
@@ -187,7 +194,7 @@ constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 __device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((k >> 4) & 1) << 2); }
 
 template <int OUT, bool XROW>
-__global__ __launch_bounds__(512) void k_sp24_i8(
+__global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
     const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
     float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn) {
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
     __shared__ __attribute__((aligned(1024))) char st1[kStage];
     __shared__ __attribute__((aligned(1024))) char st2[kStage];
     __shared__ __attribute__((aligned(1024))) char st3[kStage];
-    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const int wm = w >> 1, wn = w & 1;
     const int kb = l >> 4, c = l & 15;
     int mt, nt;
@@ -206,11 +213,12 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
         mt = T / ntn;
         nt = T % ntn;
     }
-    const int64_t mb0 = (int64_t)mt * 16;
+    const int64_t mb0 = (int64_t)mt * (kI8TileM / 16);
     const int64_t n0 = (int64_t)nt * kI8TileN;
-    // every wave issues six direct-to-LDS loads per k step: A row blocks w and
-    // w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), B rows
-    // 16w .. 16w + 15 of the step's tile (two 1 KiB runs of 8 rows)
+    // per k step every wave issues six direct-to-LDS loads: A row blocks w
+    // and w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), and
+    // B runs w and w + 8 (8 rows of 128 B each, rows 8j .. 8j + 7 of run j)
+    constexpr int kLoads = 6;
     const v4i* asrc = A + ((mb0 + w) * nkt) * 64 + l;
     const int64_t a_rb8 = (int64_t)8 * nkt * 64;
     const uint32_t* isrc = I + ((mb0 + 2 * w) * nkt) * 64 + l;
@@ -218,7 +226,7 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
     const v4i* bsrc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int n = 16 * w + 8 * i + (l >> 3);
+        const int n = 8 * (w + 8 * i) + (l >> 3);
         if constexpr (XROW) {
             const int chunk = (l & 7) ^ xrow_swizzle(n);
             bsrc[i] = reinterpret_cast<const v4i*>(B + (int64_t)n * ldb + n0 + 16 * chunk);
@@ -237,7 +245,19 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
             __builtin_amdgcn_global_load_lds(isrc + i * i_rb1 + (int64_t)s * 64, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * b_step, PFR_LDS(st + kLdsA + kLdsI + (16 * w + 8 * i) * 128), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * b_step,
+                                             PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 8 * i) * 128), 16, 0, 0);
+    };
+    // the tail's loads: the same instructions, every lane reading A[0]
+    auto issue_tail = [&](char* st) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + (w + 8 * i) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 8 * i) * 128), 16, 0, 0);
     };
     int boff_lo[4], boff_hi[4];  // XT form: the two 16-byte pieces of column n
     // X-row form: transpose read r of this lane starts at row
@@ -304,28 +324,34 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
     // while the MFMAs run on `cur`.
     // vmcnt(12) and lgkmcnt(0): this wave's fragment reads of the previous
     // step have completed before the barrier lets other waves refill a stage
-    constexpr int kWait12 = (12 & 0xF) | (7 << 4) | (0 << 8);
+    // (vmcnt holds 6 bits: low 4 in [3:0], high 2 in [15:14])
+    auto vm_wait = [](int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (0 << 8); };
     Frag fa, fb;
     auto step = [&](Frag& cur, Frag& nxt, char* st_cur, char* st_next, int s) {
-        __builtin_amdgcn_s_waitcnt(kWait12);
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * kLoads));
         __builtin_amdgcn_s_barrier();
-        issue(st_cur, min(s + 4, nkt - 1));  // past the end: reloads the last step, never read
+        if (s >= 0) issue(st_cur, s + 4);  // s is a literal -1 in the peeled tail
+        else issue_tail(st_cur);
         fetch(nxt, st_next);
         mma(cur);
     };
     issue(st0, 0);
-    issue(st1, min(1, nkt - 1));
-    issue(st2, min(2, nkt - 1));
-    issue(st3, min(3, nkt - 1));
-    __builtin_amdgcn_s_waitcnt((18 & 0xF) | ((18 >> 4) << 14) | (7 << 4) | (0xF << 8));  // stage 0 landed
+    issue(st1, 1);
+    issue(st2, 2);
+    issue(st3, 3);
+    __builtin_amdgcn_s_waitcnt(vm_wait(3 * kLoads) | (0xF << 8));  // stage 0 landed (lgkmcnt left alone)
     __builtin_amdgcn_s_barrier();
     fetch(fa, st0);
-    for (int s = 0; s < nkt; s += 4) {
+    for (int s = 0; s < nkt - 4; s += 4) {
         step(fa, fb, st0, st1, s);
         step(fb, fa, st1, st2, s + 1);
         step(fa, fb, st2, st3, s + 2);
         step(fb, fa, st3, st0, s + 3);
     }
+    step(fa, fb, st0, st1, -1);
+    step(fb, fa, st1, st2, -1);
+    step(fa, fb, st2, st3, -1);
+    step(fb, fa, st3, st0, -1);
     __builtin_amdgcn_s_waitcnt(0);  // the trailing reloads have landed
     __builtin_amdgcn_s_barrier();
     if constexpr (OUT == PFR_SP24_OUT_I8) {
@@ -351,8 +377,8 @@ __global__ __launch_bounds__(512) void k_sp24_i8(
         __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
         __builtin_amdgcn_s_barrier();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q16 = t + 512 * i, ml = q16 >> 3, cc = q16 & 7;
+        for (int i = 0; i < 4; ++i) {  // 256 rows x 8 pieces = 4 per thread
+            const int q16 = t + kI8Threads * i, ml = q16 >> 3, cc = q16 & 7;
             const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
             if (m >= M) continue;
             int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
@@ -606,14 +632,14 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     }
     const int ntn = (int)(Np / kI8TileN);
     dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
-#define PFR_SP24_LAUNCH(OUTK)                                                                              \
-    do {                                                                                                   \
-        if (xrow)                                                                                          \
-            hipLaunchKernelGGL((k_sp24_i8<OUTK, true>), grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, B, \
-                               ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
-        else                                                                                               \
-            hipLaunchKernelGGL((k_sp24_i8<OUTK, false>), grid, dim3(512), 0, ctx->stream, nkt, A, W->idx, B, \
-                               ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
+#define PFR_SP24_LAUNCH(OUTK)                                                                                  \
+    do {                                                                                                       \
+        if (xrow)                                                                                              \
+            hipLaunchKernelGGL((k_sp24_i8<OUTK, true>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, \
+                               B, ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_sp24_i8<OUTK, false>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, \
+                               B, ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
     } while (0)
     switch (out_kind) {
         case PFR_SP24_OUT_I32: PFR_SP24_LAUNCH(PFR_SP24_OUT_I32); break;

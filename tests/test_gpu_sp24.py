@@ -43,7 +43,10 @@ def rand_24_int8(rng, M, K, zero_frac=0.0):
     return q, s
 
 
-@pytest.mark.parametrize("M,K,N", [(16, 128, 16), (200, 300, 70), (128, 4096, 512), (33, 257, 1)])
+# (1600, 512, 4096) and (1600, 300, 4000): a grid of more than one
+# workgroup per CU (row-major X and transposed X)
+@pytest.mark.parametrize("M,K,N", [(16, 128, 16), (200, 300, 70), (128, 4096, 512), (33, 257, 1),
+                                   (1600, 512, 4096), (1600, 300, 4000)])
 def test_i8_accumulators_exact(ctx, M, K, N):
     rng = np.random.default_rng(M * 7 + K)
     K4 = (K + 3) // 4 * 4
