@@ -197,6 +197,56 @@ def bench_bert_linears(ctx):
     return res
 
 
+def bench_masks(ctx, cpu):
+    """Session-time mask producers on config 3's weight shape (11008 x 4096,
+    N(0, 1)): the 2:4 mask (NMSparsityPruning) and a 70 % magnitude mask
+    (MagnitudePruning), device pointers, median of 20 calls each; beside
+    them the reference's own compute_mask compiled from its sources (1
+    thread, one call each on the same weight)."""
+    import numpy as np
+    import torch
+
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((11008, 4096)).astype(np.float32)
+    dw = torch.from_numpy(w).cuda()
+    dm = torch.empty_like(dw)
+    n = w.size
+
+    def med(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(20):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return float(np.median(ts))
+
+    res = {"shape": [11008, 4096],
+           "nm_2_4_ms": round(med(lambda: ctx.nm_mask_dev(dw.data_ptr(), n, 2, 4, dm.data_ptr())), 4),
+           "magnitude_0.7_ms": round(med(lambda: ctx.magnitude_mask_dev(dw.data_ptr(), n, 0.7, dm.data_ptr())), 4)}
+    res["nm_gbs"] = round(8 * n / (res["nm_2_4_ms"] * 1e-3) / 1e9, 1)
+    if cpu:
+        from oracle import oracle as O
+
+        if O.have_ref():
+            t0 = time.perf_counter()
+            O.ref_nm_mask(w, 2, 4)
+            res["cpu_reference_nm_2_4_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+            t0 = time.perf_counter()
+            O.ref_magnitude_mask(w, 0.7)
+            res["cpu_reference_magnitude_0.7_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+            res["cpu_note"] = "reference compute_mask compiled from its sources, 1 thread, one call"
+    del dw, dm
+    torch.cuda.empty_cache()
+    log(f"masks: {res}")
+    return res
+
+
 def bench_decode_int8(ctx):
     """Llama-2-7B-shaped decode linear stack: 32 layers x (4 x 4096x4096,
     2 x 11008x4096, 4096x11008), 70 % sparsity with lognormal (sigma 0.5) row
@@ -452,6 +502,7 @@ def main():
         extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
         extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
         extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
+        extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
 
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)

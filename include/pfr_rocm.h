@@ -228,6 +228,27 @@ int pfr_softmax(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
 int pfr_softmax_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
                     int64_t inner, float* y);
 
+/* ---- pruning masks (session-time producers, on the GPU) -------------------- */
+
+/* MagnitudePruning::compute_mask (magnitude_pruning.cpp:22-102): mask[i] =
+ * 1.0f where |w[i]| exceeds the element at index min(floor((double)n * s),
+ * n - 1) of the ascending sort of |w|; then elements equal to that value
+ * are restored (set to 1) in flat order while more than (size_t)((float)n *
+ * s) zeros remain.  s <= 0 gives all ones, s >= 1 all zeros; n == 0 with
+ * 0 < s < 1 is PFR_ERR_INVALID_ARG ("Cannot prune empty weight tensor").
+ * Bit-identical to the reference for finite weights (NaN magnitudes order
+ * above +inf here; the reference's std::sort leaves them unspecified).
+ * Host pointers; _dev: device pointers on the context's stream. */
+int pfr_magnitude_mask(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask);
+int pfr_magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask);
+/* NMSparsityPruning::compute_mask (nm_sparsity.cpp:45-120): in every group
+ * of m consecutive elements (flat order) mask = 1.0f for the n largest |w|,
+ * ties broken as the reference's std::partial_sort breaks them; a last
+ * partial group of g elements keeps ceil((float)(g * n) / m).  0 < n <= m <=
+ * 16.  Host pointers; _dev: device pointers. */
+int pfr_nm_mask(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask);
+int pfr_nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask);
+
 #ifdef __cplusplus
 }
 #endif

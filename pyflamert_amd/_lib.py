@@ -48,6 +48,10 @@ SIGNATURES = {
     "pfr_copy_to_host": (_INT, [_P, _P, _P, _I64]),
     "pfr_csr_upload": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _PP]),
     "pfr_csr_upload_i32": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _PP]),
+    "pfr_magnitude_mask": (_INT, [_P, _P, _I64, C.c_float, _P]),
+    "pfr_magnitude_mask_dev": (_INT, [_P, _P, _I64, C.c_float, _P]),
+    "pfr_nm_mask": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
+    "pfr_nm_mask_dev": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
     "pfr_csr_from_dense": (_INT, [_P, _P, _I64, _I64, _INT, _F, _PP]),
     "pfr_csr_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
     "pfr_csr_free": (_INT, [_P]),

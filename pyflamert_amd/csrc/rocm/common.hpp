@@ -80,8 +80,9 @@ struct pfr_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     // scratch[0..1]: staged inputs, scratch[2]: staged output, scratch[3]:
-    // transposed activations of the Gemm form.
-    pfr::DevBuf scratch[4];
+    // transposed activations of the Gemm form, scratch[4]: the magnitude
+    // mask's selection state (histogram, counters, per-block tie counts).
+    pfr::DevBuf scratch[5];
 };
 
 struct pfr_csr {

@@ -1,0 +1,382 @@
+// Pruning masks on the GPU, bit-identical to the reference's CPU producers.
+//
+// Magnitude (MagnitudePruning::compute_mask, magnitude_pruning.cpp:22-102):
+//   importance |w| (:8-20); threshold = the element at index
+//   min(floor((double)n * s), n - 1) of the ascending sort (:65-73); keep
+//   |w| > threshold (:79-81); then, while more than (size_t)((float)n * s)
+//   zeros remain (:84), restore elements equal to the threshold in flat
+//   order (:91-99).  Here the order statistic is a radix select over the
+//   |w| bit patterns (non-negative floats order as their uint32 bits; NaN,
+//   whose position the reference's std::sort leaves unspecified, sorts above
+//   +inf), four 8-bit passes, each a histogram kernel and a one-block bucket
+//   choice, all on the stream; the tie restore is a flat-order rank of the
+//   elements equal to the threshold (per-block counts, a one-block scan,
+//   then per-element ranks).
+//
+// N:M (NMSparsityPruning::compute_mask, nm_sparsity.cpp:45-120): in every
+//   group of m consecutive elements keep the n of largest |w| (a last,
+//   partial group of g elements keeps ceil((float)(g n) / m)).  Which of
+//   equal magnitudes win is decided by std::partial_sort with the comparator
+//   |w[a]| > |w[b]|; libstdc++ implements partial_sort as a heap select
+//   (bits/stl_algo.h __heap_select: make a heap of the first `keep`
+//   positions, then every later position that compares ahead of the heap
+//   top replaces it) followed by a sort of the heap, which does not change
+//   the kept set.  One thread runs that heap select on its group's indices.
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+
+namespace {
+
+constexpr int kMaskThreads = 256;
+constexpr int kMaskPerThread = 16;
+constexpr int kMaskPerBlock = kMaskThreads * kMaskPerThread;  // 4096 elements
+constexpr int kMaxM = 16;
+
+__device__ __forceinline__ uint32_t mag_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// ---- N:M --------------------------------------------------------------------
+
+// libstdc++'s heap primitives on an index array, with comp(a, b) = "a is
+// kept before b" = |w[a]| > |w[b]| (the heap top is the weakest kept index).
+struct NmHeap {
+    const float* mag;  // |w| of the group
+    int* idx;
+    __device__ bool comp(int a, int b) const { return mag[a] > mag[b]; }
+    __device__ void push(int hole, int top, int value) {
+        int parent = (hole - 1) / 2;
+        while (hole > top && comp(idx[parent], value)) {
+            idx[hole] = idx[parent];
+            hole = parent;
+            parent = (hole - 1) / 2;
+        }
+        idx[hole] = value;
+    }
+    __device__ void adjust(int hole, int len, int value) {
+        const int top = hole;
+        int child = hole;
+        while (child < (len - 1) / 2) {
+            child = 2 * (child + 1);
+            if (comp(idx[child], idx[child - 1])) child--;
+            idx[hole] = idx[child];
+            hole = child;
+        }
+        if ((len & 1) == 0 && child == (len - 2) / 2) {
+            child = 2 * (child + 1);
+            idx[hole] = idx[child - 1];
+            hole = child - 1;
+        }
+        push(hole, top, value);
+    }
+    __device__ void make(int len) {
+        if (len < 2) return;
+        for (int parent = (len - 2) / 2;; --parent) {
+            adjust(parent, len, idx[parent]);
+            if (parent == 0) return;
+        }
+    }
+    // The first `keep` slots of idx end holding the kept indices.
+    __device__ void select(int keep, int len) {
+        make(keep);
+        for (int i = keep; i < len; ++i)
+            if (comp(idx[i], idx[0])) {
+                const int value = idx[i];
+                idx[i] = idx[0];
+                adjust(0, keep, value);
+            }
+    }
+};
+
+__global__ __launch_bounds__(256) void k_nm_mask(const float* __restrict__ w, int64_t total, int n, int m,
+                                                 int64_t groups, float* __restrict__ mask) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= groups) return;
+    const int64_t base = g * m;
+    const int len = (int)min<int64_t>(m, total - base);
+    int keep = n;
+    if (len < m) {
+        // nm_sparsity.cpp:84-86: ceil in float, capped at the group size
+        keep = (int)ceilf((float)(len * n) / (float)m);
+        keep = keep < len ? keep : len;
+    }
+    float mag[kMaxM];
+    int idx[kMaxM];
+    for (int i = 0; i < len; ++i) {
+        mag[i] = fabsf(w[base + i]);
+        idx[i] = i;
+    }
+    NmHeap h{mag, idx};
+    h.select(keep, len);
+    uint32_t kept = 0;
+    for (int j = 0; j < keep; ++j) kept |= 1u << idx[j];
+    for (int i = 0; i < len; ++i) mask[base + i] = (kept >> i) & 1u ? 1.0f : 0.0f;
+}
+
+// ---- magnitude --------------------------------------------------------------
+
+// Selection state, in scratch: hist[256], then the words below, then the
+// per-block tie counts and their exclusive prefix.
+struct MagState {
+    uint32_t hist[256];
+    uint32_t prefix;   // high bits of the threshold found so far
+    uint32_t pad;
+    uint64_t k;        // rank still to find among keys matching the prefix
+    uint64_t zeros;    // keys <= threshold
+    uint64_t target;   // (size_t)((float)n * s)
+};
+
+__global__ __launch_bounds__(256) void k_mag_init(MagState* st, uint64_t k, uint64_t target) {
+    st->hist[threadIdx.x] = 0;
+    if (threadIdx.x == 0) {
+        st->prefix = 0;
+        st->k = k;
+        st->zeros = 0;
+        st->target = target;
+    }
+}
+
+// Histogram of digit `pass` (bits 31-8*pass .. 24-8*pass) over keys whose
+// higher bits equal the prefix.
+__global__ __launch_bounds__(kMaskThreads) void k_mag_hist(const float* __restrict__ w, int64_t n, int pass,
+                                                            MagState* __restrict__ st) {
+    __shared__ uint32_t h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int shift = 24 - 8 * pass;
+    const uint32_t prefix = st->prefix;
+    const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock;
+    for (int i = 0; i < kMaskPerThread; ++i) {
+        const int64_t e = start + (int64_t)i * kMaskThreads + threadIdx.x;
+        if (e < n) {
+            const uint32_t key = mag_bits(w[e]);
+            const bool match = pass == 0 || (key >> (shift + 8)) == prefix;
+            if (match) atomicAdd(&h[(key >> shift) & 255u], 1u);
+        }
+    }
+    __syncthreads();
+    if (h[threadIdx.x]) atomicAdd(&st->hist[threadIdx.x], h[threadIdx.x]);
+}
+
+// One block: the bucket holding rank k, then the histogram cleared for the
+// next pass.
+__global__ __launch_bounds__(256) void k_mag_pick(MagState* st) {
+    __shared__ uint64_t cum[256];
+    const int t = threadIdx.x;
+    cum[t] = st->hist[t];
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
+        const uint64_t v = t >= off ? cum[t - off] : 0;
+        __syncthreads();
+        cum[t] += v;
+        __syncthreads();
+    }
+    const uint64_t k = st->k;
+    const uint64_t before = t ? cum[t - 1] : 0;
+    const bool here = before <= k && k < cum[t];
+    __syncthreads();
+    if (here) {
+        st->prefix = (st->prefix << 8) | (uint32_t)t;
+        st->k = k - before;
+    }
+    st->hist[t] = 0;
+}
+
+// Per block: keys equal to the threshold (in the block's flat range) and,
+// across blocks, keys at or below it.
+__global__ __launch_bounds__(kMaskThreads) void k_mag_count(const float* __restrict__ w, int64_t n,
+                                                             MagState* __restrict__ st, uint32_t* __restrict__ ties) {
+    __shared__ uint32_t s_tie, s_le;
+    if (threadIdx.x == 0) s_tie = s_le = 0;
+    __syncthreads();
+    const uint32_t thr = st->prefix;
+    const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock + (int64_t)threadIdx.x * kMaskPerThread;
+    uint32_t tie = 0, le = 0;
+    for (int i = 0; i < kMaskPerThread; ++i) {
+        const int64_t e = start + i;
+        if (e < n) {
+            const uint32_t key = mag_bits(w[e]);
+            tie += key == thr;
+            le += key <= thr;
+        }
+    }
+    if (tie) atomicAdd(&s_tie, tie);
+    if (le) atomicAdd(&s_le, le);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ties[blockIdx.x] = s_tie;
+        if (s_le) atomicAdd(reinterpret_cast<unsigned long long*>(&st->zeros), (unsigned long long)s_le);
+    }
+}
+
+// One block: exclusive prefix of the per-block tie counts, in place.
+__global__ __launch_bounds__(1024) void k_mag_scan(uint32_t* ties, int64_t nblocks) {
+    __shared__ uint64_t part[1024];
+    __shared__ uint64_t carry;
+    const int t = threadIdx.x;
+    if (t == 0) carry = 0;
+    __syncthreads();
+    for (int64_t b0 = 0; b0 < nblocks; b0 += 1024) {
+        const int64_t b = b0 + t;
+        const uint64_t v = b < nblocks ? ties[b] : 0;
+        part[t] = v;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const uint64_t u = t >= off ? part[t - off] : 0;
+            __syncthreads();
+            part[t] += u;
+            __syncthreads();
+        }
+        const uint64_t excl = carry + part[t] - v;
+        __syncthreads();
+        if (b < nblocks) ties[b] = (uint32_t)excl;  // ranks stay below 2^32 (n < 2^32)
+        if (t == 1023) carry += part[1023];
+        __syncthreads();
+    }
+}
+
+// mask = key > threshold, plus the first (zeros - target) threshold ties in
+// flat order.  Each thread owns 16 consecutive elements, so flat order is
+// (block, thread, element) order.
+__global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restrict__ w, int64_t n,
+                                                             const MagState* __restrict__ st,
+                                                             const uint32_t* __restrict__ tie_off,
+                                                             float* __restrict__ mask) {
+    __shared__ uint32_t scan[kMaskThreads];
+    const int t = threadIdx.x;
+    const uint32_t thr = st->prefix;
+    const uint64_t zeros = st->zeros, target = st->target;
+    const uint64_t restore = zeros > target ? zeros - target : 0;
+    const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock + (int64_t)t * kMaskPerThread;
+    uint32_t keys[kMaskPerThread];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < kMaskPerThread; ++i) {
+        const int64_t e = start + i;
+        keys[i] = e < n ? mag_bits(w[e]) : 0u;
+        mine += (e < n) && keys[i] == thr;
+    }
+    scan[t] = mine;
+    __syncthreads();
+    for (int off = 1; off < kMaskThreads; off <<= 1) {
+        const uint32_t u = t >= off ? scan[t - off] : 0;
+        __syncthreads();
+        scan[t] += u;
+        __syncthreads();
+    }
+    uint64_t rank = (uint64_t)tie_off[blockIdx.x] + scan[t] - mine;
+#pragma unroll
+    for (int i = 0; i < kMaskPerThread; ++i) {
+        const int64_t e = start + i;
+        if (e >= n) break;
+        float v = keys[i] > thr ? 1.0f : 0.0f;
+        if (keys[i] == thr) {
+            if (rank < restore) v = 1.0f;
+            ++rank;
+        }
+        mask[e] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fill(float* __restrict__ y, int64_t n, float v) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = v;
+}
+
+void fill_dev(pfr_ctx* ctx, float* y, int64_t n, float v) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_fill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, y, n, v);
+    PFR_HIP(hipGetLastError());
+}
+
+void magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float s, float* mask) {
+    pfr::require(n >= 0, "negative element count");
+    pfr::require(!std::isnan(s), "sparsity is NaN");
+    pfr::require(n == 0 || mask != nullptr, "null mask");
+    if (s <= 0.0f) return fill_dev(ctx, mask, n, 1.0f);  // magnitude_pruning.cpp:31-37
+    if (s >= 1.0f) return fill_dev(ctx, mask, n, 0.0f);  // :39-45
+    if (n == 0) throw pfr::Error(PFR_ERR_INVALID_ARG, "Cannot prune empty weight tensor");  // :52-54
+    pfr::require(w != nullptr, "null weights");
+    pfr::require(n < ((int64_t)1 << 32), "more than 2^32 - 1 elements");
+    // :69-72 index in double, clamped; :84 target in float
+    uint64_t k = (uint64_t)std::floor((double)n * (double)s);
+    if (k > (uint64_t)(n - 1)) k = (uint64_t)(n - 1);
+    const uint64_t target = (uint64_t)((float)n * s);
+    const int64_t nblocks = (n + kMaskPerBlock - 1) / kMaskPerBlock;
+    char* scr = static_cast<char*>(ctx->scratch[4].ensure(sizeof(MagState) + 4 * (size_t)nblocks));
+    MagState* st = reinterpret_cast<MagState*>(scr);
+    uint32_t* ties = reinterpret_cast<uint32_t*>(scr + sizeof(MagState));
+    hipStream_t q = ctx->stream;
+    hipLaunchKernelGGL(k_mag_init, dim3(1), dim3(256), 0, q, st, k, target);
+    for (int pass = 0; pass < 4; ++pass) {
+        hipLaunchKernelGGL(k_mag_hist, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, pass, st);
+        hipLaunchKernelGGL(k_mag_pick, dim3(1), dim3(256), 0, q, st);
+    }
+    hipLaunchKernelGGL(k_mag_count, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties);
+    hipLaunchKernelGGL(k_mag_scan, dim3(1), dim3(1024), 0, q, ties, nblocks);
+    hipLaunchKernelGGL(k_mag_write, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties, mask);
+    PFR_HIP(hipGetLastError());
+}
+
+void nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask) {
+    pfr::require(total >= 0, "negative element count");
+    // NMSparsityPruning's constructor (nm_sparsity.cpp:9-18) rejects n > m
+    // and zeros; groups of more than 16 are outside this kernel
+    pfr::require(n > 0 && m > 0 && n <= m, "N:M needs 0 < n <= m");
+    pfr::require(m <= kMaxM, "N:M groups larger than 16 are not supported");
+    if (total == 0) return;
+    pfr::require(w && mask, "null w/mask");
+    const int64_t groups = (total + m - 1) / m;
+    hipLaunchKernelGGL(k_nm_mask, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, ctx->stream, w, total, n,
+                       m, groups, mask);
+    PFR_HIP(hipGetLastError());
+}
+
+// Host-pointer form: stage, run, copy back, synchronise.
+template <class F>
+void host_mask_call(pfr_ctx* ctx, const float* w, int64_t n, float* mask, F&& f) {
+    if (n == 0) return f(nullptr, nullptr);
+    pfr::require(w && mask, "null w/mask");
+    float* dw = static_cast<float*>(ctx->scratch[0].ensure((size_t)n * 4));
+    float* dm = static_cast<float*>(ctx->scratch[2].ensure((size_t)n * 4));
+    PFR_HIP(hipMemcpyAsync(dw, w, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    f(dw, dm);
+    PFR_HIP(hipMemcpyAsync(mask, dm, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    PFR_HIP(hipStreamSynchronize(ctx->stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int pfr_magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        magnitude_mask_dev(ctx, w, n, sparsity, mask);
+    });
+}
+
+int pfr_magnitude_mask(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        host_mask_call(ctx, w, n, mask, [&](float* dw, float* dm) { magnitude_mask_dev(ctx, dw, n, sparsity, dm); });
+    });
+}
+
+int pfr_nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        nm_mask_dev(ctx, w, total, n, m, mask);
+    });
+}
+
+int pfr_nm_mask(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(total >= 0, "negative element count");
+        host_mask_call(ctx, w, total, mask, [&](float* dw, float* dm) { nm_mask_dev(ctx, dw, total, n, m, dm); });
+    });
+}
+
+}  // extern "C"

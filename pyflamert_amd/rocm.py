@@ -118,6 +118,29 @@ class Context:
                                      alpha, beta, _ptr(C_), csz, _ptr(Y), _MODES[mode]))
         return Y
 
+    # -- pruning masks ---------------------------------------------------
+    def magnitude_mask(self, w, sparsity):
+        """MagnitudePruning::compute_mask on the GPU (float32 0/1 mask of
+        w's shape)."""
+        w = np.ascontiguousarray(w, np.float32)
+        mask = np.empty_like(w)
+        check(self._lib.pfr_magnitude_mask(self.handle, _ptr(w), w.size, float(sparsity), _ptr(mask)))
+        return mask
+
+    def magnitude_mask_dev(self, w_ptr, n, sparsity, mask_ptr):
+        check(self._lib.pfr_magnitude_mask_dev(self.handle, w_ptr, n, float(sparsity), mask_ptr))
+
+    def nm_mask(self, w, n=2, m=4):
+        """NMSparsityPruning::compute_mask on the GPU: n kept of every m
+        consecutive elements in flat order."""
+        w = np.ascontiguousarray(w, np.float32)
+        mask = np.empty_like(w)
+        check(self._lib.pfr_nm_mask(self.handle, _ptr(w), w.size, int(n), int(m), _ptr(mask)))
+        return mask
+
+    def nm_mask_dev(self, w_ptr, total, n, m, mask_ptr):
+        check(self._lib.pfr_nm_mask_dev(self.handle, w_ptr, total, int(n), int(m), mask_ptr))
+
     def gemm_csr_dev(self, A_ptr, Mb, K, BT, Y_ptr, alpha=1.0, beta=1.0, C_ptr=None, c_size=0,
                      transA=False, mode="strict", relu=False):
         if relu:
