@@ -206,6 +206,24 @@ int pfr_sp24_gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X,
                          float out_scale, int32_t out_zp, void* Y,
                          int64_t ldy);
 
+/* The int8 2:4 GEMM with the activation as (Dynamic)QuantizeLinear leaves
+ * it: int8 (x_dtype PFR_I8) or uint8 (PFR_U8) with a zero point:
+ *   acc[m, n] = sum_k W[m, k] * (X[k, n] - zero_point)   (exact, int32)
+ * then out_kind as above with x_scale: quantization::quantized_matmul
+ * (quant_ops.cpp:387-506, which reads uint8 as uint8) with a per-channel
+ * weight scale.  The scale and zero point are host values, or (_dev, when
+ * x_scale_dev / x_zero_point_dev are non-NULL) device scalars such as the
+ * outputs of pfr_dynamic_quantize_linear_dev on the same stream.  K < 2^17.
+ * Host form: X and Y host pointers, X rows N apart. */
+int pfr_sp24_gemm_q(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype,
+                    int64_t N, float x_scale, int32_t x_zero_point, int out_kind,
+                    float out_scale, int32_t out_zp, void* Y);
+int pfr_sp24_gemm_q_dev(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype,
+                        int64_t N, int64_t ldx, float x_scale, int32_t x_zero_point,
+                        const float* x_scale_dev, const uint8_t* x_zero_point_dev,
+                        int out_kind, float out_scale, int32_t out_zp, void* Y,
+                        int64_t ldy);
+
 /* Y[M, N] (float) = W[M, K] . X[K, N] with bf16 operands and fp32
  * accumulation: cpu_gemm on bf16-rounded operands
  * (half_types.cpp:132-174 then math.cpp:377-438), within the bf16
@@ -227,6 +245,23 @@ int pfr_softmax(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
                 int64_t inner, float* y);
 int pfr_softmax_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
                     int64_t inner, float* y);
+
+/* ---- dynamic activation quantization -------------------------------------- */
+
+/* DynamicQuantizeLinear (cpu_dynamic_quantize_linear, quantized_ops.cpp:
+ * 251-278): uint8 asymmetric per-tensor parameters from the finite minimum
+ * and maximum of x (compute_dynamic_params, quant_ops.cpp:288-327, and
+ * QuantParams::compute_from_minmax, quant_params.cpp:14-55), then y =
+ * clamp((int)round(x * (1 / scale)) + zero_point, 0, 255) (quantize_tensor,
+ * quant_ops.cpp:15-47).  Bit-exact.  Host pointers: y[n], *scale,
+ * *zero_point; a non-finite scale fails with PFR_ERR_INVALID_ARG
+ * ("QuantParams::per_tensor: scale must be positive and finite").  _dev:
+ * device pointers, and (nullable) a device int32 *status that becomes 1 in
+ * that case, 0 otherwise. */
+int pfr_dynamic_quantize_linear(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y,
+                                float* scale, uint8_t* zero_point);
+int pfr_dynamic_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y,
+                                    float* scale, uint8_t* zero_point, int32_t* status);
 
 /* ---- pruning masks (session-time producers, on the GPU) -------------------- */
 

@@ -48,6 +48,8 @@ SIGNATURES = {
     "pfr_copy_to_host": (_INT, [_P, _P, _P, _I64]),
     "pfr_csr_upload": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _PP]),
     "pfr_csr_upload_i32": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _INT, _P, _PP]),
+    "pfr_dynamic_quantize_linear": (_INT, [_P, _P, _I64, _P, _P, _P]),
+    "pfr_dynamic_quantize_linear_dev": (_INT, [_P, _P, _I64, _P, _P, _P, _P]),
     "pfr_magnitude_mask": (_INT, [_P, _P, _I64, C.c_float, _P]),
     "pfr_magnitude_mask_dev": (_INT, [_P, _P, _I64, C.c_float, _P]),
     "pfr_nm_mask": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
@@ -66,6 +68,8 @@ SIGNATURES = {
     "pfr_sp24_free": (_INT, [_P]),
     "pfr_sp24_gemm_i8": (_INT, [_P, _P, _P, _I64, _F, _INT, _F, _I32, _P]),
     "pfr_sp24_gemm_i8_dev": (_INT, [_P, _P, _P, _I64, _I64, _F, _INT, _F, _I32, _P, _I64]),
+    "pfr_sp24_gemm_q": (_INT, [_P, _P, _P, _INT, _I64, _F, _I32, _INT, _F, _I32, _P]),
+    "pfr_sp24_gemm_q_dev": (_INT, [_P, _P, _P, _INT, _I64, _I64, _F, _I32, _P, _P, _INT, _F, _I32, _P, _I64]),
     "pfr_sp24_gemm_bf16": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_sp24_gemm_bf16_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64]),
     "pfr_relu": (_INT, [_P, _P, _I64, _P]),

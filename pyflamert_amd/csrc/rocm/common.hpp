@@ -51,6 +51,13 @@ int guarded(F&& f) {
     }
 }
 
+// x86 static_cast<int32_t>(float): truncation, 0x80000000 for NaN or out of
+// range (what the reference's quantize_tensor and requant do on its build
+// target, quant_ops.cpp:42-47).
+__device__ __forceinline__ int32_t f2i_trunc_x86(float r) {
+    return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
+}
+
 // Grow-only device buffer owned by a context.
 struct DevBuf {
     void* p = nullptr;

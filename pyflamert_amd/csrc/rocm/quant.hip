@@ -1,0 +1,169 @@
+// DynamicQuantizeLinear on the GPU (cpu_dynamic_quantize_linear,
+// quantized_ops.cpp:251-278): per-tensor uint8 asymmetric parameters from
+// the data, then the quantized tensor.
+//   params  compute_dynamic_params(x, UInt8, symmetric = false)
+//           (quant_ops.cpp:288-327): min and max over the finite elements;
+//           none finite, or an empty tensor: scale 1, zero point 0; else
+//           compute_from_minmax (quant_params.cpp:14-55): |max - min| <
+//           1e-8 gives scale 1, zero point 0; otherwise scale = (max - min) /
+//           255, zero point = clamp(0 - (int)round(min / scale), 0, 255),
+//           scale floored at 1e-10; a non-finite scale is the error of
+//           QuantParams::per_tensor (quant_params.hpp:60-82).
+//   values  quantize_tensor (quant_ops.cpp:15-47): inv = 1 / scale,
+//           q = (int)round(x * inv) + zero point, clamped to [0, 255].
+// The reduction order of min and max cannot change them except for the sign
+// of a zero, which does not reach the parameters (max - min, round(min /
+// scale) and the comparisons are the same for +0 and -0), so a parallel
+// reduction gives the reference's parameters exactly.
+#include <cfloat>
+#include <cmath>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kRedThreads = 256;
+constexpr int kRedBlocks = 1024;  // partial min/max pairs
+
+struct DqlState {
+    float part_min[kRedBlocks];
+    float part_max[kRedBlocks];
+    float inv_scale;
+    int32_t zp;
+};
+
+__global__ __launch_bounds__(kRedThreads) void k_dql_minmax(const float* __restrict__ x, int64_t n,
+                                                             DqlState* __restrict__ st) {
+    __shared__ float smin[kRedThreads], smax[kRedThreads];
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kRedThreads) {
+        const float v = x[i];
+        if (isfinite(v)) {
+            mn = v < mn ? v : mn;
+            mx = mx < v ? v : mx;
+        }
+    }
+    smin[threadIdx.x] = mn;
+    smax[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = kRedThreads / 2; off > 0; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float a = smin[threadIdx.x + off], b = smax[threadIdx.x + off];
+            smin[threadIdx.x] = a < smin[threadIdx.x] ? a : smin[threadIdx.x];
+            smax[threadIdx.x] = smax[threadIdx.x] < b ? b : smax[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        st->part_min[blockIdx.x] = smin[0];
+        st->part_max[blockIdx.x] = smax[0];
+    }
+}
+
+// One block: the parameters, written to the op's scale and zero-point
+// outputs and kept (inverse scale, zero point) for the quantize kernel.
+// status (optional): 0, or 1 when the scale is not finite (the error
+// QuantParams::per_tensor raises).
+__global__ __launch_bounds__(kRedThreads) void k_dql_params(int nparts, DqlState* __restrict__ st,
+                                                             float* __restrict__ scale_out,
+                                                             uint8_t* __restrict__ zp_out, int32_t* status) {
+    __shared__ float smin[kRedThreads], smax[kRedThreads];
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    for (int i = threadIdx.x; i < nparts; i += kRedThreads) {
+        const float a = st->part_min[i], b = st->part_max[i];
+        mn = a < mn ? a : mn;
+        mx = mx < b ? b : mx;
+    }
+    smin[threadIdx.x] = mn;
+    smax[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = kRedThreads / 2; off > 0; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float a = smin[threadIdx.x + off], b = smax[threadIdx.x + off];
+            smin[threadIdx.x] = a < smin[threadIdx.x] ? a : smin[threadIdx.x];
+            smax[threadIdx.x] = smax[threadIdx.x] < b ? b : smax[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x != 0) return;
+    const float min_val = smin[0], max_val = smax[0];
+    float scale = 1.0f;
+    int32_t zp = 0;
+    if (nparts > 0 && !(min_val > max_val) && !(fabsf(max_val - min_val) < 1e-8f)) {
+        scale = (max_val - min_val) / 255.0f;
+        zp = (int32_t)(0u - (uint32_t)pfr::f2i_trunc_x86(roundf(min_val / scale)));  // x86 wraps
+        zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
+        if (scale < 1e-10f) scale = 1e-10f;
+    }
+    if (status) *status = (scale > 0.0f && isfinite(scale)) ? 0 : 1;
+    st->inv_scale = 1.0f / scale;
+    st->zp = zp;
+    *scale_out = scale;
+    *zp_out = (uint8_t)zp;
+}
+
+__global__ __launch_bounds__(256) void k_dql_quant(const float* __restrict__ x, int64_t n,
+                                                   const DqlState* __restrict__ st, uint8_t* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float inv = st->inv_scale;
+    const int32_t zp = st->zp;
+    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(x[i] * inv)) + (uint32_t)zp);
+    q = q < 0 ? 0 : (q > 255 ? 255 : q);
+    y[i] = (uint8_t)q;
+}
+
+void dql_dev(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y, float* scale, uint8_t* zp, int32_t* status) {
+    pfr::require(n >= 0, "negative element count");
+    pfr::require(scale && zp, "null scale/zero-point output");
+    pfr::require(n == 0 || (x && y), "null x/y");
+    DqlState* st = static_cast<DqlState*>(ctx->scratch[4].ensure(sizeof(DqlState)));
+    const int nparts = n == 0 ? 0 : (int)std::min<int64_t>(kRedBlocks, (n + kRedThreads - 1) / kRedThreads);
+    hipStream_t q = ctx->stream;
+    if (nparts) hipLaunchKernelGGL(k_dql_minmax, dim3(nparts), dim3(kRedThreads), 0, q, x, n, st);
+    hipLaunchKernelGGL(k_dql_params, dim3(1), dim3(kRedThreads), 0, q, nparts, st, scale, zp, status);
+    if (n) hipLaunchKernelGGL(k_dql_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, q, x, n, st, y);
+    PFR_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+int pfr_dynamic_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y, float* scale,
+                                    uint8_t* zero_point, int32_t* status) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        dql_dev(ctx, x, n, y, scale, zero_point, status);
+    });
+}
+
+int pfr_dynamic_quantize_linear(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y, float* scale,
+                                uint8_t* zero_point) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        pfr::require(scale && zero_point, "null scale/zero-point output");
+        pfr::require(n == 0 || (x && y), "null x/y");
+        float* dx = static_cast<float*>(ctx->scratch[0].ensure((size_t)n * 4 + 4));
+        uint8_t* dy = static_cast<uint8_t*>(ctx->scratch[2].ensure((size_t)n + 64));
+        float* dscale = reinterpret_cast<float*>(dy + ((n + 15) / 16) * 16);
+        int32_t* dstatus = reinterpret_cast<int32_t*>(dscale + 1);
+        uint8_t* dzp = reinterpret_cast<uint8_t*>(dstatus + 1);
+        if (n) PFR_HIP(hipMemcpyAsync(dx, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+        dql_dev(ctx, dx, n, dy, dscale, dzp, dstatus);
+        int32_t status = 0;
+        PFR_HIP(hipMemcpyAsync(&status, dstatus, 4, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
+        if (status)
+            throw pfr::Error(PFR_ERR_INVALID_ARG, "QuantParams::per_tensor: scale must be positive and finite");
+        if (n) PFR_HIP(hipMemcpyAsync(y, dy, (size_t)n, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipMemcpyAsync(scale, dscale, 4, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipMemcpyAsync(zero_point, dzp, 1, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+}  // extern "C"

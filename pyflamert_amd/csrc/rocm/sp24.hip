@@ -37,6 +37,7 @@ struct pfr_sp24 {
     void* a = nullptr;        // compressed values, [Mp/16][Kp/KT][64][16 B]
     uint32_t* idx = nullptr;  // [Mp/16][Kp/KT (int8) | Kp/128 (bf16)][64]
     float* w_scale = nullptr; // [M] (per-tensor scales expanded)
+    int32_t* row_sum = nullptr;  // int8: [Mp] sum over k of W[m, k] (the zero-point correction)
 };
 
 namespace {
@@ -49,7 +50,7 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 void free_sp24(pfr_sp24* w) {
     if (!w) return;
-    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale})
+    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale, (void*)w->row_sum})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -94,12 +95,6 @@ __global__ __launch_bounds__(256) void k_transpose_pad(const T* __restrict__ X, 
         const int nn = (t >> 6) + 4 * i, kk = t & 63;
         XT[(n0 + nn) * Kp + k0 + kk] = tile[kk][nn];
     }
-}
-
-// x86 static_cast<int32_t>(float): truncation, 0x80000000 for NaN / out of
-// range (what the reference's requant does on its build target).
-__device__ __forceinline__ int32_t f2i_trunc_x86(float r) {
-    return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
 }
 
 // XT[n][k] (Np x Kp) = X[k][n] for int8, zero outside K x N.  A wave owns a
@@ -193,11 +188,19 @@ constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 // chunk gives lane t the eight k values k0 .. k0+7 of column chunk + t.
 __device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((k >> 4) & 1) << 2); }
 
+// Activation zero point: acc = sum_k w[m, k] (x[k, n] - zp) =
+// sum_k w x - zp * row_sum[m], exact in int32.  A uint8 activation arrives
+// as x - 128 (sign bit flipped by k_flip_sign), so its correction uses
+// zp - 128 (zp_shift = 128).  The activation's scale and zero point come
+// from xs / x_zp or, when xs_dev / zp_dev are set, from device scalars (the
+// outputs of a DynamicQuantizeLinear on the same stream).
 template <int OUT, bool XROW>
 __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
     const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
-    float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn) {
+    float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn, int32_t x_zp,
+    int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
+    const int32_t* __restrict__ row_sum) {
     __shared__ __attribute__((aligned(1024))) char st0[kStage];
     __shared__ __attribute__((aligned(1024))) char st1[kStage];
     __shared__ __attribute__((aligned(1024))) char st2[kStage];
@@ -352,8 +355,14 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     step(fb, fa, st1, st2, -1);
     step(fa, fb, st2, st3, -1);
     step(fb, fa, st3, st0, -1);
-    __builtin_amdgcn_s_waitcnt(0);  // the trailing reloads have landed
+    __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
     __builtin_amdgcn_s_barrier();
+    const float xs_eff = xs_dev ? *xs_dev : xs;
+    const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
+    const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
+    // the exact accumulator of row m (int32 wrap-around arithmetic; the true
+    // value is within int32 for K < 2^17)
+    auto exact = [&](int32_t a, int m) { return zcorr ? (int32_t)((uint32_t)a - zcorr * (uint32_t)row_sum[m]) : a; };
     if constexpr (OUT == PFR_SP24_OUT_I8) {
         // requantise into an LDS tile [256][128] (stage 0), then store 16-byte row pieces
         char* tile = st0;
@@ -363,12 +372,12 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
             for (int r = 0; r < 4; ++r) {
                 const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
                 const int m = (int)(mb0 * 16) + ml;
-                const float sab = m < M ? ws[m] * xs : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
+                const float sab = m < M ? ws[m] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float f = (float)acc[i][j][r] * sab;
+                    const float f = (float)exact(acc[i][j][r], m) * sab;
                     const float prod = f * inv_out;
-                    int32_t q = (int32_t)((uint32_t)f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
+                    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
                     q = q < -128 ? -128 : (q > 127 ? 127 : q);
                     tile[ml * 128 + wn * 64 + 16 * j + c] = (char)q;
                 }
@@ -397,12 +406,12 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
                 const int m = (int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r;
                 if (m >= M) continue;
                 float sab = 1.0f;
-                if constexpr (OUT == PFR_SP24_OUT_F32) sab = ws[m] * xs;
+                if constexpr (OUT == PFR_SP24_OUT_F32) sab = ws[m] * xs_eff;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int64_t n = n0 + wn * 64 + 16 * j + c;
                     if (n >= N) continue;
-                    const int32_t v = acc[i][j][r];
+                    const int32_t v = exact(acc[i][j][r], m);
                     const int64_t o = (int64_t)m * ldy + n;
                     if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
                     else static_cast<float*>(Y)[o] = (float)v * sab;
@@ -472,6 +481,14 @@ __global__ __launch_bounds__(256) void k_sp24_bf16(
         }
 }
 
+// x - 128 as int8 for uint8 x (rows of n bytes, ld apart, to a compact copy)
+__global__ __launch_bounds__(256) void k_flip_sign(const uint8_t* __restrict__ X, int64_t K, int64_t N,
+                                                   int64_t ldx, uint8_t* __restrict__ Y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= K * N) return;
+    Y[i] = X[(i / N) * ldx + i % N] ^ 0x80u;
+}
+
 // ---- host -----------------------------------------------------------------
 
 pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
@@ -515,10 +532,18 @@ pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
         w->Mp = Mp;
         w->Kp = Kp;
         w->dtype = PFR_I8;
+        std::vector<int32_t> rs((size_t)Mp, 0);
+        for (int64_t r = 0; r < M; ++r) {
+            int64_t sum = 0;
+            for (int64_t k = 0; k < K; ++k) sum += W[r * K + k];
+            rs[(size_t)r] = (int32_t)sum;  // |sum| <= 128 K < 2^31
+        }
         PFR_HIP(hipMalloc(&w->a, a.size()));
         PFR_HIP(hipMalloc(&w->idx, ix.size() * 4));
+        PFR_HIP(hipMalloc(&w->row_sum, rs.size() * 4));
         PFR_HIP(hipMemcpy(w->a, a.data(), a.size(), hipMemcpyHostToDevice));
         PFR_HIP(hipMemcpy(w->idx, ix.data(), ix.size() * 4, hipMemcpyHostToDevice));
+        PFR_HIP(hipMemcpy(w->row_sum, rs.data(), rs.size() * 4, hipMemcpyHostToDevice));
         return w;
     } catch (...) {
         free_sp24(w);
@@ -593,20 +618,35 @@ T* stage_xt(pfr_ctx* ctx, const T* X, int64_t K, int64_t N, int64_t ldx, int64_t
     return xt;
 }
 
+// x_u8: X holds uint8 values.  x_zp: the activation zero point, or
+// (zp_dev set) a device uint8 holding it; x_scale likewise with xs_dev.
 void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, int64_t ldx, float x_scale,
-                 int out_kind, float out_scale, int32_t out_zp, void* Y, int64_t ldy) {
+                 int out_kind, float out_scale, int32_t out_zp, void* Y, int64_t ldy, bool x_u8 = false,
+                 int32_t x_zp = 0, const float* xs_dev = nullptr, const uint8_t* zp_dev = nullptr) {
     check_i8(W);
+    pfr::require(W->K < (1 << 17), "K must be below 2^17 for exact int32 accumulation");
+    pfr::require(x_u8 ? (x_zp >= 0 && x_zp <= 255) : (x_zp >= -128 && x_zp <= 127),
+                 "activation zero point outside the activation type's range");
     pfr::require(N >= 0 && N < INT32_MAX, "bad column count");
     pfr::require(ldx >= N && ldy >= N, "leading dimension smaller than N");
     pfr::require(out_kind >= PFR_SP24_OUT_I32 && out_kind <= PFR_SP24_OUT_I8, "unknown output kind");
     if (W->M == 0 || N == 0) return;
     pfr::require(X != nullptr && Y != nullptr, "null X/Y");
     float inv_out = 1.0f;
-    if (out_kind != PFR_SP24_OUT_I32)
+    if (out_kind != PFR_SP24_OUT_I32 && !xs_dev)
         pfr::require(x_scale > 0.0f && std::isfinite(x_scale), "x_scale must be positive and finite");
     if (out_kind == PFR_SP24_OUT_I8) {
         pfr::require(out_scale > 0.0f && std::isfinite(out_scale), "output scale must be positive and finite");
         inv_out = 1.0f / out_scale;  // quant_ops.cpp:41
+    }
+    if (x_u8) {
+        // the signed MFMA takes x - 128; the zero-point correction adds the 128 back
+        uint8_t* xs8 = static_cast<uint8_t*>(ctx->scratch[1].ensure((size_t)(W->K * N) + 16));
+        hipLaunchKernelGGL(k_flip_sign, dim3((unsigned)((W->K * N + 255) / 256)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const uint8_t*>(X), W->K, N, ldx, xs8);
+        PFR_HIP(hipGetLastError());
+        X = reinterpret_cast<const int8_t*>(xs8);
+        ldx = N;
     }
     const int64_t Kp = W->Kp;
     const int nkt = (int)(Kp / 128);
@@ -632,14 +672,14 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     }
     const int ntn = (int)(Np / kI8TileN);
     dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
-#define PFR_SP24_LAUNCH(OUTK)                                                                                  \
-    do {                                                                                                       \
-        if (xrow)                                                                                              \
-            hipLaunchKernelGGL((k_sp24_i8<OUTK, true>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, \
-                               B, ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
-        else                                                                                                   \
-            hipLaunchKernelGGL((k_sp24_i8<OUTK, false>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, \
-                               B, ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn); \
+#define PFR_SP24_LAUNCH_X(OUTK, XR)                                                                             \
+    hipLaunchKernelGGL((k_sp24_i8<OUTK, XR>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, B, ldb,    \
+                       (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn, x_zp,            \
+                       x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
+#define PFR_SP24_LAUNCH(OUTK)                      \
+    do {                                           \
+        if (xrow) PFR_SP24_LAUNCH_X(OUTK, true);   \
+        else PFR_SP24_LAUNCH_X(OUTK, false);       \
     } while (0)
     switch (out_kind) {
         case PFR_SP24_OUT_I32: PFR_SP24_LAUNCH(PFR_SP24_OUT_I32); break;
@@ -647,6 +687,7 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
         default: PFR_SP24_LAUNCH(PFR_SP24_OUT_I8);
     }
 #undef PFR_SP24_LAUNCH
+#undef PFR_SP24_LAUNCH_X
     PFR_HIP(hipGetLastError());
 }
 
@@ -743,6 +784,39 @@ int pfr_sp24_gemm_i8(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N
         void* dY = ctx->scratch[2].ensure(yb);
         if (xb) PFR_HIP(hipMemcpyAsync(dX, X, xb, hipMemcpyHostToDevice, s));
         gemm_i8_dev(ctx, W, dX, N, N, x_scale, out_kind, out_scale, out_zp, dY, N);
+        PFR_HIP(hipMemcpyAsync(Y, dY, yb, hipMemcpyDeviceToHost, s));
+        PFR_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int pfr_sp24_gemm_q_dev(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype, int64_t N,
+                        int64_t ldx, float x_scale, int32_t x_zero_point, const float* x_scale_dev,
+                        const uint8_t* x_zero_point_dev, int out_kind, float out_scale, int32_t out_zp, void* Y,
+                        int64_t ldy) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(x_dtype == PFR_I8 || x_dtype == PFR_U8, "activation must be int8 or uint8");
+        gemm_i8_dev(ctx, W, static_cast<const int8_t*>(X), N, ldx, x_scale, out_kind, out_scale, out_zp, Y, ldy,
+                    x_dtype == PFR_U8, x_zero_point, x_scale_dev, x_zero_point_dev);
+    });
+}
+
+int pfr_sp24_gemm_q(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype, int64_t N, float x_scale,
+                    int32_t x_zero_point, int out_kind, float out_scale, int32_t out_zp, void* Y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        check_i8(W);
+        pfr::require(x_dtype == PFR_I8 || x_dtype == PFR_U8, "activation must be int8 or uint8");
+        pfr::require(N >= 0, "bad column count");
+        const size_t esz = out_kind == PFR_SP24_OUT_I8 ? 1 : 4;
+        const size_t xb = (size_t)(W->K * N), yb = esz * (size_t)(W->M * N);
+        if (yb == 0) return;
+        pfr::require(Y != nullptr && (X != nullptr || xb == 0), "null X/Y");
+        hipStream_t s = ctx->stream;
+        int8_t* dX = static_cast<int8_t*>(ctx->scratch[0].ensure(xb ? xb : 4));
+        void* dY = ctx->scratch[2].ensure(yb);
+        if (xb) PFR_HIP(hipMemcpyAsync(dX, X, xb, hipMemcpyHostToDevice, s));
+        gemm_i8_dev(ctx, W, dX, N, N, x_scale, out_kind, out_scale, out_zp, dY, N, x_dtype == PFR_U8, x_zero_point);
         PFR_HIP(hipMemcpyAsync(Y, dY, yb, hipMemcpyDeviceToHost, s));
         PFR_HIP(hipStreamSynchronize(s));
     });

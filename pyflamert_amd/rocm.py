@@ -118,6 +118,17 @@ class Context:
                                      alpha, beta, _ptr(C_), csz, _ptr(Y), _MODES[mode]))
         return Y
 
+    # -- dynamic activation quantization ----------------------------------
+    def dynamic_quantize_linear(self, x):
+        """DynamicQuantizeLinear: (uint8 y of x's shape, float32 scale,
+        uint8 zero point)."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(x.shape, np.uint8)
+        scale = np.zeros(1, np.float32)
+        zp = np.zeros(1, np.uint8)
+        check(self._lib.pfr_dynamic_quantize_linear(self.handle, _ptr(x), x.size, _ptr(y), _ptr(scale), _ptr(zp)))
+        return y, scale[0], zp[0]
+
     # -- pruning masks ---------------------------------------------------
     def magnitude_mask(self, w, sparsity):
         """MagnitudePruning::compute_mask on the GPU (float32 0/1 mask of
@@ -233,6 +244,29 @@ class Sp24Weight:
     def gemm_i8_dev(self, X_ptr, N, Y_ptr, x_scale=1.0, out="i32", out_scale=1.0, out_zp=0, ldx=None, ldy=None):
         check(self.ctx._lib.pfr_sp24_gemm_i8_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, x_scale,
                                                  _SP24_OUT[out], out_scale, out_zp, Y_ptr, ldy or N))
+
+    def gemm_q(self, X, x_scale=1.0, x_zp=0, out="f32", out_scale=1.0, out_zp=0):
+        """Y = W . (X - x_zp) for int8 or uint8 X [K, N] (the activation as
+        QuantizeLinear / DynamicQuantizeLinear leave it)."""
+        X = np.ascontiguousarray(X)
+        if X.dtype not in (np.int8, np.uint8):
+            raise ValueError("activation must be int8 or uint8")
+        if X.shape[0] != self.K:
+            raise ValueError("quantized_matmul: inner dimensions must match")
+        N = X.shape[1]
+        dt = {"i32": np.int32, "f32": np.float32, "i8": np.int8}[out]
+        Y = np.empty((self.M, N), dt)
+        xdt = _lib.PFR_U8 if X.dtype == np.uint8 else _lib.PFR_I8
+        check(self.ctx._lib.pfr_sp24_gemm_q(self.ctx.handle, self.handle, _ptr(X), xdt, N, x_scale, int(x_zp),
+                                            _SP24_OUT[out], out_scale, out_zp, _ptr(Y)))
+        return Y
+
+    def gemm_q_dev(self, X_ptr, x_u8, N, Y_ptr, x_scale=1.0, x_zp=0, x_scale_ptr=None, x_zp_ptr=None, out="f32",
+                   out_scale=1.0, out_zp=0, ldx=None, ldy=None):
+        xdt = _lib.PFR_U8 if x_u8 else _lib.PFR_I8
+        check(self.ctx._lib.pfr_sp24_gemm_q_dev(self.ctx.handle, self.handle, X_ptr, xdt, N, ldx or N, x_scale,
+                                                int(x_zp), x_scale_ptr, x_zp_ptr, _SP24_OUT[out], out_scale, out_zp,
+                                                Y_ptr, ldy or N))
 
     def gemm_bf16(self, X):
         """Y (float32) = W . X for bf16-bit X [K, N] (uint16)."""

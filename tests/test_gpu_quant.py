@@ -1,0 +1,139 @@
+"""The quantized path's GPU pieces against the reference.
+
+DynamicQuantizeLinear: bit-exact against the oracle's compute_dynamic_params
++ quantize_tensor (pinned by the quant golden vectors) and, where it is
+built, the reference's own cpu_dynamic_quantize_linear op.  The 2:4 GEMM on
+quantized activations: int8 or uint8 X with a zero point, per-tensor or
+per-channel weight scales, bit-exact against quantization::quantized_matmul
+(oracle, pinned by the qmatmul golden vectors); a per-channel scale is the
+per-tensor product of that row with its own scale, so each row is checked
+against the oracle's single-row product.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pyflamert_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from pyflamert_amd import rocm
+
+    c = rocm.Context(0)
+    yield c
+    c.close()
+
+
+def dql_oracle(x):
+    s, z = O.orc_dynamic_params(x, O.U8, symmetric=False)
+    q = O.orc_quantize(x, s, z, O.U8)
+    return q.astype(np.uint8), np.float32(s), np.uint8(z)
+
+
+def dql_cases(rng):
+    yield "normal", rng.standard_normal((64, 300)).astype(np.float32)
+    yield "positive", (rng.random(5000) * 7 + 3).astype(np.float32)  # zero point clamps to 0
+    yield "negative", (-rng.random(777) * 2 - 1).astype(np.float32)  # zero point clamps to 255
+    x = rng.standard_normal(10000).astype(np.float32)
+    x[::97] = np.nan
+    x[::101] = np.inf
+    x[::103] = -np.inf
+    yield "non-finite", x
+    yield "constant", np.full(333, 2.5, np.float32)  # |max - min| < 1e-8: scale 1
+    yield "all non-finite", np.array([np.nan, np.inf, -np.inf], np.float32)
+    yield "one", np.array([-3.25], np.float32)
+    yield "empty", np.zeros(0, np.float32)
+    yield "large", rng.standard_normal(3_000_001).astype(np.float32) * 40
+    yield "tiny range", (1000.0 + rng.random(4096) * 1e-3).astype(np.float32)
+
+
+def test_dynamic_quantize_linear(ctx):
+    rng = np.random.default_rng(3)
+    for name, x in dql_cases(rng):
+        say(f"DynamicQuantizeLinear {name} n={x.size}")
+        y, s, z = ctx.dynamic_quantize_linear(x)
+        ry, rs, rz = dql_oracle(x.ravel())
+        assert np.array_equal(y.ravel(), ry), name
+        assert np.array_equal(np.float32(s).view(np.uint32), rs.view(np.uint32)), (name, s, rs)
+        assert z == rz, (name, z, rz)
+        if O.have_ref() and x.size:
+            # the reference op itself (its first output, the quantized tensor)
+            raw, shape = O.ref_run_op("DynamicQuantizeLinear", [x.ravel()], out_bytes=x.size)
+            assert shape == (x.size,) and np.array_equal(raw[: x.size], y.ravel()), name
+
+
+def test_dynamic_quantize_linear_scale_error(ctx):
+    # max - min overflows to +inf: QuantParams::per_tensor rejects the scale
+    x = np.array([-3e38, 3e38], np.float32)
+    with pytest.raises(_lib.InvalidArgument, match="scale must be positive and finite"):
+        ctx.dynamic_quantize_linear(x)
+
+
+def rand_24(rng, M, K):
+    w = rng.standard_normal((M, K)).astype(np.float32)
+    w = O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(M, K))
+    s, _ = O.orc_dynamic_params_per_channel(w.reshape(1, M, K))
+    q = O.orc_quantize(w, s, np.zeros(M, np.int32), O.I8, (1, M, K))
+    return q, s.astype(np.float32)
+
+
+@pytest.mark.parametrize("M,K,N", [(200, 512, 128), (96, 300, 70), (256, 4096, 512)])
+def test_sp24_quantized_activation(ctx, M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    q, s = rand_24(rng, M, K)
+    x = rng.standard_normal((K, N)).astype(np.float32) * 3
+    xq, xs, xz = dql_oracle(x.ravel())
+    xq = xq.reshape(K, N)
+    say(f"2:4 GEMM on uint8 activations M={M} K={K} N={N} zp={xz}")
+    # per-tensor weight scale: quantization::quantized_matmul exactly
+    W1 = ctx.sp24_pack(q, s[:1])
+    Y = W1.gemm_q(xq, float(xs), int(xz), out="f32")
+    assert np.array_equal(bits(Y), bits(O.orc_quantized_matmul(q, xq, s[0], xs, 0, int(xz))))
+    acc = W1.gemm_q(xq, float(xs), int(xz), out="i32")
+    ref = (q.astype(np.int64) @ (xq.astype(np.int64) - int(xz))).astype(np.int32)
+    assert np.array_equal(acc, ref)
+    # per-channel weight scales: row m is the per-tensor product with s[m]
+    W = ctx.sp24_pack(q, s)
+    Y = W.gemm_q(xq, float(xs), int(xz), out="f32")
+    rows = rng.choice(M, size=min(M, 24), replace=False)
+    for m in rows:
+        r = O.orc_quantized_matmul(q[m:m + 1], xq, s[m], xs, 0, int(xz))
+        assert np.array_equal(bits(Y[m:m + 1]), bits(r)), m
+    # int8 activations with a nonzero zero point, and requantised output
+    xi = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    Yi = W1.gemm_q(xi, 0.05, -7, out="f32")
+    assert np.array_equal(bits(Yi), bits(O.orc_quantized_matmul(q, xi, s[0], np.float32(0.05), 0, -7)))
+
+
+def test_sp24_device_scale_and_zero_point(ctx):
+    """The activation's scale and zero point read from device scalars (as
+    pfr_dynamic_quantize_linear_dev leaves them) give the host-value result."""
+    import torch
+
+    rng = np.random.default_rng(9)
+    M, K, N = 512, 1024, 256
+    q, s = rand_24(rng, M, K)
+    x = rng.standard_normal((K, N)).astype(np.float32)
+    xq, xs, xz = dql_oracle(x.ravel())
+    W = ctx.sp24_pack(q, s)
+    dX = torch.from_numpy(xq.reshape(K, N)).cuda()
+    dS = torch.tensor([xs], dtype=torch.float32, device="cuda")
+    dZ = torch.tensor([xz], dtype=torch.uint8, device="cuda")
+    dY = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    W.gemm_q_dev(dX.data_ptr(), True, N, dY.data_ptr(), x_scale_ptr=dS.data_ptr(), x_zp_ptr=dZ.data_ptr())
+    ctx.synchronize()
+    assert np.array_equal(bits(dY.cpu().numpy()), bits(W.gemm_q(xq.reshape(K, N), float(xs), int(xz))))
