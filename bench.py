@@ -197,6 +197,56 @@ def bench_bert_linears(ctx):
     return res
 
 
+def bench_dynamic_int8(ctx):
+    """The dynamic int8 path of config 3's shape: X fp32 4096 x 512 ->
+    DynamicQuantizeLinear (uint8, scale and zero point on the device) ->
+    2:4 int8 GEMM with per-channel weight scales (11008 x 4096, top-2-of-4)
+    -> fp32 Y; what one rewritten MatMul(W, X) node runs in a
+    quantization="dynamic_int8" session.  Median of 100 pairs."""
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import workloads
+
+    M, K, N = 11008, 4096, 512
+    q, s = workloads.sp24_int8_weight(M, K, seed=3)
+    W = ctx.sp24_pack(q, s)
+    dX = torch.from_numpy(workloads.dense_normal((K, N), 1.0, seed=4)).cuda()
+    dXq = torch.empty((K, N), dtype=torch.uint8, device="cuda")
+    dS = torch.empty(1, dtype=torch.float32, device="cuda")
+    dZ = torch.empty(1, dtype=torch.uint8, device="cuda")
+    dSt = torch.empty(1, dtype=torch.int32, device="cuda")
+    dY = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    from pyflamert_amd._lib import check as _lib_check
+
+    L = ctx._lib
+
+    def pair():
+        _lib_check(L.pfr_dynamic_quantize_linear_dev(ctx.handle, dX.data_ptr(), K * N, dXq.data_ptr(),
+                                                     dS.data_ptr(), dZ.data_ptr(), dSt.data_ptr()))
+        W.gemm_q_dev(dXq.data_ptr(), True, N, dY.data_ptr(), x_scale_ptr=dS.data_ptr(), x_zp_ptr=dZ.data_ptr())
+
+    for _ in range(10):
+        pair()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(100):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        pair()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = float(np.median(ts))
+    res = {"ms_per_node": round(ms, 5), "shape": [M, K, N],
+           "dense_equiv_tops": round(2 * M * N * K / (ms * 1e-3) / 1e12, 1),
+           "note": "DynamicQuantizeLinear of X + 2:4 GEMM on uint8 X, per-channel scales, fp32 out; one weight copy"}
+    W.free()
+    log(f"dynamic int8 node: {res}")
+    return res
+
+
 def bench_masks(ctx, cpu):
     """Session-time mask producers on config 3's weight shape (11008 x 4096,
     N(0, 1)): the 2:4 mask (NMSparsityPruning) and a 70 % magnitude mask
@@ -503,6 +553,7 @@ def main():
         extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
         extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
         extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
+        extra["dynamic_int8_node_11008x4096x512"] = bench_dynamic_int8(ctx)
 
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)

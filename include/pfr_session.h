@@ -34,9 +34,14 @@ const char* pfr_session_last_error(void);
  * optimization_level: the reference's OptLevel (types.hpp:119-124).  0 None
  * runs node by node through the rocm:: OpFuncs; 1 Basic runs the
  * device-resident plan; 2 Extended (the reference's default) and 3 All add
- * operator fusion (Relu into the preceding pruned product). */
+ * operator fusion (Relu into the preceding pruned product).
+ * quantization: NULL or "" for none; "dynamic_int8" rewrites every MatMul(W,
+ * X) with a float 2:4-pruned initializer W into DynamicQuantizeLinear(X) +
+ * QuantizedMatMul(per-row int8 W, ...) (the reference's QuantMode::
+ * DynamicInt8 with per-channel weights). */
 int pfr_session_create(const char* model_path, const char* device, int strict_math_mode, int math_mode,
-                       int device_id, int optimization_level, pfr_session** out);
+                       int device_id, int optimization_level, const char* quantization,
+                       pfr_session** out);
 int pfr_session_destroy(pfr_session* s);
 int pfr_session_io_count(pfr_session* s, int* n_inputs, int* n_outputs);
 /* Name, DType code and shape (-1 = dynamic, at most 16 dims) of input or
@@ -65,6 +70,10 @@ int pfr_session_device_plan(pfr_session* s, int* device_resident, int* steps);
  * pfr_model_resave loads in_path and writes it back with this runtime's
  * writer (initializers and attributes in name order). */
 int pfr_model_describe(const char* path, char* buf, int64_t cap, int64_t* needed);
+/* The quantization rewrite offline: load in_path, apply mode ("dynamic_int8",
+ * as the session option does), write out_path (version 2 when it adds 2:4
+ * records); *rewritten (nullable) gets the number of MatMul nodes replaced. */
+int pfr_model_quantize(const char* in_path, const char* out_path, const char* mode, int* rewritten);
 int pfr_model_resave(const char* in_path, const char* out_path);
 
 #ifdef __cplusplus

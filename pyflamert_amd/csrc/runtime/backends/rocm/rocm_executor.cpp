@@ -200,8 +200,24 @@ std::vector<std::string> RocmExecutor::get_supported_ops() const {
 //  Gemm(A, W[, C])          W f32 2-D  -> CSR of op(W)^T
 //  MatMul(A, W)             W f32 2-D  -> CSR of W^T
 //  MatMul(W, B)             W f32 2-D, B an activation -> CSR of W
-//  QuantizedMatMul(W, B)    W int8 2-D 2:4 along K, zero points 0
-//                           -> 2:4 compressed, per-tensor scale a_scale
+//  QuantizedMatMul(W, B)    W int8 2-D 2:4 along K, a_zero_point 0
+//                           -> 2:4 compressed, per-tensor scale a_scale or
+//                              per-channel a_scales
+namespace {
+// The weight scales of a QuantizedMatMul: a_scales (one per row) when set,
+// else the per-tensor a_scale.
+std::vector<float> weight_scales(const Node& n, int64_t rows) {
+    auto v = n.get_attr<std::vector<float>>("a_scales");
+    if (v) {
+        if ((int64_t)v->size() != rows)
+            throw std::invalid_argument("QuantizedMatMul: a_scales has " + std::to_string(v->size()) +
+                                        " entries for " + std::to_string(rows) + " rows");
+        return *v;
+    }
+    return {n.get_attr<float>("a_scale", 1.0f)};
+}
+}  // namespace
+
 void RocmExecutor::prepare(const Graph& graph) {
     if (prepared_for_ == &graph) return;
     release_weights();
@@ -230,12 +246,12 @@ void RocmExecutor::prepare(const Graph& graph) {
                 w.csr = upload_sparse_csr(ctx_, *sparse(0), false);
                 w.kind = DeviceWeight::CsrA;
             } else if (n->op_type() == "QuantizedMatMul" && sparse(0) &&
-                       sparse(0)->format == SparseInitializer::Nm24 &&
-                       n->get_attr<int64_t>("a_zero_point", 0) == 0 && n->get_attr<int64_t>("b_zero_point", 0) == 0) {
+                       sparse(0)->format == SparseInitializer::Nm24 && n->get_attr<int64_t>("a_zero_point", 0) == 0) {
                 // expanded for the packer only; the record is 2:4 by construction
                 const Tensor A = sparse(0)->to_dense();
-                const float a_scale = n->get_attr<float>("a_scale", 1.0f);
-                pfr_check(pfr_sp24_pack(ctx_, A.shape()[0], A.shape()[1], A.data(), PFR_I8, &a_scale, 1, &w.sp24));
+                const std::vector<float> sc = weight_scales(*n, A.shape()[0]);
+                pfr_check(pfr_sp24_pack(ctx_, A.shape()[0], A.shape()[1], A.data(), PFR_I8, sc.data(),
+                                        (int64_t)sc.size(), &w.sp24));
                 w.kind = DeviceWeight::Sp24A;
             } else if (n->op_type() == "Gemm" && init(1) && is_f32_matrix(*init(1))) {
                 const Tensor& B = *init(1);
@@ -253,12 +269,13 @@ void RocmExecutor::prepare(const Graph& graph) {
                 w.kind = DeviceWeight::CsrA;
             } else if (n->op_type() == "QuantizedMatMul" && init(0) && init(0)->ndim() == 2 &&
                        (init(0)->dtype() == DType::Int8 || init(0)->dtype() == DType::UInt8) &&
-                       n->get_attr<int64_t>("a_zero_point", 0) == 0 && n->get_attr<int64_t>("b_zero_point", 0) == 0) {
+                       n->get_attr<int64_t>("a_zero_point", 0) == 0) {
                 const Tensor& A = *init(0);
-                const float a_scale = n->get_attr<float>("a_scale", 1.0f);
+                const std::vector<float> sc = weight_scales(*n, A.shape()[0]);
                 // UInt8 data is read as int8, as the reference kernel does
                 // (src/backends/cpu/ops/quantized_ops.cpp:143-144).
-                const int st = pfr_sp24_pack(ctx_, A.shape()[0], A.shape()[1], A.data(), PFR_I8, &a_scale, 1, &w.sp24);
+                const int st = pfr_sp24_pack(ctx_, A.shape()[0], A.shape()[1], A.data(), PFR_I8, sc.data(),
+                                             (int64_t)sc.size(), &w.sp24);
                 if (st == PFR_OK) w.kind = DeviceWeight::Sp24A;
             }
         } catch (const std::exception& e) {
@@ -291,9 +308,10 @@ void RocmExecutor::build_plan(const Graph& graph) {
     std::vector<PlanStep> steps;
     for (const auto& np : order) {
         const Node* n = np.get();
-        if (n->outputs().size() != 1) return;
-        const DeviceWeight* w = weight(n);
         const std::string& op = n->op_type();
+        const bool dynq = op == "DynamicQuantizeLinear" && n->inputs().size() == 1 && n->outputs().size() == 3;
+        if (!dynq && n->outputs().size() != 1) return;
+        const DeviceWeight* w = weight(n);
         PlanStep st{PlanStep::Relu, n, false, n->outputs()[0]};
         if (op == "Gemm" && w && w->kind == DeviceWeight::CsrB)
             st.op = PlanStep::Gemm;
@@ -307,6 +325,8 @@ void RocmExecutor::build_plan(const Graph& graph) {
             st.op = PlanStep::Relu;
         else if (op == "Softmax" && n->inputs().size() == 1)
             st.op = PlanStep::Softmax;
+        else if (dynq)
+            st.op = PlanStep::DynQuant;
         else
             return;
         steps.push_back(st);
@@ -363,6 +383,7 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                                                const std::vector<std::string>& names) {
     StreamDrain drain{ctx_};
     std::unordered_map<std::string, DevTensor> live(constants_);
+    std::vector<std::pair<const Node*, void*>> statuses;  // DynamicQuantizeLinear scale checks
     for (const auto& kv : input_feed) {
         const Tensor& t = kv.second;
         const int64_t bytes = (int64_t)t.size_bytes();
@@ -480,12 +501,63 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 if (b.shape.size() != 2)
                     throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D int8 initializer A that "
                                              "is 2:4 sparse along K, zero points 0, and a 2-D B");
-                const float b_scale = n->get_attr<float>("b_scale", 1.0f);
+                // two inputs: B's bytes as int8, scale and zero point attributes
+                // (quantized_ops.cpp:87-90, :143-144); four: B's scale and zero
+                // point as device tensors, uint8 B as uint8
+                float b_scale = n->get_attr<float>("b_scale", 1.0f);
+                int32_t b_zp = (int32_t)n->get_attr<int64_t>("b_zero_point", 0);
+                const float* s_dev = nullptr;
+                const uint8_t* z_dev = nullptr;
+                pfr_dtype bdt = PFR_I8;
+                if (in.size() >= 4) {
+                    const DevTensor& s = act_in(2);
+                    const DevTensor& z = act_in(3);
+                    if (s.dtype != DType::Float32 || numel(s.shape) != 1)
+                        throw std::invalid_argument("QuantizedMatMul: b_scale input must be one float32");
+                    if ((z.dtype != DType::UInt8 && z.dtype != DType::Int8) || numel(z.shape) != 1)
+                        throw std::invalid_argument("QuantizedMatMul: b_zero_point input must be one int8 or uint8");
+                    s_dev = static_cast<const float*>(s.p);
+                    if (z.dtype == DType::UInt8) {
+                        z_dev = static_cast<const uint8_t*>(z.p);
+                    } else {
+                        int8_t zv = 0;
+                        pfr_check(pfr_copy_to_host(ctx_, &zv, z.p, 1));
+                        b_zp = zv;
+                    }
+                    bdt = b.dtype == DType::UInt8 ? PFR_U8 : PFR_I8;
+                }
                 const int64_t M = a.shape()[0], N = b.shape[1];
                 out.shape = {M, N};
                 out.p = device_buffer(st.out, M * N * 4);
-                pfr_check(pfr_sp24_gemm_i8_dev(ctx_, weight(n)->sp24, static_cast<const int8_t*>(b.p), N, N, b_scale,
-                                               PFR_SP24_OUT_F32, 1.0f, 0, out.p, N));
+                pfr_check(pfr_sp24_gemm_q_dev(ctx_, weight(n)->sp24, b.p, bdt, N, N, b_scale, b_zp, s_dev, z_dev,
+                                              PFR_SP24_OUT_F32, 1.0f, 0, out.p, N));
+                break;
+            }
+            case PlanStep::DynQuant: {
+                // quantized_ops.cpp:251-278; outputs y (uint8), scale [1], zero point [1]
+                const DevTensor& x = act_in(0);
+                if (x.dtype != DType::Float32)
+                    throw std::invalid_argument("DynamicQuantizeLinear: input must be Float32");
+                const int64_t cnt = numel(x.shape);
+                const auto& outs = n->outputs();
+                DevTensor sc, zp;
+                sc.p = device_buffer(outs[1], 4);
+                sc.shape = {1};
+                sc.dtype = DType::Float32;
+                zp.p = device_buffer(outs[2], 1);
+                zp.shape = {1};
+                zp.dtype = DType::UInt8;
+                out.p = device_buffer(st.out, cnt);
+                out.shape = x.shape;
+                out.dtype = DType::UInt8;
+                // the status word (a non-finite scale) sits after the scale
+                void* status = device_buffer(std::string("\x01status:") + n->name(), 4);
+                pfr_check(pfr_dynamic_quantize_linear_dev(ctx_, static_cast<const float*>(x.p), cnt,
+                                                          static_cast<uint8_t*>(out.p), static_cast<float*>(sc.p),
+                                                          static_cast<uint8_t*>(zp.p), static_cast<int32_t*>(status)));
+                statuses.push_back({n, status});
+                live[outs[1]] = sc;
+                live[outs[2]] = zp;
                 break;
             }
             case PlanStep::Relu: {
@@ -547,6 +619,12 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
     }
     pfr_check(pfr_synchronize(ctx_));
     drain.armed = false;
+    for (const auto& ns : statuses) {
+        int32_t status = 0;
+        pfr_check(pfr_copy_to_host(ctx_, &status, ns.second, 4));
+        if (status)
+            throw BackendError("QuantParams::per_tensor: scale must be positive and finite", ns.first->name());
+    }
     return results;
 }
 

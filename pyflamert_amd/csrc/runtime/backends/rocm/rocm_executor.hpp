@@ -13,8 +13,8 @@
 //    its compressed form, never expanded to a dense host tensor;
 //  * inputs and initializers are not deep-copied on every run;
 //  * from OptLevel::Basic up, a graph whose every node has a device kernel
-//    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, Relu, Softmax) runs as a
-//    device-resident plan:
+//    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, DynamicQuantizeLinear,
+//    Relu, Softmax) runs as a device-resident plan:
 //    graph inputs are copied to the GPU once per run, the remaining
 //    initializers once per graph, activations stay in device buffers
 //    between nodes, from OptLevel::Extended up a Gemm/MatMul whose only
@@ -68,7 +68,7 @@ public:
 private:
     // One kernel launch of the device plan.
     struct PlanStep {
-        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax } op;
+        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant } op;
         const Node* node;
         bool fuse_relu = false;  // the following Relu runs in this step's epilogue
         std::string out;         // tensor the step writes (the Relu's output when fused)

@@ -104,7 +104,14 @@ std::vector<Tensor> rocm_gemm(const std::vector<const Tensor*>& in, const OpCont
 }
 
 // QuantizedMatMul with a 2:4 int8 initializer A (quantized_ops.cpp:77-167):
-// out = (float)acc * (a_scale * b_scale), int32 accumulation.
+// out = (float)acc * (a_scale * b_scale), acc = sum_k A[m, k] (B[k, n] -
+// b_zero_point), int32 accumulation.  With two inputs B's bytes are read as
+// int8 whatever its type, as the reference kernel reads them
+// (quantized_ops.cpp:143-144), and b_scale / b_zero_point are attributes.
+// With four inputs (what the dynamic int8 rewrite emits) B's scale and zero
+// point are the tensors in[2] and in[3], and a uint8 B is read as uint8
+// (quantization::quantized_matmul, quant_ops.cpp:468-490).  A per-channel
+// float-vector attribute a_scales replaces a_scale.
 std::vector<Tensor> rocm_qmatmul(const std::vector<const Tensor*>& in, const OpContext& ctx) {
     need_inputs(in, 2, "QuantizedMatMul");
     RocmExecutor& ex = exec();
@@ -124,12 +131,39 @@ std::vector<Tensor> rocm_qmatmul(const std::vector<const Tensor*>& in, const OpC
     if (!w || w->kind != RocmExecutor::DeviceWeight::Sp24A || b.ndim() != 2)
         throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D int8 initializer A that is 2:4 "
                                  "sparse along K, zero points 0, and a 2-D B");
-    const float b_scale = ctx.node->get_attr<float>("b_scale", 1.0f);
+    float b_scale = ctx.node->get_attr<float>("b_scale", 1.0f);
+    int64_t b_zp = ctx.node->get_attr<int64_t>("b_zero_point", 0);
+    pfr_dtype bdt = PFR_I8;
+    if (in.size() >= 4) {
+        const Tensor& s = *in[2];
+        const Tensor& z = *in[3];
+        if (s.dtype() != DType::Float32 || s.num_elements() != 1)
+            throw std::invalid_argument("QuantizedMatMul: b_scale input must be one float32");
+        if ((z.dtype() != DType::UInt8 && z.dtype() != DType::Int8) || z.num_elements() != 1)
+            throw std::invalid_argument("QuantizedMatMul: b_zero_point input must be one int8 or uint8");
+        b_scale = s.data_ptr<float>()[0];
+        b_zp = z.dtype() == DType::UInt8 ? (int64_t) static_cast<const uint8_t*>(z.data())[0]
+                                         : (int64_t) static_cast<const int8_t*>(z.data())[0];
+        bdt = b.dtype() == DType::UInt8 ? PFR_U8 : PFR_I8;
+    }
     const int64_t M = a.shape()[0], N = b.shape()[1];
     Tensor out({M, N}, DType::Float32);
-    pfr_check(pfr_sp24_gemm_i8(ex.ctx(), w->sp24, static_cast<const int8_t*>(b.data()), N, b_scale,
-                               PFR_SP24_OUT_F32, 1.0f, 0, out.data()));
+    pfr_check(pfr_sp24_gemm_q(ex.ctx(), w->sp24, b.data(), bdt, N, b_scale, (int32_t)b_zp, PFR_SP24_OUT_F32, 1.0f, 0,
+                              out.data()));
     return {std::move(out)};
+}
+
+// DynamicQuantizeLinear (quantized_ops.cpp:251-278): uint8 tensor, scale
+// [1] float32, zero point [1] uint8.
+std::vector<Tensor> rocm_dynamic_quantize_linear(const std::vector<const Tensor*>& in, const OpContext&) {
+    need_inputs(in, 1, "DynamicQuantizeLinear");
+    const Tensor& x = *in[0];
+    if (x.dtype() != DType::Float32) throw std::invalid_argument("DynamicQuantizeLinear: input must be Float32");
+    Tensor y(x.shape(), DType::UInt8), s({1}, DType::Float32), z({1}, DType::UInt8);
+    pfr_check(pfr_dynamic_quantize_linear(exec().ctx(), x.data_ptr<float>(), x.num_elements(),
+                                          static_cast<uint8_t*>(y.data()), s.data_ptr<float>(),
+                                          static_cast<uint8_t*>(z.data())));
+    return {std::move(y), std::move(s), std::move(z)};
 }
 
 std::vector<Tensor> rocm_relu(const std::vector<const Tensor*>& in, const OpContext&) {
@@ -165,6 +199,7 @@ struct RocmOpsRegistrar {
         r.register_op("rocm::MatMul", rocm_matmul);
         r.register_op("rocm::Gemm", rocm_gemm);
         r.register_op("rocm::QuantizedMatMul", rocm_qmatmul);
+        r.register_op("rocm::DynamicQuantizeLinear", rocm_dynamic_quantize_linear);
         r.register_op("rocm::Relu", rocm_relu);
         r.register_op("rocm::Softmax", rocm_softmax);
     }

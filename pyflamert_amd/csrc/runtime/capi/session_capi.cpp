@@ -7,6 +7,7 @@
 #include "pfr_session.h"
 #include "pyflame_rt/errors.hpp"
 #include "pyflame_rt/pyflame_format.hpp"
+#include "pyflame_rt/quantize.hpp"
 #include "pyflame_rt/session.hpp"
 #include "../backends/rocm/rocm_executor.hpp"
 
@@ -66,7 +67,7 @@ extern "C" {
 const char* pfr_session_last_error(void) { return g_err.c_str(); }
 
 int pfr_session_create(const char* path, const char* device, int strict_math_mode, int math_mode, int device_id,
-                       int optimization_level, pfr_session** out) {
+                       int optimization_level, const char* quantization, pfr_session** out) {
     return guard([&] {
         if (!out || !path || !device) throw PyFlameRTError("null argument");
         *out = nullptr;
@@ -79,6 +80,7 @@ int pfr_session_create(const char* path, const char* device, int strict_math_mod
             throw PyFlameRTError("optimization_level must be 0 (None) .. 3 (All), got " +
                                  std::to_string(optimization_level));
         o.optimization_level = static_cast<OptLevel>(optimization_level);
+        o.quantization = quantization ? quantization : "";
         auto s = std::make_unique<pfr_session>();
         s->sess = std::make_unique<InferenceSession>(path, o);
         *out = s.release();
@@ -264,6 +266,23 @@ int pfr_model_describe(const char* path, char* buf, int64_t cap, int64_t* needed
             std::memcpy(buf, s.data(), n);
             buf[n] = '\0';
         }
+    });
+}
+
+int pfr_model_quantize(const char* in_path, const char* out_path, const char* mode, int* rewritten) {
+    return guard([&] {
+        if (!in_path || !out_path || !mode) throw PyFlameRTError("null argument");
+        if (std::string(mode) != "dynamic_int8")
+            throw PyFlameRTError(std::string("Invalid quantization mode: ") + mode + " (supported: dynamic_int8)");
+        auto g = load_model(in_path);
+        auto errs = g->validate();
+        if (!errs.empty()) throw ValidationError(errs);
+        QuantizeStats st;
+        auto q = quantize_dynamic_int8(*g, &st);
+        errs = q->validate();
+        if (!errs.empty()) throw ValidationError(errs);
+        save_model(*q, out_path);
+        if (rewritten) *rewritten = st.rewritten;
     });
 }
 

@@ -23,6 +23,12 @@ struct SessionOptions {
     // multiply-add in the same order).
     int rocm_math_mode = 0;
     int rocm_device_id = 0;
+    // The reference's SessionOptions::quantization (a QuantConfig,
+    // include/pyflame_rt/options.hpp) reduced to its mode: "" for none, or
+    // "dynamic_int8" (QuantMode::DynamicInt8 with per-channel weights): the
+    // 2:4-pruned MatMul(W, X) nodes run as DynamicQuantizeLinear +
+    // QuantizedMatMul (quantize.hpp).
+    std::string quantization;
 
     std::vector<std::string> validate() const;
 };

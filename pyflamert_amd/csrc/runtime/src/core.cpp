@@ -261,6 +261,8 @@ std::vector<std::string> SessionOptions::validate() const {
         e.push_back("num_threads must be <= 256 (got " + std::to_string(num_threads) + ")");
     if (rocm_math_mode != 0 && rocm_math_mode != 1) e.push_back("rocm_math_mode must be 0 (strict) or 1 (fast)");
     if (rocm_device_id < 0) e.push_back("rocm_device_id must be >= 0");
+    if (!quantization.empty() && quantization != "dynamic_int8")
+        e.push_back("Invalid quantization mode: " + quantization + " (supported: dynamic_int8)");
     return e;
 }
 

@@ -9,6 +9,7 @@
 #include "../backends/rocm/rocm_executor.hpp"
 #include "pyflame_rt/errors.hpp"
 #include "pyflame_rt/pyflame_format.hpp"
+#include "pyflame_rt/quantize.hpp"
 
 namespace pyflame_rt {
 
@@ -24,6 +25,13 @@ InferenceSession::InferenceSession(const std::string& model_path, SessionOptions
     graph_ = load_model(model_path);
     auto verr = graph_->validate();
     if (!verr.empty()) throw ValidationError(verr);
+    // the reference applies quantization after the graph passes
+    // (src/session.cpp:38-41)
+    if (options_.quantization == "dynamic_int8") {
+        graph_ = quantize_dynamic_int8(*graph_);
+        verr = graph_->validate();
+        if (!verr.empty()) throw ValidationError(verr);
+    }
     if (options_.device != "rocm")
         throw PyFlameRTError("Device '" + options_.device +
                              "' is not provided by this runtime; it runs device='rocm' (MI355X)");

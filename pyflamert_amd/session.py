@@ -22,7 +22,7 @@ _I64 = C.c_int64
 _INT = C.c_int
 _SIGS = {
     "pfr_session_last_error": (C.c_char_p, []),
-    "pfr_session_create": (_INT, [C.c_char_p, C.c_char_p, _INT, _INT, _INT, _INT, C.POINTER(_P)]),
+    "pfr_session_create": (_INT, [C.c_char_p, C.c_char_p, _INT, _INT, _INT, _INT, C.c_char_p, C.POINTER(_P)]),
     "pfr_session_destroy": (_INT, [_P]),
     "pfr_session_io_count": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT)]),
     "pfr_session_io_info": (_INT, [_P, _INT, _INT, C.POINTER(C.c_char_p), C.POINTER(_INT), _P, C.POINTER(_INT)]),
@@ -32,6 +32,7 @@ _SIGS = {
     "pfr_session_device_plan": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT)]),
     "pfr_model_describe": (_INT, [C.c_char_p, C.c_char_p, _I64, C.POINTER(_I64)]),
     "pfr_model_resave": (_INT, [C.c_char_p, C.c_char_p]),
+    "pfr_model_quantize": (_INT, [C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(_INT)]),
 }
 _DT = {0: np.float32, 1: np.float16, 2: np.uint16, 3: np.float64, 4: np.int64, 5: np.int32, 6: np.int16,
        7: np.int8, 8: np.uint8, 9: np.bool_}
@@ -101,6 +102,9 @@ class SessionOptions:
     # OpFuncs, 1 Basic = device-resident plan, 2 Extended (default) and 3 All
     # = plan + Relu fused into the pruned product before it
     optimization_level: int = 2
+    # "" or "dynamic_int8": 2:4-pruned MatMul(W, X) nodes run as
+    # DynamicQuantizeLinear + per-channel int8 QuantizedMatMul
+    quantization: str = ""
 
 
 @dataclass
@@ -123,6 +127,14 @@ def resave_model(src, dst):
     _check(runtime().pfr_model_resave(src.encode(), dst.encode()))
 
 
+def quantize_model(src, dst, mode="dynamic_int8"):
+    """The session's quantization rewrite applied offline; returns the number
+    of MatMul nodes replaced."""
+    n = _INT(0)
+    _check(runtime().pfr_model_quantize(src.encode(), dst.encode(), mode.encode(), C.byref(n)))
+    return n.value
+
+
 class InferenceSession:
     def __init__(self, model_path, options=None, providers=None):
         options = options or SessionOptions()
@@ -131,7 +143,8 @@ class InferenceSession:
         mode = {"strict": 0, "fast": 1}[options.math_mode]
         _check(L.pfr_session_create(str(model_path).encode(), options.device.encode(),
                                     int(options.strict_math_mode), mode, options.device_id,
-                                    int(options.optimization_level), C.byref(h)))
+                                    int(options.optimization_level), (options.quantization or "").encode(),
+                                    C.byref(h)))
         self._h = h
         self._L = L
 

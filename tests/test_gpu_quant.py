@@ -137,3 +137,80 @@ def test_sp24_device_scale_and_zero_point(ctx):
     W.gemm_q_dev(dX.data_ptr(), True, N, dY.data_ptr(), x_scale_ptr=dS.data_ptr(), x_zp_ptr=dZ.data_ptr())
     ctx.synchronize()
     assert np.array_equal(bits(dY.cpu().numpy()), bits(W.gemm_q(xq.reshape(K, N), float(xs), int(xz))))
+
+
+def test_dynamic_int8_session(tmp_path):
+    """A session with quantization="dynamic_int8": each 2:4 MatMul(W, X) runs
+    as DynamicQuantizeLinear + per-channel QuantizedMatMul on the GPU, the
+    other MatMul stays fp32; results bit-exact against the oracle applied
+    node by node (per-row weight quantization, the activation's dynamic
+    parameters, the quantized product row by row), on the device-resident
+    plan and node by node alike."""
+    from pyflamert_amd import pfm, session
+
+    sys.path.insert(0, str(__import__("pathlib").Path(__file__).parent))
+    from test_runtime_cpu import quant_graph
+
+    rng = np.random.default_rng(11)
+    m, w1, w2 = quant_graph(rng, K=512, M1=384, M2=256, N=64)
+    p = str(tmp_path / "q.pfm")
+    pfm.save(m, p)
+    x = rng.standard_normal((512, 64)).astype(np.float32)
+
+    def qrows(w):
+        M, K = w.shape
+        s, _ = O.orc_dynamic_params_per_channel(w.reshape(1, M, K))
+        q = O.orc_quantize(w, s, np.zeros(M, np.int32), O.I8, (1, M, K))
+        return q, np.asarray(s, np.float32)
+
+    def qmm(w, act):
+        q, s = qrows(w)
+        aq, xs, xz = dql_oracle(act.ravel())
+        aq = aq.reshape(act.shape)
+        return np.concatenate([O.orc_quantized_matmul(q[r:r + 1], aq, s[r], xs, 0, int(xz)) for r in range(len(q))])
+
+    h = qmm(w1, x)
+    y_ref = qmm(w2, O.orc_relu(h))
+    z_ref = O.orc_matmul(m["initializers"]["w3"], x)
+    for lvl in (2, 0):
+        say(f"dynamic int8 session, optimization level {lvl}")
+        s = session.InferenceSession(p, session.SessionOptions(quantization="dynamic_int8", optimization_level=lvl))
+        y, z = s.run(None, {"x": x})
+        assert s.device_plan() == ((True, 6) if lvl else (False, 0))
+        assert np.array_equal(bits(y), bits(y_ref)), lvl
+        assert np.array_equal(bits(z), bits(z_ref)), lvl
+
+
+def test_two_input_quantized_matmul_zero_point(tmp_path):
+    """The reference form of QuantizedMatMul (two inputs, attributes) with a
+    nonzero b_zero_point and per-channel a_scales, int8 and uint8 B (whose
+    bytes the reference reads as int8): cpu_quantized_matmul's result (the
+    oracle restatement, and the reference op itself for a per-tensor scale)."""
+    from pyflamert_amd import pfm, session
+
+    rng = np.random.default_rng(21)
+    M, K, N = 128, 256, 40
+    q, s = rand_24(rng, M, K)
+    for bdt, code in ((np.int8, 7), (np.uint8, 8)):
+        b = rng.integers(-128, 128, (K, N)).astype(np.int8).view(bdt)
+        for per_channel in (False, True):
+            attrs = {"b_scale": 0.04, "b_zero_point": -9}
+            attrs.update({"a_scales": [float(v) for v in s]} if per_channel else {"a_scale": float(s[0])})
+            m = {"name": "q2", "inputs": [("b", code, [K, N])], "outputs": [("y", 0, [M, N])],
+                 "initializers": {"w": q}, "nodes": [("qmm", "QuantizedMatMul", ["w", "b"], ["y"], attrs)]}
+            p = str(tmp_path / "q2.pfm")
+            pfm.save(m, p)
+            say(f"QuantizedMatMul two inputs B={np.dtype(bdt).name} per_channel={per_channel}")
+            for lvl in (2, 0):
+                (y,) = session.InferenceSession(p, session.SessionOptions(optimization_level=lvl)).run(None, {"b": b})
+                if per_channel:
+                    for r in rng.choice(M, 16, replace=False):
+                        ref = O.orc_cpu_quantized_matmul(q[r:r + 1], b, np.float32(s[r]), np.float32(0.04), 0, -9)
+                        assert np.array_equal(bits(y[r:r + 1]), bits(ref)), (r, lvl)
+                else:
+                    ref = O.orc_cpu_quantized_matmul(q, b, np.float32(s[0]), np.float32(0.04), 0, -9)
+                    assert np.array_equal(bits(y), bits(ref)), lvl
+                    if O.have_ref():
+                        got = O.ref_op_f32("QuantizedMatMul", [q, b], fattrs={"a_scale": float(s[0]), "b_scale": 0.04},
+                                           iattrs={"b_zero_point": -9})
+                        assert np.array_equal(bits(y), bits(got)), lvl

@@ -270,3 +270,56 @@ def test_sparse_record_validation(tmp_path):
     p = write(tmp_path, "dup.pfm", m)
     with pytest.raises(session.InvalidModelError, match="already a dense initializer"):
         session.describe_model(p)
+
+
+def quant_graph(rng, K=64, M1=48, M2=32, N=5, keep_dense=False):
+    """MatMul(W1, x) -> Relu -> MatMul(W2, .) with 2:4-pruned W1 (CSR record)
+    and W2 (dense), plus a MatMul whose weight is not 2:4 (left alone)."""
+    def pruned24(m, k):
+        w = rng.standard_normal((m, k)).astype(np.float32)
+        return O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(m, k))
+    w1, w2 = pruned24(M1, K), pruned24(M2, M1)
+    w1[3, :] = 0.0  # an all-zero row: scale 1 (quant_params.cpp:78-82)
+    dense3 = rng.standard_normal((7, K)).astype(np.float32)
+    m = {"name": "q", "inputs": [("x", 0, [K, N])], "outputs": [("y", 0, [M2, N]), ("z", 0, [7, N])],
+         "initializers": {"w2": w2, "w3": dense3},
+         "sparse_initializers": {} if keep_dense else {"w1": pfm.csr_record(w1)},
+         "nodes": [("mm1", "MatMul", ["w1", "x"], ["h"], {}), ("r", "Relu", ["h"], ["a"], {}),
+                   ("mm2", "MatMul", ["w2", "a"], ["y"], {}), ("mm3", "MatMul", ["w3", "x"], ["z"], {})]}
+    if keep_dense:
+        m["initializers"]["w1"] = w1
+    return m, w1, w2
+
+
+def test_dynamic_int8_rewrite(tmp_path):
+    """The rewrite replaces the 2:4 MatMul(W, X) nodes by
+    DynamicQuantizeLinear + QuantizedMatMul with the per-row int8 weights and
+    scales of compute_dynamic_params_per_channel + quantize_tensor (oracle),
+    stores them as 2:4 records, keeps the other nodes, and drops the float
+    weights it replaced."""
+    rng = np.random.default_rng(2)
+    m, w1, w2 = quant_graph(rng)
+    p = write(tmp_path, "q.pfm", m)
+    out = str(tmp_path / "q_int8.pfm")
+    assert session.quantize_model(p, out) == 2
+    q = pfm.load(out)
+    ops = [(n[1], n[2]) for n in q["nodes"]]
+    assert [o for o, _ in ops] == ["DynamicQuantizeLinear", "QuantizedMatMul", "Relu", "DynamicQuantizeLinear",
+                                   "QuantizedMatMul", "MatMul"]
+    assert "w1" not in q["sparse_initializers"] and "w2" not in q["initializers"] and "w3" in q["initializers"]
+    for w, node in ((w1, q["nodes"][1]), (w2, q["nodes"][4])):
+        M, K = w.shape
+        s_ref, _ = O.orc_dynamic_params_per_channel(w.reshape(1, M, K))
+        q_ref = O.orc_quantize(w, s_ref, np.zeros(M, np.int32), O.I8, (1, M, K))
+        name = node[2][0]
+        rec = q["sparse_initializers"][name]
+        assert rec["format"] == "2:4"
+        assert np.array_equal(pfm.record_to_dense(rec), q_ref)
+        assert np.array_equal(np.array(node[4]["a_scales"], np.float32).view(np.uint32),
+                              np.asarray(s_ref, np.float32).view(np.uint32))
+        assert node[4]["a_zero_point"] == 0
+    # the quantizer output is itself a loadable, re-savable model
+    session.resave_model(out, str(tmp_path / "again.pfm"))
+    assert open(out, "rb").read() == open(str(tmp_path / "again.pfm"), "rb").read()
+    with pytest.raises(session.PyFlameRTError, match="Invalid quantization mode"):
+        session.quantize_model(p, out, "static_int4")
