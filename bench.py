@@ -541,6 +541,19 @@ def main():
             "flop_per_launch": flops,
         }
         log(f"N={N}: {ms * 1e3:.2f} us/launch  {extra[f'N{N}']}")
+        if N == N_MAIN and args.mode == "strict":
+            # the fused multiply-add form of the same product (within 1e-5
+            # normwise of the strict result, the fp32 tolerance)
+            msf = time_gpu(sets, N, max(200, steps // 4), args.warmup, "fast")
+            Yf = sets[0][2].cpu().numpy()
+            err = float(np.abs(Yf - Y0).max() / np.abs(Y0).max())
+            extra[f"N{N}_fast"] = {
+                "ms_per_launch": round(msf, 5),
+                "gflops": round(flops / (msf * 1e-3) / 1e9, 1),
+                "gbs": round(byts / (msf * 1e-3) / 1e9, 1),
+                "normwise_err_vs_strict": err,
+            }
+            log(f"N={N} fast: {msf * 1e3:.2f} us/launch  {extra[f'N{N}_fast']}")
         for W, _, _ in sets:
             W.free()
         del sets
