@@ -197,6 +197,91 @@ def bench_bert_linears(ctx):
     return res
 
 
+def bench_bert_ffn_block(ctx):
+    """One BERT-base encoder FFN block (Gemm 768->3072 + Gelu, Gemm
+    3072->768, residual Add, LayerNormalization eps 1e-12), weights [out, in]
+    N(0, 0.02) with 80 % uniform-random zeros, 1024 tokens (batch 8 x seq
+    128), through InferenceSession(device="rocm") at the Extended level (Gelu
+    fused into the first Gemm's epilogue: 4 launches) and the Basic level
+    (5 launches).  Microseconds per run(), host x in and host y out (3 MiB
+    each way, staged by the HIP runtime from pageable memory) included; and
+    the same four device calls on device-resident tensors, timed with
+    events, as a model with resident activations runs them."""
+    import tempfile
+
+    import numpy as np
+
+    from pyflamert_amd import pfm, session
+
+    T, H, F = 1024, 768, 3072
+    rng = np.random.default_rng(4321)
+
+    def pruned(shape):
+        w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+        w[rng.random(shape) < 0.8] = 0
+        return w
+
+    w1, w2 = pruned((F, H)), pruned((H, F))
+    inits = {"w1": w1, "b1": (rng.standard_normal(F) * 0.1).astype(np.float32), "w2": w2,
+             "b2": (rng.standard_normal(H) * 0.1).astype(np.float32),
+             "ln_s": np.ones(H, np.float32), "ln_b": np.zeros(H, np.float32)}
+    model = {"name": "ffn", "inputs": [("x", 0, [T, H])], "outputs": [("y", 0, [T, H])], "initializers": inits,
+             "nodes": [("fc1", "Gemm", ["x", "w1", "b1"], ["h"], {"transB": 1}),
+                       ("act", "Gelu", ["h"], ["g"], {}),
+                       ("fc2", "Gemm", ["g", "w2", "b2"], ["f"], {"transB": 1}),
+                       ("res", "Add", ["f", "x"], ["r"], {}),
+                       ("ln", "LayerNormalization", ["r", "ln_s", "ln_b"], ["y"], {"epsilon": 1e-12})]}
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    res = {"nnz": int((w1 != 0).sum() + (w2 != 0).sum())}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "ffn.pfm")
+        pfm.save(model, path)
+        for lvl, key in ((2, "extended"), (1, "basic")):
+            sess = session.InferenceSession(path, session.SessionOptions(device="rocm", optimization_level=lvl))
+            for _ in range(5):
+                sess.run(None, {"x": x})
+            ts = []
+            for _ in range(50):
+                t0 = time.perf_counter()
+                sess.run(None, {"x": x})
+                ts.append(time.perf_counter() - t0)
+            res[f"{key}_us_per_run"] = round(float(np.median(ts)) * 1e6, 1)
+            res[f"{key}_plan"] = list(sess.device_plan())
+            sess.close()
+    import torch
+
+    dev = {k: torch.from_numpy(v).cuda() for k, v in inits.items() if k not in ("w1", "w2")}
+    dx = torch.from_numpy(x).cuda()
+    dh = torch.empty((T, F), device="cuda")
+    df = torch.empty((T, H), device="cuda")
+    dr = torch.empty((T, H), device="cuda")
+    dy = torch.empty((T, H), device="cuda")
+    W1, W2 = ctx.csr_from_dense(w1), ctx.csr_from_dense(w2)  # CSR of op(B)^T for transB = 1
+    torch.cuda.synchronize()
+
+    def block():
+        ctx.gemm_csr_dev(dx.data_ptr(), T, H, W1, dh.data_ptr(), 1.0, 1.0, dev["b1"].data_ptr(), F, gelu=True)
+        ctx.gemm_csr_dev(dh.data_ptr(), T, F, W2, df.data_ptr(), 1.0, 1.0, dev["b2"].data_ptr(), H)
+        ctx.add_dev(df.data_ptr(), (T, H), dx.data_ptr(), (T, H), dr.data_ptr())
+        ctx.layernorm_dev(dr.data_ptr(), T, H, dev["ln_s"].data_ptr(), dev["ln_b"].data_ptr(), 1e-12, dy.data_ptr())
+
+    for _ in range(10):
+        block()
+    ctx.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(100):
+        block()
+    ev1.record()
+    torch.cuda.synchronize()
+    res["device_us_per_block"] = round(ev0.elapsed_time(ev1) / 100 * 1e3, 1)
+    W1.free()
+    W2.free()
+    res["flop_per_run"] = 2 * T * res["nnz"]
+    log(f"BERT FFN block: {res}")
+    return res
+
+
 def bench_dynamic_int8(ctx):
     """The dynamic int8 path of config 3's shape: X fp32 4096 x 512 ->
     DynamicQuantizeLinear (uint8, scale and zero point on the device) ->
@@ -564,6 +649,7 @@ def main():
         extra["sp24_i8"] = bench_sp24(ctx, args)
         extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
         extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
+        extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)
         extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
         extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
         extra["dynamic_int8_node_11008x4096x512"] = bench_dynamic_int8(ctx)

@@ -52,7 +52,9 @@ typedef enum pfr_mode { PFR_MODE_STRICT = 0, PFR_MODE_FAST = 1 } pfr_mode;
 /* Activation fused into a product's epilogue (after the bias). */
 typedef enum pfr_act {
     PFR_ACT_NONE = 0,
-    PFR_ACT_RELU = 1  /* cpu_relu, activation.cpp:45-60: std::max(0.0f, v) */
+    PFR_ACT_RELU = 1, /* cpu_relu, activation.cpp:45-60: std::max(0.0f, v) */
+    PFR_ACT_GELU = 2  /* cpu_gelu, activation.cpp:239-259: tanh approximation
+                         (device tanhf: within a few ulp of the reference) */
 } pfr_act;
 
 typedef struct pfr_ctx pfr_ctx;   /* one device + one stream + scratch */
@@ -245,6 +247,25 @@ int pfr_softmax(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
                 int64_t inner, float* y);
 int pfr_softmax_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t axis,
                     int64_t inner, float* y);
+/* Gelu, cpu_gelu (activation.cpp:239-259): 0.5 x (1 + tanh(sqrt(2/pi)
+ * (x + 0.044715 x^3))) with the device tanhf (a few ulp from the CPU). */
+int pfr_gelu(pfr_ctx* ctx, const float* x, int64_t n, float* y);
+int pfr_gelu_dev(pfr_ctx* ctx, const float* x, int64_t n, float* y);
+/* Add with numpy broadcasting (cpu_add, math.cpp:150-224), bit-exact; at
+ * most 8 dimensions.  y has the broadcast shape; shapes that do not
+ * broadcast give PFR_ERR_INVALID_ARG. */
+int pfr_add(pfr_ctx* ctx, const float* a, const int64_t* a_shape, int a_ndim,
+            const float* b, const int64_t* b_shape, int b_ndim, float* y);
+int pfr_add_dev(pfr_ctx* ctx, const float* a, const int64_t* a_shape, int a_ndim,
+                const float* b, const int64_t* b_shape, int b_ndim, float* y);
+/* LayerNormalization over the trailing `norm` elements of each of `outer`
+ * rows (cpu_layer_norm, nn.cpp:419-490): sequential mean and variance in the
+ * reference's order, y = scale * (x - mean) * (1 / sqrt(var + epsilon)) +
+ * bias; bit-exact.  scale and bias hold `norm` floats. */
+int pfr_layernorm(pfr_ctx* ctx, const float* x, int64_t outer, int64_t norm,
+                  const float* scale, const float* bias, float epsilon, float* y);
+int pfr_layernorm_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t norm,
+                      const float* scale, const float* bias, float epsilon, float* y);
 
 /* ---- dynamic activation quantization -------------------------------------- */
 

@@ -62,6 +62,9 @@ def lib():
             "orc_f32_to_bf16": (None, [_P, _P, _I64]),
             "orc_bf16_to_f32": (None, [_P, _P, _I64]),
             "orc_relu": (None, [_P, _I64, _P]),
+            "orc_gelu": (None, [_P, _I64, _P]),
+            "orc_layernorm": (None, [_P, _I64, _I64, _P, _P, _F, _P]),
+            "orc_add": (_INT, [_P, _P, _INT, _P, _P, _INT, _P, _P, C.POINTER(_INT)]),
             "orc_softmax": (None, [_P, _I64, _I64, _I64, _P]),
         }
         for name, (res, args) in sig.items():
@@ -337,6 +340,44 @@ def orc_relu(x):
     out = np.empty_like(x)
     lib().orc_relu(_ptr(x), x.size, _ptr(out))
     return out
+
+
+def orc_gelu(x):
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_gelu(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def orc_layernorm(x, scale, bias, epsilon=1e-5, axis=-1):
+    x = _c(x, np.float32)
+    axis = axis % x.ndim
+    outer = int(np.prod(x.shape[:axis]))
+    norm = int(np.prod(x.shape[axis:]))
+    out = np.empty_like(x)
+    lib().orc_layernorm(_ptr(x), outer, norm, _ptr(_c(scale, np.float32)), _ptr(_c(bias, np.float32)),
+                        epsilon, _ptr(out))
+    return out
+
+
+def orc_add(a, b):
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    ash = np.array(a.shape, np.int64)
+    bsh = np.array(b.shape, np.int64)
+    nd = max(a.ndim, b.ndim)
+    # capacity: the product of the larger extent per right-aligned axis
+    ea = [1] * (nd - a.ndim) + list(a.shape)
+    eb = [1] * (nd - b.ndim) + list(b.shape)
+    osh = np.zeros(16, np.int64)
+    ond = C.c_int(0)
+    out = np.empty(max(1, int(np.prod([max(x, y) for x, y in zip(ea, eb)], dtype=np.int64))), np.float32)
+    rc = lib().orc_add(_ptr(a), _ptr(ash), a.ndim, _ptr(b), _ptr(bsh), b.ndim, _ptr(out), _ptr(osh),
+                       C.byref(ond))
+    if rc:
+        raise ValueError("Add: shapes are not broadcastable")
+    shape = tuple(int(v) for v in osh[:ond.value])
+    return out[: int(np.prod(shape, dtype=np.int64))].reshape(shape)
 
 
 def orc_softmax(x, axis=-1):

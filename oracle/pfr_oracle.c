@@ -629,6 +629,74 @@ void orc_relu(const float* x, int64_t n, float* out) {
 }
 
 /* activation.cpp:157-237. */
+/* activation.cpp:249-256: inner = c * (v + ((0.044715 * v) * v) * v),
+ * out = (0.5 * v) * (1 + tanhf(inner)), left to right as written. */
+void orc_gelu(const float* x, int64_t n, float* out) {
+    const float c = 0.7978845608028654f;
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        const float inner = c * (v + 0.044715f * v * v * v);
+        out[i] = 0.5f * v * (1.0f + tanhf(inner));
+    }
+}
+
+/* nn.cpp:458-486. */
+void orc_layernorm(const float* x, int64_t outer, int64_t norm, const float* scale,
+                   const float* bias, float epsilon, float* out) {
+    for (int64_t o = 0; o < outer; ++o) {
+        const float* xr = x + o * norm;
+        float mean = 0;
+        for (int64_t i = 0; i < norm; ++i) mean += xr[i];
+        mean /= (float)norm;
+        float var = 0;
+        for (int64_t i = 0; i < norm; ++i) {
+            const float d = xr[i] - mean;
+            var += d * d;
+        }
+        var /= (float)norm;
+        const float inv_std = 1.0f / sqrtf(var + epsilon);
+        for (int64_t i = 0; i < norm; ++i)
+            out[o * norm + i] = scale[i] * (xr[i] - mean) * inv_std + bias[i];
+    }
+}
+
+/* math.cpp:150-224: shapes right-aligned, a dimension of 1 (or a missing
+ * one) broadcasts; out[i] = a[ia] + b[ib]. */
+int orc_add(const float* a, const int64_t* a_shape, int a_nd, const float* b,
+            const int64_t* b_shape, int b_nd, float* out, int64_t* out_shape,
+            int* out_nd) {
+    const int nd = a_nd > b_nd ? a_nd : b_nd;
+    if (nd > 16) return -1;
+    int64_t as[16], bs[16];
+    for (int d = 0; d < nd; ++d) {
+        const int da = d - (nd - a_nd), db = d - (nd - b_nd);
+        as[d] = da >= 0 ? a_shape[da] : 1;
+        bs[d] = db >= 0 ? b_shape[db] : 1;
+        if (as[d] != bs[d] && as[d] != 1 && bs[d] != 1) return -1;
+        out_shape[d] = as[d] > bs[d] ? as[d] : bs[d]; /* math.cpp:54-64: the larger */
+    }
+    *out_nd = nd;
+    int64_t n = 1, na = 1, nb = 1;
+    for (int d = 0; d < nd; ++d) n *= out_shape[d], na *= as[d], nb *= bs[d];
+    if (na == 0 || nb == 0) { /* math.cpp:170-173 returns the new tensor, zeroed by tensor.cpp:47 */
+        for (int64_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return 0;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t rem = i, ia = 0, ib = 0, sa = 1, sb = 1;
+        for (int d = nd - 1; d >= 0; --d) {
+            const int64_t idx = rem % out_shape[d];
+            rem /= out_shape[d];
+            if (as[d] != 1) ia += idx * sa;
+            if (bs[d] != 1) ib += idx * sb;
+            sa *= as[d];
+            sb *= bs[d];
+        }
+        out[i] = a[ia] + b[ib];
+    }
+    return 0;
+}
+
 void orc_softmax(const float* x, int64_t outer, int64_t axis_size,
                  int64_t inner, float* out) {
     if (axis_size == 0) return;

@@ -142,6 +142,18 @@ void orc_bf16_to_f32(const uint16_t* in, float* out, int64_t n);
 /* ---- neighbours on the MLP graph (src/backends/cpu/ops/activation.cpp) --- */
 
 void orc_relu(const float* x, int64_t n, float* out);   /* :45-60 */
+/* cpu_gelu, activation.cpp:239-259 (tanh approximation, libm tanhf). */
+void orc_gelu(const float* x, int64_t n, float* out);
+/* cpu_layernorm, nn.cpp:419-490: x viewed as [outer, norm] (norm = the
+ * product of the dimensions from axis on), sequential mean and variance,
+ * out = scale[i] * (x - mean) * inv_std + bias[i]. */
+void orc_layernorm(const float* x, int64_t outer, int64_t norm, const float* scale,
+                   const float* bias, float epsilon, float* out);
+/* cpu_add (math.cpp:150-224 binary_elementwise with +): numpy-style
+ * broadcasting of a [a_nd dims] and b [b_nd dims] to out [out_nd dims]. */
+int orc_add(const float* a, const int64_t* a_shape, int a_nd, const float* b,
+            const int64_t* b_shape, int b_nd, float* out, int64_t* out_shape,
+            int* out_nd);
 void orc_softmax(const float* x, int64_t outer, int64_t axis_size,
                  int64_t inner, float* out);            /* :157-237 */
 

@@ -23,7 +23,7 @@ PFR_ERR_NO_DEVICE = 4
 
 PFR_F32, PFR_BF16, PFR_I32, PFR_I8, PFR_U8 = 0, 2, 5, 7, 8
 MODE_STRICT, MODE_FAST = 0, 1
-ACT_NONE, ACT_RELU = 0, 1
+ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 SP24_OUT_I32, SP24_OUT_F32, SP24_OUT_I8 = 0, 1, 2
 
 _P = C.c_void_p
@@ -76,6 +76,12 @@ SIGNATURES = {
     "pfr_relu_dev": (_INT, [_P, _P, _I64, _P]),
     "pfr_softmax": (_INT, [_P, _P, _I64, _I64, _I64, _P]),
     "pfr_softmax_dev": (_INT, [_P, _P, _I64, _I64, _I64, _P]),
+    "pfr_gelu": (_INT, [_P, _P, _I64, _P]),
+    "pfr_gelu_dev": (_INT, [_P, _P, _I64, _P]),
+    "pfr_add": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
+    "pfr_add_dev": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
+    "pfr_layernorm": (_INT, [_P, _P, _I64, _I64, _P, _P, _F, _P]),
+    "pfr_layernorm_dev": (_INT, [_P, _P, _I64, _I64, _P, _P, _F, _P]),
 }
 
 _lib = None

@@ -58,6 +58,14 @@ __device__ __forceinline__ int32_t f2i_trunc_x86(float r) {
     return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
 }
 
+// cpu_gelu (activation.cpp:249-256), same operations in the same order;
+// tanhf is the device's, so results are within a few ulp of the reference's
+// glibc tanhf, not bit-identical.
+__device__ __forceinline__ float gelu(float v) {
+    const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
 // Grow-only device buffer owned by a context.
 struct DevBuf {
     void* p = nullptr;

@@ -43,7 +43,7 @@ __device__ __forceinline__ float wval(const void* __restrict__ val, const float*
 
 // Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size],
 // then optionally a fused Relu (activation.cpp:45-60: std::max(0.0f, v), which
-// is (0 < v) ? v : +0, so -0 and NaN give +0).
+// is (0 < v) ? v : +0, so -0 and NaN give +0) or Gelu (activation.cpp:239-259).
 __device__ __forceinline__ float bias_add(float v, int64_t f, const float* __restrict__ bias,
                                           int64_t c_size, float beta, int act) {
     if (bias != nullptr) {
@@ -51,6 +51,7 @@ __device__ __forceinline__ float bias_add(float v, int64_t f, const float* __res
         v = v + t;
     }
     if (act == PFR_ACT_RELU) v = (0.0f < v) ? v : 0.0f;
+    else if (act == PFR_ACT_GELU) v = pfr::gelu(v);
     return v;
 }
 
@@ -315,6 +316,51 @@ __global__ __launch_bounds__(256) void k_transpose_scale(const float* __restrict
     }
 }
 
+// The same transpose for rows and cols multiples of 4 and a 16-byte aligned
+// A: 16-byte loads and stores, every load issued before the first LDS
+// write (addresses clamped into the matrix, out-of-range values dropped).
+// Both LDS passes are free of bank conflicts (row pitch 65).
+__global__ __launch_bounds__(256) void k_transpose_scale4(const float* __restrict__ A, int64_t rows,
+                                                          int64_t cols, float alpha, int scale,
+                                                          float* __restrict__ At) {
+    __shared__ float tile[64][65];
+    const int t = threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+    const int lc = (t & 15) * 4;
+    float4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t r = r0 + (t >> 4) + 16 * i, c = c0 + lc;
+        const int64_t rc = r < rows ? r : rows - 1, cc = c < cols ? c : cols - 4;
+        v[i] = *reinterpret_cast<const float4*>(A + rc * cols + cc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int lr = (t >> 4) + 16 * i;
+        float4 w = v[i];
+        if (scale) {
+            w.x = alpha * w.x;
+            w.y = alpha * w.y;
+            w.z = alpha * w.z;
+            w.w = alpha * w.w;
+        }
+        tile[lr][lc] = w.x;
+        tile[lr][lc + 1] = w.y;
+        tile[lr][lc + 2] = w.z;
+        tile[lr][lc + 3] = w.w;
+    }
+    __syncthreads();
+    const int lr4 = (t & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int lcol = (t >> 4) + 16 * i;
+        const int64_t c = c0 + lcol, r = r0 + lr4;
+        if (c < cols && r < rows)
+            *reinterpret_cast<float4*>(At + c * rows + r) =
+                make_float4(tile[lr4][lcol], tile[lr4 + 1][lcol], tile[lr4 + 2][lcol], tile[lr4 + 3][lcol]);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_scale(const float* __restrict__ A, int64_t n, float alpha,
                                                float* __restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -439,6 +485,11 @@ __global__ __launch_bounds__(64 * W) void k_spmm_sell(
                     a1 = (0.0f < a1) ? a1 : 0.0f;
                     a2 = (0.0f < a2) ? a2 : 0.0f;
                     a3 = (0.0f < a3) ? a3 : 0.0f;
+                } else if (act == PFR_ACT_GELU) {
+                    a0 = pfr::gelu(a0);
+                    a1 = pfr::gelu(a1);
+                    a2 = pfr::gelu(a2);
+                    a3 = pfr::gelu(a3);
                 }
                 *reinterpret_cast<float4*>(yr + cn) = make_float4(a0, a1, a2, a3);
             } else {
@@ -593,7 +644,7 @@ void check_csr(const pfr_csr* W) {
 }
 
 void check_act(int act) {
-    pfr::require(act == PFR_ACT_NONE || act == PFR_ACT_RELU, "unknown activation");
+    pfr::require(act == PFR_ACT_NONE || act == PFR_ACT_RELU || act == PFR_ACT_GELU, "unknown activation");
 }
 
 void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
@@ -632,8 +683,12 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
         float* t = static_cast<float*>(ctx->scratch[3].ensure(sizeof(float) * (size_t)(K * Mb)));
         dim3 grid((unsigned)((K + 63) / 64), (unsigned)((Mb + 63) / 64));
         pfr::require(grid.y < 65536u, "activation too tall for the transpose grid");
-        hipLaunchKernelGGL(k_transpose_scale, grid, dim3(256), 0, s, A, Mb, K, alpha,
-                           alpha != 1.0f ? 1 : 0, t);
+        if (Mb % 4 == 0 && K % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0)
+            hipLaunchKernelGGL(k_transpose_scale4, grid, dim3(256), 0, s, A, Mb, K, alpha,
+                               alpha != 1.0f ? 1 : 0, t);
+        else
+            hipLaunchKernelGGL(k_transpose_scale, grid, dim3(256), 0, s, A, Mb, K, alpha,
+                               alpha != 1.0f ? 1 : 0, t);
         PFR_HIP(hipGetLastError());
         At = t;
     } else if (alpha != 1.0f) {

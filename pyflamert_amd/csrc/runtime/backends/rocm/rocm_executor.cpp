@@ -180,6 +180,40 @@ void* RocmExecutor::device_buffer(const std::string& name, int64_t bytes) {
 
 RocmExecutor* RocmExecutor::current() { return t_current; }
 
+std::vector<int64_t> broadcast_shapes(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                                      const char* op) {
+    const size_t nd = std::max(a.size(), b.size());
+    std::vector<int64_t> out(nd);
+    for (size_t i = 0; i < nd; ++i) {
+        const int64_t da = i < a.size() ? a[a.size() - 1 - i] : 1;
+        const int64_t db = i < b.size() ? b[b.size() - 1 - i] : 1;
+        if (da != db && da != 1 && db != 1)
+            throw std::invalid_argument(std::string(op) + ": shapes are not broadcastable");
+        out[nd - 1 - i] = std::max(da, db);
+    }
+    return out;
+}
+
+LayerNormExtent layernorm_extent(const std::vector<int64_t>& x_shape, int64_t scale_numel, int64_t bias_numel,
+                                 const Node* node) {
+    const int64_t nd = (int64_t)x_shape.size();
+    if (nd < 1)
+        throw std::invalid_argument("LayerNormalization input must have at least 1 dimensions, got " +
+                                    std::to_string(nd));
+    LayerNormExtent e{1, 1, node->get_attr<float>("epsilon", 1e-5f)};
+    int64_t axis = node->get_attr<int64_t>("axis", -1);
+    if (axis < 0) axis += nd;
+    if (axis < 0 || axis >= nd)
+        throw std::invalid_argument("LayerNormalization: axis " + std::to_string(axis) + " out of range");
+    for (int64_t i = 0; i < axis; ++i) e.outer *= x_shape[(size_t)i];
+    for (int64_t i = axis; i < nd; ++i) e.norm *= x_shape[(size_t)i];
+    if (scale_numel < e.norm || bias_numel < e.norm)
+        throw std::invalid_argument("LayerNormalization: scale and bias need " + std::to_string(e.norm) +
+                                    " elements, got " + std::to_string(scale_numel) + " and " +
+                                    std::to_string(bias_numel));
+    return e;
+}
+
 const RocmExecutor::DeviceWeight* RocmExecutor::weight(const Node* node) const {
     auto it = weights_.find(node);
     return it == weights_.end() ? nullptr : &it->second;
@@ -289,10 +323,12 @@ void RocmExecutor::prepare(const Graph& graph) {
 }
 
 // The device-resident plan: one step per node in topological order, each a
-// device entry point; a product whose output feeds exactly one node, a Relu,
-// and is not a graph output takes that Relu into its epilogue (PFR_ACT_RELU;
-// the Relu then runs at the product's position, which its single input
-// allows).  Any node without a device kernel leaves plan_ok_ false.
+// device entry point; a product whose output feeds exactly one node, a Relu
+// or a Gelu, and is not a graph output takes that activation into its
+// epilogue (PFR_ACT_RELU / PFR_ACT_GELU: the same function of the same fp32
+// value, so fusion changes no bit; the activation then runs at the
+// product's position, which its single input allows).  Any node without a
+// device kernel leaves plan_ok_ false.
 void RocmExecutor::build_plan(const Graph& graph) {
     plan_.clear();
     fused_away_.clear();
@@ -312,7 +348,7 @@ void RocmExecutor::build_plan(const Graph& graph) {
         const bool dynq = op == "DynamicQuantizeLinear" && n->inputs().size() == 1 && n->outputs().size() == 3;
         if (!dynq && n->outputs().size() != 1) return;
         const DeviceWeight* w = weight(n);
-        PlanStep st{PlanStep::Relu, n, false, n->outputs()[0]};
+        PlanStep st{PlanStep::Relu, n, PFR_ACT_NONE, n->outputs()[0]};
         if (op == "Gemm" && w && w->kind == DeviceWeight::CsrB)
             st.op = PlanStep::Gemm;
         else if (op == "MatMul" && w && w->kind == DeviceWeight::CsrB)
@@ -325,6 +361,12 @@ void RocmExecutor::build_plan(const Graph& graph) {
             st.op = PlanStep::Relu;
         else if (op == "Softmax" && n->inputs().size() == 1)
             st.op = PlanStep::Softmax;
+        else if (op == "Gelu" && n->inputs().size() == 1)
+            st.op = PlanStep::Gelu;
+        else if (op == "Add" && n->inputs().size() == 2)
+            st.op = PlanStep::Add;
+        else if (op == "LayerNormalization" && n->inputs().size() == 3)
+            st.op = PlanStep::LayerNorm;
         else if (dynq)
             st.op = PlanStep::DynQuant;
         else
@@ -339,8 +381,9 @@ void RocmExecutor::build_plan(const Graph& graph) {
         const std::string prod = st.out;
         if (uses[prod] != 1 || graph_outs.count(prod)) continue;
         for (size_t j = 0; j < steps.size(); ++j) {
-            if (dropped[j] || steps[j].op != PlanStep::Relu || steps[j].node->inputs()[0] != prod) continue;
-            st.fuse_relu = true;
+            const bool relu = steps[j].op == PlanStep::Relu, gelu = steps[j].op == PlanStep::Gelu;
+            if (dropped[j] || !(relu || gelu) || steps[j].node->inputs()[0] != prod) continue;
+            st.act = relu ? PFR_ACT_RELU : PFR_ACT_GELU;
             st.out = steps[j].out;
             dropped[j] = true;
             fused_away_.insert(prod);
@@ -348,9 +391,9 @@ void RocmExecutor::build_plan(const Graph& graph) {
         }
     }
 
-    // Initializers a step reads as an activation (biases, or a constant
-    // operand of Relu/Softmax) go to the device once; the pruned operand of a
-    // product is already a device weight.
+    // Initializers a step reads as an activation (biases, LayerNorm's scale
+    // and bias, a constant operand of an elementwise step) go to the device
+    // once; the pruned operand of a product is already a device weight.
     for (size_t i = 0; i < steps.size(); ++i) {
         if (dropped[i]) continue;
         const PlanStep& st = steps[i];
@@ -409,7 +452,7 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 throw std::invalid_argument(std::string(op) + ": expected at least " + std::to_string(k) +
                                             " inputs, got " + std::to_string(in.size()));
         };
-        const int act = st.fuse_relu ? PFR_ACT_RELU : PFR_ACT_NONE;
+        const int act = st.act;
         DevTensor out;
         out.dtype = DType::Float32;
         try {
@@ -587,6 +630,45 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 out.p = device_buffer(st.out, numel(x.shape) * 4);
                 pfr_check(pfr_softmax_dev(ctx_, static_cast<const float*>(x.p), outer, x.shape[axis], inner,
                                           static_cast<float*>(out.p)));
+                break;
+            }
+            case PlanStep::Gelu: {
+                // activation.cpp:239-259.
+                const DevTensor& x = act_in(0);
+                need_f32(x.dtype, "Gelu input");
+                out.shape = x.shape;
+                out.p = device_buffer(st.out, numel(x.shape) * 4);
+                pfr_check(pfr_gelu_dev(ctx_, static_cast<const float*>(x.p), numel(x.shape),
+                                       static_cast<float*>(out.p)));
+                break;
+            }
+            case PlanStep::Add: {
+                // math.cpp:150-226.
+                const DevTensor& a = act_in(0);
+                const DevTensor& b = act_in(1);
+                need_f32(a.dtype, "Add input A");
+                need_f32(b.dtype, "Add input B");
+                out.shape = broadcast_shapes(a.shape, b.shape, "Add");
+                out.p = device_buffer(st.out, std::max<int64_t>(numel(out.shape), 1) * 4);
+                pfr_check(pfr_add_dev(ctx_, static_cast<const float*>(a.p), a.shape.data(), (int)a.shape.size(),
+                                      static_cast<const float*>(b.p), b.shape.data(), (int)b.shape.size(),
+                                      static_cast<float*>(out.p)));
+                break;
+            }
+            case PlanStep::LayerNorm: {
+                // nn.cpp:419-478.
+                const DevTensor& x = act_in(0);
+                const DevTensor& sc = act_in(1);
+                const DevTensor& bi = act_in(2);
+                need_f32(x.dtype, "LayerNormalization input");
+                need_f32(sc.dtype, "LayerNormalization scale");
+                need_f32(bi.dtype, "LayerNormalization bias");
+                const LayerNormExtent e = layernorm_extent(x.shape, numel(sc.shape), numel(bi.shape), n);
+                out.shape = x.shape;
+                out.p = device_buffer(st.out, numel(x.shape) * 4);
+                pfr_check(pfr_layernorm_dev(ctx_, static_cast<const float*>(x.p), e.outer, e.norm,
+                                            static_cast<const float*>(sc.p), static_cast<const float*>(bi.p),
+                                            e.epsilon, static_cast<float*>(out.p)));
                 break;
             }
             }

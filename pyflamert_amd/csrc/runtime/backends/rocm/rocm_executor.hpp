@@ -14,11 +14,12 @@
 //  * inputs and initializers are not deep-copied on every run;
 //  * from OptLevel::Basic up, a graph whose every node has a device kernel
 //    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, DynamicQuantizeLinear,
-//    Relu, Softmax) runs as a device-resident plan:
+//    Relu, Softmax, Gelu, Add, LayerNormalization) runs as a
+//    device-resident plan:
 //    graph inputs are copied to the GPU once per run, the remaining
 //    initializers once per graph, activations stay in device buffers
 //    between nodes, from OptLevel::Extended up a Gemm/MatMul whose only
-//    consumer is a Relu runs with the Relu fused into its epilogue (the
+//    consumer is a Relu or a Gelu runs with it fused into its epilogue (the
 //    reference's Extended level adds operator fusion, types.hpp:119-124), and
 //    only the requested outputs come back to the host.  Other graphs, and
 //    OptLevel::None, run node by node through the host OpFuncs.
@@ -34,6 +35,24 @@
 #include "pyflame_rt/registry.hpp"
 
 namespace pyflame_rt {
+
+// Output shape of a broadcasting binary op (math.cpp:39-64): shapes are
+// right-aligned, each axis takes the larger extent; throws "<op>: shapes are
+// not broadcastable" (math.cpp:154-158).
+std::vector<int64_t> broadcast_shapes(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                                      const char* op);
+
+// LayerNormalization's attributes and extents (nn.cpp:419-455): epsilon
+// (1e-5), axis (-1) over a tensor of at least one dimension; the rows are
+// the product of the dimensions before axis, the normalised extent that of
+// the rest.  scale and bias must hold the normalised extent (the reference
+// reads that many elements of each).
+struct LayerNormExtent {
+    int64_t outer, norm;
+    float epsilon;
+};
+LayerNormExtent layernorm_extent(const std::vector<int64_t>& x_shape, int64_t scale_numel, int64_t bias_numel,
+                                 const Node* node);
 
 class RocmExecutor : public Backend {
 public:
@@ -68,10 +87,10 @@ public:
 private:
     // One kernel launch of the device plan.
     struct PlanStep {
-        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant } op;
+        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm } op;
         const Node* node;
-        bool fuse_relu = false;  // the following Relu runs in this step's epilogue
-        std::string out;         // tensor the step writes (the Relu's output when fused)
+        int act = 0;      // pfr_act of a following Relu/Gelu run in this step's epilogue
+        std::string out;  // tensor the step writes (the activation's output when fused)
     };
     // A tensor held in device memory while a plan runs.
     struct DevTensor {

@@ -2,8 +2,9 @@
 // with the reference's calling convention: borrowed host inputs in, owning
 // host outputs out, synchronous.  The arithmetic runs on the GPU through the
 // C ABI; shapes, attributes and error texts follow the reference kernels
-// (src/backends/cpu/ops/math.cpp:268-438, quantized_ops.cpp:77-167,
-// activation.cpp:45-60 and :157-237).
+// (src/backends/cpu/ops/math.cpp:150-226 and :268-438, quantized_ops.cpp:
+// 77-167 and :251-278, activation.cpp:45-60, :157-237 and :239-259,
+// nn.cpp:419-478).
 #include <stdexcept>
 #include <string>
 
@@ -193,6 +194,45 @@ std::vector<Tensor> rocm_softmax(const std::vector<const Tensor*>& in, const OpC
     return {std::move(out)};
 }
 
+// Gelu (activation.cpp:239-259).
+std::vector<Tensor> rocm_gelu(const std::vector<const Tensor*>& in, const OpContext&) {
+    need_inputs(in, 1, "Gelu");
+    const Tensor& x = *in[0];
+    need_f32(x, "Gelu input");
+    Tensor out(x.shape(), x.dtype());
+    pfr_check(pfr_gelu(exec().ctx(), x.data_ptr<float>(), x.num_elements(), out.data_ptr<float>()));
+    return {std::move(out)};
+}
+
+// Add with broadcasting (math.cpp:150-226).
+std::vector<Tensor> rocm_add(const std::vector<const Tensor*>& in, const OpContext&) {
+    need_inputs(in, 2, "Add");
+    const Tensor& a = *in[0];
+    const Tensor& b = *in[1];
+    need_f32(a, "Add input A");
+    need_f32(b, "Add input B");
+    Tensor out(broadcast_shapes(a.shape(), b.shape(), "Add"), DType::Float32);
+    pfr_check(pfr_add(exec().ctx(), a.data_ptr<float>(), a.shape().data(), (int)a.ndim(), b.data_ptr<float>(),
+                      b.shape().data(), (int)b.ndim(), out.data_ptr<float>()));
+    return {std::move(out)};
+}
+
+// LayerNormalization (nn.cpp:419-478).
+std::vector<Tensor> rocm_layernorm(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 3, "LayerNormalization");
+    const Tensor& x = *in[0];
+    const Tensor& scale = *in[1];
+    const Tensor& bias = *in[2];
+    need_f32(x, "LayerNormalization input");
+    need_f32(scale, "LayerNormalization scale");
+    need_f32(bias, "LayerNormalization bias");
+    const LayerNormExtent e = layernorm_extent(x.shape(), scale.num_elements(), bias.num_elements(), ctx.node);
+    Tensor out(x.shape(), x.dtype());
+    pfr_check(pfr_layernorm(exec().ctx(), x.data_ptr<float>(), e.outer, e.norm, scale.data_ptr<float>(),
+                            bias.data_ptr<float>(), e.epsilon, out.data_ptr<float>()));
+    return {std::move(out)};
+}
+
 struct RocmOpsRegistrar {
     RocmOpsRegistrar() {
         auto& r = OperatorRegistry::instance();
@@ -202,6 +242,9 @@ struct RocmOpsRegistrar {
         r.register_op("rocm::DynamicQuantizeLinear", rocm_dynamic_quantize_linear);
         r.register_op("rocm::Relu", rocm_relu);
         r.register_op("rocm::Softmax", rocm_softmax);
+        r.register_op("rocm::Gelu", rocm_gelu);
+        r.register_op("rocm::Add", rocm_add);
+        r.register_op("rocm::LayerNormalization", rocm_layernorm);
     }
 };
 RocmOpsRegistrar registrar;

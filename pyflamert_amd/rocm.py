@@ -118,6 +118,52 @@ class Context:
                                      alpha, beta, _ptr(C_), csz, _ptr(Y), _MODES[mode]))
         return Y
 
+    # -- graph neighbours ------------------------------------------------
+    def gelu(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        check(self._lib.pfr_gelu(self.handle, _ptr(x), x.size, _ptr(y)))
+        return y
+
+    def add(self, a, b):
+        """a + b with numpy broadcasting (float32)."""
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        sa = np.asarray(a.shape, np.int64)
+        sb = np.asarray(b.shape, np.int64)
+        # math.cpp:54-64: right-aligned, the larger extent per axis (an
+        # empty operand against a size-1 axis keeps the 1); the library
+        # rejects shapes that do not broadcast
+        nd = max(a.ndim, b.ndim)
+        ea = (1,) * (nd - a.ndim) + a.shape
+        eb = (1,) * (nd - b.ndim) + b.shape
+        y = np.empty(tuple(max(x, z) for x, z in zip(ea, eb)), np.float32)
+        check(self._lib.pfr_add(self.handle, _ptr(a), _ptr(sa), a.ndim, _ptr(b), _ptr(sb), b.ndim, _ptr(y)))
+        return y
+
+    def layernorm(self, x, scale, bias, epsilon=1e-5, axis=-1):
+        """LayerNormalization over the dimensions from `axis` on."""
+        x = np.ascontiguousarray(x, np.float32)
+        ax = axis + x.ndim if axis < 0 else axis
+        norm = int(np.prod(x.shape[ax:], dtype=np.int64))
+        outer = int(np.prod(x.shape[:ax], dtype=np.int64))
+        scale = np.ascontiguousarray(scale, np.float32).ravel()
+        bias = np.ascontiguousarray(bias, np.float32).ravel()
+        if scale.size != norm or bias.size != norm:
+            raise ValueError("scale and bias must hold the normalised extent")
+        y = np.empty_like(x)
+        check(self._lib.pfr_layernorm(self.handle, _ptr(x), outer, norm, _ptr(scale), _ptr(bias),
+                                      float(epsilon), _ptr(y)))
+        return y
+
+    def add_dev(self, a_ptr, a_shape, b_ptr, b_shape, y_ptr):
+        sa = np.asarray(a_shape, np.int64)
+        sb = np.asarray(b_shape, np.int64)
+        check(self._lib.pfr_add_dev(self.handle, a_ptr, _ptr(sa), sa.size, b_ptr, _ptr(sb), sb.size, y_ptr))
+
+    def layernorm_dev(self, x_ptr, outer, norm, scale_ptr, bias_ptr, epsilon, y_ptr):
+        check(self._lib.pfr_layernorm_dev(self.handle, x_ptr, outer, norm, scale_ptr, bias_ptr, float(epsilon), y_ptr))
+
     # -- dynamic activation quantization ----------------------------------
     def dynamic_quantize_linear(self, x):
         """DynamicQuantizeLinear: (uint8 y of x's shape, float32 scale,
@@ -153,10 +199,11 @@ class Context:
         check(self._lib.pfr_nm_mask_dev(self.handle, w_ptr, total, int(n), int(m), mask_ptr))
 
     def gemm_csr_dev(self, A_ptr, Mb, K, BT, Y_ptr, alpha=1.0, beta=1.0, C_ptr=None, c_size=0,
-                     transA=False, mode="strict", relu=False):
-        if relu:
+                     transA=False, mode="strict", relu=False, gelu=False):
+        if relu or gelu:
+            act = _lib.ACT_GELU if gelu else _lib.ACT_RELU
             check(self._lib.pfr_gemm_csr_act_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
-                                                 alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode], _lib.ACT_RELU))
+                                                 alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode], act))
         else:
             check(self._lib.pfr_gemm_csr_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
                                              alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode]))
@@ -195,10 +242,11 @@ class CsrWeight:
         check(self.ctx._lib.pfr_spmm_csr(self.ctx.handle, self.handle, _ptr(X), N, _ptr(Y), _MODES[mode]))
         return Y
 
-    def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict", relu=False):
-        if relu:
+    def spmm_dev(self, X_ptr, N, Y_ptr, ldx=None, ldy=None, mode="strict", relu=False, gelu=False):
+        if relu or gelu:
+            act = _lib.ACT_GELU if gelu else _lib.ACT_RELU
             check(self.ctx._lib.pfr_spmm_csr_act_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
-                                                     ldy or N, _MODES[mode], _lib.ACT_RELU))
+                                                     ldy or N, _MODES[mode], act))
         else:
             check(self.ctx._lib.pfr_spmm_csr_dev(self.ctx.handle, self.handle, X_ptr, N, ldx or N, Y_ptr,
                                                  ldy or N, _MODES[mode]))

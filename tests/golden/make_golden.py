@@ -268,6 +268,41 @@ def gen_mlp(rng):
     return [n1, "mlp_784_512_10.pfm.gz"]
 
 
+def gen_neighbours(rng):
+    """The products' graph neighbours on the BERT-shaped workload: Gelu
+    (activation.cpp:239-259) over a wide range and special values,
+    LayerNormalization (nn.cpp:419-490) on [1024, 768]-like rows with random
+    scale and bias, two epsilons and a normalisation over the last two axes,
+    and Add (math.cpp:150-224) with equal shapes, a bias broadcast over the
+    last axis, a scalar and a middle-axis broadcast."""
+    g = np.concatenate([f32(rng.normal(0, 3, 4000)), f32(np.linspace(-12, 12, 2001)),
+                        f32([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 88.0, -88.0, np.inf, -np.inf, np.nan])])
+    out = {"gelu_x": g, "gelu_y": O.ref_op_f32("Gelu", [g])}
+    x = f32(rng.normal(0.5, 2.0, (64, 768)))
+    sc = f32(rng.normal(1.0, 0.2, 768))
+    bi = f32(rng.normal(0.0, 0.2, 768))
+    out.update(ln_x=x, ln_scale=sc, ln_bias=bi,
+               ln_y=O.ref_op_f32("LayerNormalization", [x, sc, bi], {"epsilon": 1e-5}, {"axis": -1}),
+               ln_y_eps12=O.ref_op_f32("LayerNormalization", [x, sc, bi], {"epsilon": 1e-12}, {"axis": -1}))
+    x3 = f32(rng.normal(0, 1, (4, 6, 32)))
+    sc3 = f32(rng.normal(1, 0.1, 6 * 32))
+    bi3 = f32(rng.normal(0, 0.1, 6 * 32))
+    out.update(ln3_x=x3, ln3_scale=sc3, ln3_bias=bi3,
+               ln3_y=O.ref_op_f32("LayerNormalization", [x3, sc3, bi3], {"epsilon": 1e-5}, {"axis": 1}))
+    a = f32(rng.normal(0, 1, (8, 16, 32)))
+    out.update(add_a=a, add_b_same=f32(rng.normal(0, 1, (8, 16, 32))), add_b_bias=f32(rng.normal(0, 1, 32)),
+               add_b_scalar=f32([0.375]), add_b_mid=f32(rng.normal(0, 1, (16, 1))))
+    for k in ("same", "bias", "scalar", "mid"):
+        out[f"add_y_{k}"] = O.ref_op_f32("Add", [a, out[f"add_b_{k}"]])
+    # both operands broadcast, and an empty operand against a size-1 one
+    # (the output takes the larger extent per axis and stays zero)
+    out.update(add2_a=f32(rng.normal(0, 1, (4, 1, 5))), add2_b=f32(rng.normal(0, 1, (3, 1))))
+    out["add2_y"] = O.ref_op_f32("Add", [out["add2_a"], out["add2_b"]])
+    out.update(add0_a=np.zeros((2, 0, 3), np.float32), add0_b=f32(rng.normal(0, 1, (1, 3))))
+    out["add0_y"] = O.ref_op_f32("Add", [out["add0_a"], out["add0_b"]])
+    return save("neighbours.npz", **out)
+
+
 def main():
     if not O.have_ref():
         raise SystemExit("build the reference library first: make -C oracle ref")
@@ -275,6 +310,7 @@ def main():
     names = [gen_kat(), gen_gemm(rng), gen_matmul(rng), gen_csr(rng), gen_masks(rng),
              gen_quant(rng), gen_qmatmul(rng), gen_bf16(rng)]
     names += gen_mlp(rng)
+    names.append(gen_neighbours(rng))
     manifest = {}
     for n in names:
         data = open(os.path.join(HERE, n), "rb").read()

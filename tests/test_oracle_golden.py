@@ -288,3 +288,28 @@ def test_oracle_matches_reference_random():
     w = rng.integers(-2, 3, 999).astype(np.float32)
     for n, m in ((2, 4), (3, 5)):
         assert same(O.orc_nm_mask(w, n, m), O.ref_nm_mask(w, n, m))
+
+
+def test_neighbours_golden(golden):
+    """Gelu, LayerNormalization and Add restated against the reference ops'
+    outputs, bit for bit (same libm tanhf as the reference build)."""
+    g = golden("neighbours.npz")
+    assert same(O.orc_gelu(g["gelu_x"]), g["gelu_y"])
+    assert same(O.orc_layernorm(g["ln_x"], g["ln_scale"], g["ln_bias"], 1e-5), g["ln_y"])
+    assert same(O.orc_layernorm(g["ln_x"], g["ln_scale"], g["ln_bias"], 1e-12), g["ln_y_eps12"])
+    assert same(O.orc_layernorm(g["ln3_x"], g["ln3_scale"], g["ln3_bias"], 1e-5, axis=1), g["ln3_y"])
+    for k in ("same", "bias", "scalar", "mid"):
+        assert same(O.orc_add(g["add_a"], g[f"add_b_{k}"]), g[f"add_y_{k}"]), k
+    assert same(O.orc_add(g["add2_a"], g["add2_b"]), g["add2_y"])
+    # an empty operand: the output takes the larger extent per axis (0 vs 1
+    # gives 1, not numpy's 0) and holds zeros
+    y0 = O.orc_add(g["add0_a"], g["add0_b"])
+    assert y0.shape == (2, 1, 3) and same(y0, g["add0_y"]) and not np.any(y0)
+    with pytest.raises(ValueError, match="not broadcastable"):
+        O.orc_add(np.zeros((3, 4), np.float32), np.zeros(3, np.float32))
+    # the bar is sensitive to rounding order: the same formula in float64
+    # (another summation and rounding sequence) does not give these bits
+    x, sc, bi = g["ln_x"].astype(np.float64), g["ln_scale"], g["ln_bias"]
+    d = x - x.mean(1, keepdims=True)
+    ln64 = (sc * d / np.sqrt((d * d).mean(1, keepdims=True) + 1e-5) + bi).astype(np.float32)
+    assert not same(ln64, g["ln_y"])
