@@ -129,9 +129,30 @@ struct pfr_csr {
     int4* sell_blk = nullptr;      // [sell_len + kSellTail]
     int32_t sell_nslab = 0, sell_nch = 0, sell_kc = 0;
     int64_t sell_len = 0;
+    // Row-chain copy for the in-order vector kernels (few columns, strict):
+    // rows sorted by count (descending) into slabs of chain_rows (16, 32 or
+    // 64); slab s holds chain_q0[s + 1] - chain_q0[s] quad rows, quad row g
+    // of slab s at index (chain_q0[s] + g) * chain_rows + lane, each holding steps
+    // 4g .. 4g+3 of that lane's row in storage order: four values (int8 or
+    // float, as val) and four columns.  When K < kChainXMax (chain_xlds) the
+    // kernel stages x in LDS with a zero at index K and a column is stored as
+    // the uint16 byte offset 4 * col; steps past a row's count hold value 0
+    // and offset 4 * K.  Otherwise columns are indices (uint16 when K <=
+    // 65536, else int32) and steps past a row's count hold value 0, column 0.
+    int32_t* chain_q0 = nullptr;    // [chain_nslab + 1]
+    int32_t* chain_len = nullptr;   // [chain_nslab * chain_rows] steps of each lane's row (0: none)
+    int32_t* chain_perm = nullptr;  // [chain_nslab * chain_rows] row of each lane, -1 none
+    void* chain_val = nullptr;
+    void* chain_col = nullptr;
+    int32_t chain_nslab = 0;
+    int32_t chain_rows = 64;
+    bool chain_c16 = false;
+    bool chain_xlds = false;
 };
 
 namespace pfr {
+constexpr int kChainRows = 64;     // rows per row-chain slab of the global-gather form (one folding lane each)
+constexpr int kChainXMax = 16384;  // x staged in LDS (with its zero slot) below this K
 constexpr int kSellRows = 16;      // rows per slab (one wave: 4 lanes x 4 columns per row)
 constexpr int kSellCols = 16;      // columns of X per workgroup slice
 constexpr int kSellMaxKC = 2048;   // K rows per LDS chunk (2048 x 64 B = 128 KiB)

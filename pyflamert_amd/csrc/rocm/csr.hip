@@ -33,7 +33,8 @@ T* dev_alloc_copy(const T* host, int64_t count, hipStream_t s) {
 void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
-                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk})
+                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0,
+                    (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -140,6 +141,78 @@ void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vecto
     PFR_HIP(hipStreamSynchronize(s));
 }
 
+// Row-chain copy (layout described at pfr_csr::chain_q0).  Rows are sorted
+// by count, longest first (ties by row index), so each slab's rows have
+// similar lengths and the padding to the slab maximum stays small.
+template <class V, class C>
+void fill_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
+                const std::vector<int32_t>& order, const std::vector<int32_t>& q0, hipStream_t s) {
+    const int64_t R = w->chain_rows, nslab = w->chain_nslab, nrec = (int64_t)q0.back() * R;
+    // staged-x form: byte offsets into the LDS copy of x, padding at its zero
+    // slot K; otherwise column indices, padding at column 0
+    // one spare quad row of padding after the last slab: the kernels' clamped
+    // loads may touch it
+    const int64_t mul = w->chain_xlds ? 4 : 1;
+    std::vector<V> v((size_t)((nrec + R) * 4), V(0));
+    std::vector<C> c((size_t)((nrec + R) * 4), C(w->chain_xlds ? w->K * 4 : 0));
+    std::vector<int32_t> len((size_t)(nslab * R), 0), perm((size_t)(nslab * R), -1);
+    for (int64_t i = 0; i < (int64_t)order.size(); ++i) {
+        const int32_t row = order[(size_t)i];
+        const int64_t sl = i / R, lane = i % R;
+        perm[(size_t)i] = row;
+        len[(size_t)i] = rowptr[row + 1] - rowptr[row];
+        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
+            const int64_t step = j - rowptr[row];
+            const size_t at = (size_t)((((int64_t)q0[(size_t)sl] + step / 4) * R + lane) * 4 + step % 4);
+            v[at] = vals[j];
+            c[at] = (C)(col[j] * mul);
+        }
+    }
+    w->chain_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
+    w->chain_col = dev_alloc_copy(c.data(), (int64_t)c.size(), s);
+    w->chain_len = dev_alloc_copy(len.data(), (int64_t)len.size(), s);
+    w->chain_perm = dev_alloc_copy(perm.data(), (int64_t)perm.size(), s);
+    w->chain_q0 = dev_alloc_copy(q0.data(), (int64_t)q0.size(), s);
+    PFR_HIP(hipStreamSynchronize(s));  // the host vectors go out of scope here
+}
+
+void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
+                 const void* vals, hipStream_t s) {
+    const int64_t M = w->M;
+    if (M == 0 || w->nnz == 0) return;
+    // Slab height: the staged-x kernel's per-CU LDS traffic and producer work
+    // per step grow with the rows a workgroup folds, so short matrices use
+    // 16-row slabs (which also spreads them over every CU); the global-gather
+    // kernel takes 64.
+    w->chain_xlds = w->K < pfr::kChainXMax;
+    const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
+    const int64_t R = !w->chain_xlds ? pfr::kChainRows : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
+    w->chain_rows = (int32_t)R;
+    std::vector<int32_t> order((size_t)M);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+        return rowptr[a + 1] - rowptr[a] > rowptr[b + 1] - rowptr[b];
+    });
+    const int64_t nslab = (M + R - 1) / R;
+    std::vector<int32_t> q0((size_t)nslab + 1, 0);
+    int64_t total = 0;
+    for (int64_t sl = 0; sl < nslab; ++sl) {
+        const int32_t first = order[(size_t)(sl * R)];  // the slab's longest row
+        total += (rowptr[first + 1] - rowptr[first] + 3) / 4;
+        if ((total + 1) * R * 4 > INT32_MAX) return;  // keep the block kernels
+        q0[(size_t)sl + 1] = (int32_t)total;
+    }
+    w->chain_nslab = (int32_t)nslab;
+    w->chain_c16 = w->chain_xlds || w->K <= 65536;
+    if (w->vdt == PFR_F32) {
+        if (w->chain_c16) fill_chain<float, uint16_t>(w, rowptr, col, static_cast<const float*>(vals), order, q0, s);
+        else fill_chain<float, int32_t>(w, rowptr, col, static_cast<const float*>(vals), order, q0, s);
+    } else {
+        if (w->chain_c16) fill_chain<int8_t, uint16_t>(w, rowptr, col, static_cast<const int8_t*>(vals), order, q0, s);
+        else fill_chain<int8_t, int32_t>(w, rowptr, col, static_cast<const int8_t*>(vals), order, q0, s);
+    }
+}
+
 pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
                const std::vector<int32_t>& col, const void* vals, pfr_dtype vdt,
                const float* row_scales) {
@@ -170,6 +243,7 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
                 if (col[j] <= col[j - 1]) { sorted = false; break; }
         w->cols_sorted = sorted;
         if (vdt == PFR_F32) build_sell(w, rowptr, col, static_cast<const float*>(vals), s);
+        build_chain(w, rowptr, col, vals, s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {

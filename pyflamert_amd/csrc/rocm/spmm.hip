@@ -6,6 +6,8 @@
 // sparse_tensor.cpp:500-510 / :543-548).  The whole file is compiled with
 // floating-point contraction off; fast mode asks for fmaf explicitly.
 #include <algorithm>
+#include <climits>
+#include <cstdint>
 #include <type_traits>
 
 #include "common.hpp"
@@ -222,6 +224,284 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
         const int64_t f = (int64_t)my_row * ldy_r;
         y[f] = bias_add(acc, f, bias, c_size, beta, act);
     }
+}
+
+// Strict SpMV over the row-chain copy (pfr_csr::chain_q0): one workgroup per
+// slab of 64 rows.  Eight producer waves compute the products RN(w * x[col])
+// (int8: w = RN(q * row scale)) of a 256-step chunk of all 64 rows into LDS,
+// with the next chunk's values and columns already in flight, while wave 0
+// folds the previous chunk: lane r adds row r's products in storage order,
+// one 16-byte LDS read per four steps.  Steps past a row's count give +0,
+// which leaves the sum unchanged (a sum that starts at +0 is never -0 under
+// round-to-nearest).  Two LDS buffers of 64 KiB alternate between producers
+// and folder, one barrier per chunk.
+constexpr int kChainCH = 64;                 // quad rows per chunk
+constexpr int kChainP = 8;                   // producer waves
+constexpr int kChainT = kChainCH / kChainP;  // quad rows per producer lane per chunk
+
+template <bool I8, bool C16>
+__global__ __launch_bounds__(64 * (kChainP + 1)) void k_spmv_chain(
+    const int32_t* __restrict__ q0, const int32_t* __restrict__ lens, const int32_t* __restrict__ perm,
+    const void* __restrict__ vals, const void* __restrict__ cols, const float* __restrict__ rs,
+    const float* __restrict__ x, int ldx, float* __restrict__ y, int64_t ldy_r,
+    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    __shared__ float4 buf[2][kChainCH * 64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.x;
+    const int qb = q0[s], nq = q0[s + 1] - qb;
+    const int nch = (nq + kChainCH - 1) / kChainCH;
+    const int row = perm[s * 64 + lane];
+    if (wave == 0) {
+        float acc = 0.0f;
+        for (int i = 0; i <= nch; ++i) {
+            if (i > 0) {
+                const float4* b = buf[(i - 1) & 1] + lane;
+                const int gq = min(kChainCH, nq - (i - 1) * kChainCH);
+#pragma unroll 8
+                for (int g = 0; g < gq; ++g) {
+                    const float4 v = b[g * 64];
+                    acc = acc + v.x;
+                    acc = acc + v.y;
+                    acc = acc + v.z;
+                    acc = acc + v.w;
+                }
+            }
+            __syncthreads();
+        }
+        if (row >= 0) {
+            const int64_t f = (int64_t)row * ldy_r;
+            y[f] = bias_add(acc, f, bias, c_size, beta, act);
+        }
+        return;
+    }
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;  // four steps' values
+    using ColT = typename std::conditional<C16, uint2, int4>::type;      // four steps' columns
+    const ValT* V = static_cast<const ValT*>(vals);
+    const ColT* Cl = static_cast<const ColT*>(cols);
+    const int len = lens[s * 64 + lane];
+    const float scale = (I8 && row >= 0) ? rs[row] : 1.0f;
+    const int pw = wave - 1;
+    ValT va[kChainT], vb[kChainT];
+    ColT ca[kChainT], cb[kChainT];
+    // Task t of chunk i is quad row i * kChainCH + pw + kChainP * t; the
+    // address is clamped into the slab so every load is issued.
+    auto load = [&](int i, ValT* v, ColT* c) {
+#pragma unroll
+        for (int t = 0; t < kChainT; ++t) {
+            const int g = min(i * kChainCH + pw + kChainP * t, nq - 1);
+            const int64_t at = (int64_t)(qb + g) * 64 + lane;
+            v[t] = V[at];
+            c[t] = Cl[at];
+        }
+    };
+    auto colk = [&](const ColT& c, int e) -> int {
+        if constexpr (C16) {
+            const uint32_t d = e < 2 ? c.x : c.y;
+            return (int)((e & 1) ? (d >> 16) : (d & 0xffffu));
+        } else {
+            return e == 0 ? c.x : (e == 1 ? c.y : (e == 2 ? c.z : c.w));
+        }
+    };
+    auto valk = [&](const ValT& v, int e) -> float {
+        if constexpr (I8) {
+            const float w = (float)(int8_t)((v >> (8 * e)) & 0xffu);
+            return w * scale;
+        } else {
+            return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+        }
+    };
+    // Chunk i from (vc, cc) into buffer i & 1, loading chunk i + 1 into
+    // (vn, cn); the loop alternates the two register sets, so no copy waits
+    // for the loads in flight.
+    auto chunk = [&](int i, const ValT* vc, const ColT* cc, ValT* vn, ColT* cn) {
+        if (i < nch) {
+            float xg[kChainT][4];
+#pragma unroll
+            for (int t = 0; t < kChainT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xg[t][e] = x[colk(cc[t], e) * ldx];
+            load(i + 1 < nch ? i + 1 : i, vn, cn);
+            float4* b = buf[i & 1] + lane;
+#pragma unroll
+            for (int t = 0; t < kChainT; ++t) {
+                const int gl = pw + kChainP * t;         // quad row within the chunk
+                const int j0 = 4 * (i * kChainCH + gl);  // first step of the quad
+                float p[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float prod = valk(vc[t], e) * xg[t][e];
+                    p[e] = j0 + e < len ? prod : 0.0f;
+                }
+                b[gl * 64] = make_float4(p[0], p[1], p[2], p[3]);
+            }
+        }
+        __syncthreads();
+    };
+    if (nq > 0) load(0, va, ca);
+    for (int i = 0; i <= nch; i += 2) {
+        chunk(i, va, ca, vb, cb);
+        if (i + 1 <= nch) chunk(i + 1, vb, cb, va, ca);
+    }
+}
+
+// The same with x staged in LDS (K < kChainXMax) and slabs of R = 16, 32 or
+// 64 rows (pfr_csr::chain_rows): one folding wave (lanes 0 .. R-1) and R / 8
+// producer waves, each producer instruction covering 64 / R quad rows of the
+// slab.  Columns are byte offsets into the LDS copy of x and padding steps
+// read its zero slot at K, so their products are RN(+0 * +0) = +0 with no
+// select.  A chunk is 128 steps; the values and offsets are loaded two chunks
+// ahead (three register sets in turn).  The loads are never skipped (chunk
+// indices past the slab are clamped, the spare padding row after the last
+// slab covers an empty slab) and the iteration count is a multiple of six,
+// so the loop body is straight-line code and the compiler waits only for
+// the oldest loads.  Dynamic LDS: 2 x CH quad rows x R x 16 B of products,
+// then K + 1 floats of x.
+template <int R>
+constexpr int chain_ch() { return 32; }  // quad rows per chunk (a multiple of 16: the fold's batches)
+constexpr int kChainXUnroll = 6;
+
+template <bool I8, int R>
+__global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
+    int K, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm, const void* __restrict__ vals,
+    const uint32_t* __restrict__ cols, const float* __restrict__ rs, const float* __restrict__ x, int ldx,
+    float* __restrict__ y, int64_t ldy_r, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    constexpr int P = R / 8;    // producer waves
+    constexpr int QW = 64 / R;  // quad rows per producer instruction
+    constexpr int kChainXCH = chain_ch<R>();
+    constexpr int kChainXT = kChainXCH * R / (64 * P);  // quad-row groups per producer lane per chunk
+    static_assert(kChainXCH * R == 64 * P * kChainXT, "chunk split");
+    extern __shared__ float4 dyn[];
+    float4* const buf0 = dyn;
+    float4* const buf1 = dyn + kChainXCH * R;
+    float* const xs = reinterpret_cast<float*>(dyn + 2 * kChainXCH * R);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.x;
+    const int qb = q0[s], nq = q0[s + 1] - qb;
+    const int nch = (nq + kChainXCH - 1) / kChainXCH;
+    // >= nch + 1 (the last fold needs one more barrier), a multiple of the unroll
+    const int iters = (nch + kChainXUnroll) / kChainXUnroll * kChainXUnroll;
+    for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
+    __syncthreads();
+    if (wave == 0) {
+        // The fold is bound by the latency of its dependent adds; the LDS
+        // reads of the next eight quad rows are issued before the adds of the
+        // current eight.  Whole chunks are folded: quad rows past the slab
+        // hold +0.
+        const int row = lane < R ? perm[s * R + lane] : -1;
+        float acc = 0.0f;
+        auto rd = [&](const float4* b, float4* r, int batch) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r[k] = b[(batch * 8 + k) * R];
+        };
+        auto add = [&](const float4* r) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                acc = acc + r[k].x;
+                acc = acc + r[k].y;
+                acc = acc + r[k].z;
+                acc = acc + r[k].w;
+            }
+        };
+        for (int i = 0; i < iters; ++i) {
+            if (lane < R && i > 0 && i - 1 < nch) {
+                const float4* b = ((i - 1) & 1 ? buf1 : buf0) + lane;
+                float4 ra[8], rb[8];
+                rd(b, ra, 0);
+#pragma unroll
+                for (int h = 0; h < kChainXCH / 8; h += 2) {
+                    if (h + 1 < kChainXCH / 8) rd(b, rb, h + 1);
+                    add(ra);
+                    if (h + 2 < kChainXCH / 8) rd(b, ra, h + 2);
+                    if (h + 1 < kChainXCH / 8) add(rb);
+                }
+            }
+            __syncthreads();
+        }
+        if (row >= 0) {
+            const int64_t f = (int64_t)row * ldy_r;
+            y[f] = bias_add(acc, f, bias, c_size, beta, act);
+        }
+        return;
+    }
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const int prow = perm[s * R + lane % R];
+    const float scale = (I8 && prow >= 0) ? rs[prow] : 1.0f;
+    const int pw = wave - 1;
+    const int sub = lane / R;  // quad row within the instruction's group
+    const char* xb = reinterpret_cast<const char*>(xs);
+    ValT v0[kChainXT], v1[kChainXT], v2[kChainXT];
+    uint2 c0[kChainXT], c1[kChainXT], c2[kChainXT];
+    // group t of chunk i: quad rows i * CH + (pw + P * t) * QW + sub
+    auto load = [&](int i, ValT* v, uint2* c) {
+#pragma unroll
+        for (int t = 0; t < kChainXT; ++t) {
+            const int g = max(min(i * kChainXCH + (pw + P * t) * QW + sub, nq - 1), 0);
+            const int64_t at = (int64_t)(qb + g) * R + lane % R;
+            v[t] = V[at];
+            c[t] = Cl[at];
+        }
+    };
+    auto valk = [&](const ValT& v, int e) -> float {
+        if constexpr (I8) {
+            const float w = (float)(int8_t)((v >> (8 * e)) & 0xffu);
+            return w * scale;
+        } else {
+            return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+        }
+    };
+    // chunk i (its products land in buffer i & 1; past the slab they are
+    // never folded), loading chunk i + 2
+    auto chunk = [&](int i, const ValT* vc, const uint2* cc, ValT* vn, uint2* cn) {
+        load(min(i + 2, nch - 1), vn, cn);
+        float4* b = ((i & 1) ? buf1 : buf0) + lane;
+#pragma unroll
+        for (int t = 0; t < kChainXT; ++t) {
+            const uint32_t o[4] = {cc[t].x & 0xffffu, cc[t].x >> 16, cc[t].y & 0xffffu, cc[t].y >> 16};
+            const bool in = i * kChainXCH + (pw + P * t) * QW + sub < nq;  // else a clamped copy: fold +0
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float prod = valk(vc[t], e) * *reinterpret_cast<const float*>(xb + o[e]);
+                p[e] = in ? prod : 0.0f;
+            }
+            b[(pw + P * t) * 64] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+        __syncthreads();
+    };
+    load(0, v0, c0);
+    load(min(1, nch - 1), v1, c1);
+    for (int i = 0; i < iters; i += 6) {
+        chunk(i, v0, c0, v2, c2);
+        chunk(i + 1, v1, c1, v0, c0);
+        chunk(i + 2, v2, c2, v1, c1);
+        chunk(i + 3, v0, c0, v2, c2);
+        chunk(i + 4, v1, c1, v0, c0);
+        chunk(i + 5, v2, c2, v1, c1);
+    }
+}
+
+template <bool I8, int R>
+void launch_chain_x(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, float* Y, int64_t ldy_r,
+                    const float* bias, int64_t c_size, float beta, int act) {
+    auto kern = k_spmv_chain_x<I8, R>;
+    constexpr int kChainXCH = chain_ch<R>();
+    const size_t lds = (size_t)(2 * kChainXCH * R) * 16 + (size_t)(W->K + 1) * 4;
+    // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
+    static uint64_t allowed = 0;  // bit d: done on device d (< 64)
+    const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
+    if (lds > 65536 && (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit))) {
+        const int most = 2 * kChainXCH * R * 16 + pfr::kChainXMax * 4;
+        PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    most));
+        if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)W->chain_nslab), dim3(64 * (1 + R / 8)), lds, ctx->stream, (int)W->K,
+                       W->chain_q0, W->chain_perm, W->chain_val, static_cast<const uint32_t*>(W->chain_col),
+                       W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
 }
 
 // Fast mode, N <= 8: one wave per row, lane l takes the row's nonzeros
@@ -583,6 +863,20 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
         else
             hipLaunchKernelGGL((k_spmv_fast<8, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
                                val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    } else if (N == 1 && W->chain_q0 != nullptr && W->chain_xlds && ldx < INT32_MAX) {
+        if (W->chain_rows == 16) launch_chain_x<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+        else if (W->chain_rows == 32) launch_chain_x<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+        else launch_chain_x<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (N == 1 && W->chain_q0 != nullptr && W->K * ldx < INT32_MAX) {
+        const dim3 grid((unsigned)W->chain_nslab), block(64 * (kChainP + 1));
+        if (W->chain_c16)
+            hipLaunchKernelGGL((k_spmv_chain<I8, true>), grid, block, 0, s, W->chain_q0, W->chain_len,
+                               W->chain_perm, W->chain_val, W->chain_col, rs, X, (int)ldx, Y, ldy_r, bias, c_size,
+                               beta, act);
+        else
+            hipLaunchKernelGGL((k_spmv_chain<I8, false>), grid, block, 0, s, W->chain_q0, W->chain_len,
+                               W->chain_perm, W->chain_val, W->chain_col, rs, X, (int)ldx, Y, ldy_r, bias, c_size,
+                               beta, act);
     } else if (N == 1) {
         hipLaunchKernelGGL(k_spmv_wg<I8>, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
                            W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta, act);

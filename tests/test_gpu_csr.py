@@ -271,6 +271,69 @@ def test_column_slice_layout_cases(ctx):
     assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
 
 
+def test_strict_vector_row_chains(ctx):
+    """The strict N = 1 kernel over the row-sorted chain copy: row lengths at
+    the 4-step and 256-step chunk edges and past several chunks, empty rows,
+    a row count that is not a multiple of 64, int32 columns (K > 65536),
+    +-inf and NaN in x at column 0 (the column padding steps point at: their
+    products must not reach any sum), a strided x, and the Gemm form with
+    one activation row, bias and fused activations.  Bit-exact against the
+    oracle."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    lens = [0, 1, 3, 4, 5, 255, 256, 257, 511, 512, 513, 1024, 1500, 0, 7, 64, 300, 2, 9, 777] * 5
+    lens = lens[:97]
+    for K in (4096, 70000):
+        ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        ix = np.concatenate([np.sort(rng.choice(K, n, replace=False)) for n in lens]).astype(np.int64)
+        v = rng.standard_normal(len(ix)).astype(np.float32)
+        M = len(lens)
+        W = ctx.csr_upload(M, K, ip, ix, v)
+        x = rng.standard_normal(K).astype(np.float32)
+        say(f"strict SpMV row chains M={M} K={K}")
+        assert bits_equal(W.spmm(x), O.orc_csr_spmv(M, K, ip, ix, v, x)), K
+        for bad in (np.inf, -np.inf, np.nan):
+            xb = x.copy()
+            xb[0] = bad
+            assert bits_equal(W.spmm(xb), O.orc_csr_spmv(M, K, ip, ix, v, xb)), (K, bad)
+        # int8 values with per-row scales
+        q = rng.integers(-127, 128, len(ix)).astype(np.int8)
+        q[q == 0] = 1
+        sc = (rng.random(M) * 0.01 + 1e-3).astype(np.float32)
+        Wq = ctx.csr_upload(M, K, ip, ix, q, row_scales=sc)
+        vals = workloads.dequant_rows(ip, q, sc)
+        assert bits_equal(Wq.spmm(x), O.orc_csr_spmv(M, K, ip, ix, vals, x)), K
+        # strided x (column 1 of a K x 3 matrix), strided y
+        X3 = rng.standard_normal((K, 3)).astype(np.float32)
+        dX = torch.from_numpy(X3).cuda()
+        dY = torch.zeros((M, 2), device="cuda")
+        W.spmm_dev(dX.data_ptr() + 4, 1, dY.data_ptr(), ldx=3, ldy=2)
+        ctx.synchronize()
+        assert bits_equal(dY.cpu().numpy()[:, 0], O.orc_csr_spmv(M, K, ip, ix, v, X3[:, 1].copy())), K
+        W.free()
+        Wq.free()
+    # Gemm form, one activation row: y = a . B + bias, then Relu / Gelu
+    K, Nf = 3000, 700
+    B = rng.standard_normal((K, Nf)).astype(np.float32)
+    B[rng.random(B.shape) >= 0.2] = 0
+    BT = ctx.csr_from_dense(B, transpose=True)
+    a = rng.standard_normal((1, K)).astype(np.float32)
+    bias = rng.standard_normal(Nf).astype(np.float32)
+    ref = O.orc_gemm(a, B, bias, 1.0, 1.0)
+    say("Gemm form, one row, bias")
+    assert bits_equal(ctx.gemm_csr(a, BT, 1.0, 1.0, bias), ref)
+    dA = torch.from_numpy(a).cuda()
+    dB = torch.from_numpy(bias).cuda()
+    dY = torch.empty((1, Nf), device="cuda")
+    ctx.gemm_csr_dev(dA.data_ptr(), 1, K, BT, dY.data_ptr(), 1.0, 1.0, dB.data_ptr(), Nf, relu=True)
+    ctx.synchronize()
+    assert bits_equal(dY.cpu().numpy(), relu_ref(ref))
+    ctx.gemm_csr_dev(dA.data_ptr(), 1, K, BT, dY.data_ptr(), 1.0, 1.0, dB.data_ptr(), Nf, gelu=True)
+    ctx.synchronize()
+    assert bits_equal(dY.cpu().numpy(), ctx.gelu(ref))
+
+
 def test_int8_csr_dequant_fused(ctx):
     """int8 CSR values with per-row scales: every product uses
     RN((float)q * scale[row]), i.e. dequantize_tensor followed by the fp32
