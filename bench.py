@@ -420,7 +420,9 @@ def bench_decode_int8(ctx):
             b.record()
             torch.cuda.synchronize()
             ms = a.elapsed_time(b) / 100
-            lb = nnz * 5 + 4 * (M_ + 1) + 4 * M_ + 4 * K_ * B + 4 * M_ * B
+            # algorithmic bytes: 1 B value + 2 B column (uint16 suffices for
+            # K <= 11008) per nonzero, 8 B per row (pointer and scale), x and y
+            lb = nnz * 3 + 8 * M_ + 4 * K_ * B + 4 * M_ * B
             per[name] = {"ms": round(ms, 5), "nnz": nnz, "gbs": round(lb / (ms * 1e-3) / 1e9, 1)}
             step_ms += 32 * count * ms
             byts += 32 * count * lb

@@ -504,6 +504,195 @@ void launch_chain_x(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx,
                        W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
 }
 
+// Strict product for 2 <= N <= 8 columns over the row-chain copy with 16-row
+// slabs: every (row, column) pair is its own in-order chain, one lane each,
+// so NC / 4 waves fold (NC = 2, 4 or 8, N <= NC) while four producer waves
+// load the values and offsets two chunks ahead, gather the x rows from global
+// memory (16-byte loads when x rows are aligned and N == NC >= 4) and write
+// RN(w * x[col, n]) for every column.  Steps past a row's count (and quad
+// rows past the slab) give +0; their gather addresses are clamped into x.
+// LDS: 2 x 32 quad rows x NC x 16 rows x 16 B of products.
+constexpr int kChainNR = 16;  // slab height this kernel takes
+constexpr int kChainNP = 4;   // producer waves
+
+template <int NC>
+constexpr int chain_n_folders() { return NC >= 4 ? NC / 4 : 1; }
+
+template <bool I8, int NC, bool XV>
+__global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spmm_chain(
+    int K, int N, int cshift, const int32_t* __restrict__ q0, const int32_t* __restrict__ lens,
+    const int32_t* __restrict__ perm, const void* __restrict__ vals, const uint32_t* __restrict__ cols,
+    const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r,
+    int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    constexpr int R = kChainNR, CH = 32, P = kChainNP, F = chain_n_folders<NC>(), QW = 64 / R;
+    constexpr int T = CH * R / (64 * P);  // quad-row groups per producer lane per chunk
+    static_assert(CH * R == 64 * P * T, "chunk split");
+    extern __shared__ float4 dyn[];
+    float4* const buf0 = dyn;
+    float4* const buf1 = dyn + CH * NC * R;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.x;
+    const int qb = q0[s], nq = q0[s + 1] - qb;
+    const int nch = (nq + CH - 1) / CH;
+    const int iters = (nch + kChainXUnroll) / kChainXUnroll * kChainXUnroll;
+    if (wave < F) {
+        const int c = wave * 64 + lane;  // chain: column c / R of slab row c % R
+        const int n = c / R, r = c % R;
+        const bool act_lane = c < NC * R && n < N;
+        const int row = act_lane ? perm[s * R + r] : -1;
+        float acc = 0.0f;
+        auto rd = [&](const float4* b, float4* v, int batch) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = b[(batch * 8 + k) * NC * R];
+        };
+        auto add = [&](const float4* v) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                acc = acc + v[k].x;
+                acc = acc + v[k].y;
+                acc = acc + v[k].z;
+                acc = acc + v[k].w;
+            }
+        };
+        for (int i = 0; i < iters; ++i) {
+            if (act_lane && i > 0 && i - 1 < nch) {
+                const float4* b = ((i - 1) & 1 ? buf1 : buf0) + n * R + r;
+                float4 ra[8], rb[8];
+                rd(b, ra, 0);
+#pragma unroll
+                for (int h = 0; h < CH / 8; h += 2) {
+                    rd(b, rb, h + 1);
+                    add(ra);
+                    if (h + 2 < CH / 8) rd(b, ra, h + 2);
+                    add(rb);
+                }
+            }
+            __syncthreads();
+        }
+        if (row >= 0) {
+            const int64_t f = (int64_t)row * ldy_r + (int64_t)n * ldy_c;
+            Y[f] = bias_add(acc, f, bias, c_size, beta, act);
+        }
+        return;
+    }
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const int r = lane % R, sub = lane / R;
+    const int prow = perm[s * R + r];
+    const int len = lens[s * R + r];
+    const float scale = (I8 && prow >= 0) ? rs[prow] : 1.0f;
+    const int pw = wave - F;
+    ValT v0[T], v1[T], v2[T];
+    uint2 c0[T], c1[T], c2[T];
+    auto load = [&](int i, ValT* v, uint2* cc) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int g = max(min(i * CH + (pw + P * t) * QW + sub, nq - 1), 0);
+            const int64_t at = (int64_t)(qb + g) * R + r;
+            v[t] = V[at];
+            cc[t] = Cl[at];
+        }
+    };
+    auto valk = [&](const ValT& v, int e) -> float {
+        if constexpr (I8) {
+            const float w = (float)(int8_t)((v >> (8 * e)) & 0xffu);
+            return w * scale;
+        } else {
+            return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+        }
+    };
+    auto chunk = [&](int i, const ValT* vc, const uint2* cc, ValT* vn, uint2* cn) {
+        load(min(i + 2, nch - 1), vn, cn);
+        float xg[T][4][NC];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t o = (e < 2 ? cc[t].x : cc[t].y) >> (16 * (e & 1)) & 0xffffu;
+                const int col = min((int)(o >> cshift), K - 1);
+                const float* xr = X + (int64_t)col * ldx;
+                if constexpr (XV) {
+#pragma unroll
+                    for (int q = 0; q < NC / 4; ++q) {
+                        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+                        xg[t][e][4 * q] = v.x;
+                        xg[t][e][4 * q + 1] = v.y;
+                        xg[t][e][4 * q + 2] = v.z;
+                        xg[t][e][4 * q + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NC; ++q) xg[t][e][q] = xr[min(q, N - 1)];
+                }
+            }
+        float4* b = ((i & 1) ? buf1 : buf0);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int gl = (pw + P * t) * QW + sub;  // quad row within the chunk
+            const int j0 = 4 * (i * CH + gl);         // its first step
+            float w[4];
+            bool ok[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                w[e] = valk(vc[t], e);
+                ok[e] = j0 + e < len;  // also false past the slab (len <= 4 * nq)
+            }
+#pragma unroll
+            for (int q = 0; q < NC; ++q) {
+                float p[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float prod = w[e] * xg[t][e][q];
+                    p[e] = ok[e] ? prod : 0.0f;
+                }
+                b[(gl * NC + q) * R + r] = make_float4(p[0], p[1], p[2], p[3]);
+            }
+        }
+        __syncthreads();
+    };
+    load(0, v0, c0);
+    load(min(1, nch - 1), v1, c1);
+    for (int i = 0; i < iters; i += 6) {
+        chunk(i, v0, c0, v2, c2);
+        chunk(i + 1, v1, c1, v0, c0);
+        chunk(i + 2, v2, c2, v1, c1);
+        chunk(i + 3, v0, c0, v2, c2);
+        chunk(i + 4, v1, c1, v0, c0);
+        chunk(i + 5, v2, c2, v1, c1);
+    }
+}
+
+template <bool I8, int NC, bool XV>
+void launch_chain_n(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y, int64_t ldy_r,
+                    int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
+    auto kern = k_spmm_chain<I8, NC, XV>;
+    const size_t lds = (size_t)2 * 32 * NC * kChainNR * 16;
+    static uint64_t allowed = 0;  // bit d: more than 64 KiB of dynamic LDS allowed on device d (< 64)
+    const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
+    if (lds > 65536 && (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit))) {
+        PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds));
+        if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)W->chain_nslab), dim3(64 * (chain_n_folders<NC>() + kChainNP)), lds,
+                       ctx->stream, (int)W->K, N, W->chain_xlds ? 2 : 0, W->chain_q0, W->chain_len, W->chain_perm,
+                       W->chain_val, static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, ldx, Y, ldy_r,
+                       ldy_c, bias, c_size, beta, act);
+}
+
+template <bool I8>
+void launch_chain_cols(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
+                       int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
+    const bool xv = ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    if (N <= 2) launch_chain_n<I8, 2, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    else if (N <= 4 && N == 4 && xv) launch_chain_n<I8, 4, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    else if (N <= 4) launch_chain_n<I8, 4, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    else if (N == 8 && xv) launch_chain_n<I8, 8, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    else launch_chain_n<I8, 8, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+}
+
 // Fast mode, N <= 8: one wave per row, lane l takes the row's nonzeros
 // l, l + 64, ... (coalesced index and value streams).  Each lane issues the
 // loads of U nonzeros at once (indices clamped into the row, so every load
@@ -867,6 +1056,8 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
         if (W->chain_rows == 16) launch_chain_x<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else if (W->chain_rows == 32) launch_chain_x<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else launch_chain_x<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (N >= 2 && N <= 8 && W->chain_q0 != nullptr && W->chain_rows == kChainNR && W->chain_c16) {
+        launch_chain_cols<I8>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else if (N == 1 && W->chain_q0 != nullptr && W->K * ldx < INT32_MAX) {
         const dim3 grid((unsigned)W->chain_nslab), block(64 * (kChainP + 1));
         if (W->chain_c16)

@@ -311,6 +311,21 @@ def test_strict_vector_row_chains(ctx):
         W.spmm_dev(dX.data_ptr() + 4, 1, dY.data_ptr(), ldx=3, ldy=2)
         ctx.synchronize()
         assert bits_equal(dY.cpu().numpy()[:, 0], O.orc_csr_spmv(M, K, ip, ix, v, X3[:, 1].copy())), K
+        # 2 .. 8 columns (one in-order chain per row and column), with +-inf
+        # and NaN in the first and last x rows (padding steps clamp there)
+        for n in (2, 3, 4, 5, 8):
+            Xn = rng.standard_normal((K, n)).astype(np.float32)
+            Xn[0, 0], Xn[K - 1, n - 1], Xn[K - 1, 0] = np.inf, np.nan, -np.inf
+            say(f"strict row chains M={M} K={K} N={n}")
+            assert bits_equal(W.spmm(Xn), O.orc_csr_spmm(M, K, ip, ix, v, Xn)), (K, n)
+            assert bits_equal(Wq.spmm(Xn), O.orc_csr_spmm(M, K, ip, ix, vals, Xn)), (K, n)
+        # strided X and Y for several columns
+        X9 = rng.standard_normal((K, 9)).astype(np.float32)
+        dX = torch.from_numpy(X9).cuda()
+        dY = torch.zeros((M, 11), device="cuda")
+        W.spmm_dev(dX.data_ptr(), 8, dY.data_ptr(), ldx=9, ldy=11)
+        ctx.synchronize()
+        assert bits_equal(dY.cpu().numpy()[:, :8], O.orc_csr_spmm(M, K, ip, ix, v, X9[:, :8].copy())), K
         W.free()
         Wq.free()
     # Gemm form, one activation row: y = a . B + bias, then Relu / Gelu
