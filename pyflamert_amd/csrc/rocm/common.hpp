@@ -105,6 +105,7 @@ struct pfr_csr {
     int64_t M = 0, K = 0, nnz = 0;
     int32_t* rowptr = nullptr;  // [M+1]
     int32_t* col = nullptr;     // [nnz], ascending within a row
+    uint16_t* col16 = nullptr;  // [nnz] the same columns as uint16 when K <= 65536 (fast vector kernel)
     void* val = nullptr;        // [nnz] float or int8
     pfr_dtype vdt = PFR_F32;
     float* row_scale = nullptr;  // [M] for int8 values

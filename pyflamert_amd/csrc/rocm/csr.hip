@@ -33,7 +33,7 @@ T* dev_alloc_copy(const T* host, int64_t count, hipStream_t s) {
 void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
-                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0,
+                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0, (void*)w->col16,
                     (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col})
         if (p) (void)hipFree(p);
     delete w;
@@ -229,6 +229,11 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
         hipStream_t s = ctx->stream;
         w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
         w->col = dev_alloc_copy(col.data(), w->nnz, s);
+        if (K <= 65536 && w->nnz > 0) {
+            std::vector<uint16_t> c16(col.begin(), col.end());
+            w->col16 = dev_alloc_copy(c16.data(), w->nnz, s);
+            PFR_HIP(hipStreamSynchronize(s));  // c16 goes out of scope
+        }
         if (vdt == PFR_F32)
             w->val = dev_alloc_copy(static_cast<const float*>(vals), w->nnz, s);
         else

@@ -700,28 +700,36 @@ void launch_chain_cols(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, in
 // per nonzero for NB = 8 when X rows are 16-byte aligned), then fused
 // multiply-adds into per-column partial sums, reduced across the wave at
 // the end.  The sum is reassociated, so this kernel serves the fast mode
-// only.
-template <int NB, bool I8, bool XV>
+// only.  Columns are read as uint16 when the weight has that copy (K <=
+// 65536: 3 bytes per int8 nonzero instead of 5).
+//
+// WG = true: the whole 256-thread workgroup takes one row (thread t takes
+// the row's nonzeros t, t + 256, ...; the wave sums meet in LDS), so a row of
+// a few thousand nonzeros has all its loads in flight at once instead of
+// waiting for several rounds of one wave.
+template <int NB, bool I8, bool XV, class CT, bool WG = false>
 __global__ __launch_bounds__(256) void k_spmv_fast(
-    int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+    int M, int N, const int32_t* __restrict__ rowptr, const CT* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias, int64_t c_size,
     float beta, int act) {
     constexpr int U = NB == 1 ? 16 : (NB <= 4 ? 8 : 4);
-    const int lane = threadIdx.x & 63;
-    const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kWaves + (int)(threadIdx.x >> 6));
+    constexpr int S = WG ? 256 : 64;  // threads sharing a row
+    const int lane = WG ? (int)threadIdx.x : (int)(threadIdx.x & 63);
+    const int row = WG ? (int)blockIdx.x
+                       : __builtin_amdgcn_readfirstlane((int)blockIdx.x * kWaves + (int)(threadIdx.x >> 6));
     if (row >= M) return;
     const int beg = rowptr[row], end = rowptr[row + 1];
     float acc[NB];
 #pragma unroll
     for (int c = 0; c < NB; ++c) acc[c] = 0.0f;
-    for (int base = beg; base < end; base += 64 * U) {
+    for (int base = beg; base < end; base += S * U) {
         int cl[U];
         float w[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int jj = min(base + lane + 64 * u, end - 1);
-            cl[u] = col[jj];
+            const int jj = max(min(base + lane + S * u, end - 1), 0);
+            cl[u] = (int)col[jj];
             w[u] = wval<I8>(val, rs, jj, row);
         }
         float xv[U][NB];
@@ -741,7 +749,7 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (base + lane + 64 * u < end) {
+            if (base + lane + S * u < end) {
 #pragma unroll
                 for (int c = 0; c < NB; ++c) acc[c] = __builtin_fmaf(w[u], xv[u][c], acc[c]);
             }
@@ -753,6 +761,18 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
         acc[c] = v;
+    }
+    if constexpr (WG) {
+        __shared__ float part[4][NB];
+        const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+        if (l == 0) {
+#pragma unroll
+            for (int c = 0; c < NB; ++c) part[wv][c] = acc[c];
+        }
+        __syncthreads();
+        if (wv != 0) return;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) acc[c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
     }
     if (lane < N && lane < NB) {
         float v = acc[0];
@@ -1040,18 +1060,34 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     if (FAST && N <= 8) {
         const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
         const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);
-        if (N == 1)
-            hipLaunchKernelGGL((k_spmv_fast<1, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
-        else if (N <= 4)
-            hipLaunchKernelGGL((k_spmv_fast<4, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
-        else if (xv)
-            hipLaunchKernelGGL((k_spmv_fast<8, I8, true>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
-        else
-            hipLaunchKernelGGL((k_spmv_fast<8, I8, false>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr, W->col,
-                               val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        // a workgroup per row when rows are long (mean of at least 2048
+        // nonzeros: measured faster on 4096 x 11008 at 30 %, slower on
+        // 4096 x 4096 and 11008 x 4096 at 30 %)
+        const bool wg = W->nnz >= 2048 * (int64_t)M;
+#define PFR_FASTV(NBV, XVV, COL)                                                                               \
+    do {                                                                                                       \
+        using CTy = std::remove_const_t<std::remove_pointer_t<decltype(COL)>>;                                 \
+        if (wg)                                                                                                \
+            hipLaunchKernelGGL((k_spmv_fast<NBV, I8, XVV, CTy, true>), dim3((unsigned)M), dim3(256), 0, s, M, \
+                               (int)N, W->rowptr, COL, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act); \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_spmv_fast<NBV, I8, XVV, CTy>), dim3(grid), dim3(256), 0, s, M, (int)N,       \
+                               W->rowptr, COL, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);     \
+    } while (0)
+#define PFR_FASTC(COL)                               \
+    if (N == 1) PFR_FASTV(1, false, COL);            \
+    else if (N <= 4) PFR_FASTV(4, false, COL);       \
+    else if (xv) PFR_FASTV(8, true, COL);            \
+    else PFR_FASTV(8, false, COL);
+        if (W->col16) {
+            const uint16_t* c16 = W->col16;
+            PFR_FASTC(c16)
+        } else {
+            const int32_t* c32 = W->col;
+            PFR_FASTC(c32)
+        }
+#undef PFR_FASTC
+#undef PFR_FASTV
     } else if (N == 1 && W->chain_q0 != nullptr && W->chain_xlds && ldx < INT32_MAX) {
         if (W->chain_rows == 16) launch_chain_x<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else if (W->chain_rows == 32) launch_chain_x<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
