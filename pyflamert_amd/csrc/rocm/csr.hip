@@ -181,12 +181,16 @@ void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vect
     const int64_t M = w->M;
     if (M == 0 || w->nnz == 0) return;
     // Slab height: the staged-x kernel's per-CU LDS traffic and producer work
-    // per step grow with the rows a workgroup folds, so short matrices use
-    // 16-row slabs (which also spreads them over every CU); the global-gather
-    // kernel takes 64.
+    // per step grow with the rows a workgroup folds, so matrices with long
+    // rows and few of them use 16-row slabs (which also spreads them over
+    // every CU).  Short rows (mean under 1024) keep 64-row slabs: there every
+    // workgroup's start (staging x, the first loads) outweighs the fold, and
+    // fewer workgroups start fewer times.  The global-gather kernel takes 64.
     w->chain_xlds = w->K < pfr::kChainXMax;
     const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
-    const int64_t R = !w->chain_xlds ? pfr::kChainRows : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
+    const bool long_rows = w->nnz >= 1024 * M;
+    const int64_t R = !w->chain_xlds || !long_rows ? pfr::kChainRows
+                                                    : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
     w->chain_rows = (int32_t)R;
     std::vector<int32_t> order((size_t)M);
     std::iota(order.begin(), order.end(), 0);

@@ -382,9 +382,9 @@ __global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
     const int nch = (nq + kChainXCH - 1) / kChainXCH;
     // >= nch + 1 (the last fold needs one more barrier), a multiple of the unroll
     const int iters = (nch + kChainXUnroll) / kChainXUnroll * kChainXUnroll;
-    for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
-    __syncthreads();
     if (wave == 0) {
+        for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
+        __syncthreads();
         // The fold is bound by the latency of its dependent adds; the LDS
         // reads of the next eight quad rows are issued before the adds of the
         // current eight.  Whole chunks are folded: quad rows past the slab
@@ -472,8 +472,12 @@ __global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
         }
         __syncthreads();
     };
+    // the first two chunks' loads go out before x is staged, so the two
+    // latencies overlap
     load(0, v0, c0);
     load(min(1, nch - 1), v1, c1);
+    for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
+    __syncthreads();
     for (int i = 0; i < iters; i += 6) {
         chunk(i, v0, c0, v2, c2);
         chunk(i + 1, v1, c1, v0, c0);

@@ -328,6 +328,29 @@ def test_strict_vector_row_chains(ctx):
         assert bits_equal(dY.cpu().numpy()[:, :8], O.orc_csr_spmm(M, K, ip, ix, v, X9[:, :8].copy())), K
         W.free()
         Wq.free()
+    # long rows (mean >= 1024: the 16-row slab layout and its 1..8-column
+    # kernels), empty and single-entry rows among them
+    K = 6000
+    lens = list(rng.integers(1024, 3000, 90)) + [0, 1, 5999, 6000, 4, 1023, 1024, 1025]
+    M = len(lens)
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    ix = np.concatenate([np.sort(rng.choice(K, n, replace=False)) for n in lens]).astype(np.int64)
+    v = rng.standard_normal(len(ix)).astype(np.float32)
+    q = rng.integers(-127, 128, len(ix)).astype(np.int8)
+    q[q == 0] = 3
+    sc = (rng.random(M) * 0.01 + 1e-3).astype(np.float32)
+    vals = workloads.dequant_rows(ip, q, sc)
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    Wq = ctx.csr_upload(M, K, ip, ix, q, row_scales=sc)
+    for n in (1, 2, 3, 4, 7, 8):
+        Xn = rng.standard_normal((K, n)).astype(np.float32)
+        Xn[0, 0], Xn[K - 1, n - 1] = np.inf, np.nan
+        Xa = Xn[:, 0].copy() if n == 1 else Xn
+        say(f"strict long-row chains M={M} K={K} N={n}")
+        assert bits_equal(W.spmm(Xa), O.orc_csr_spmm(M, K, ip, ix, v, Xa)), n
+        assert bits_equal(Wq.spmm(Xa), O.orc_csr_spmm(M, K, ip, ix, vals, Xa)), n
+    W.free()
+    Wq.free()
     # Gemm form, one activation row: y = a . B + bias, then Relu / Gelu
     K, Nf = 3000, 700
     B = rng.standard_normal((K, Nf)).astype(np.float32)
