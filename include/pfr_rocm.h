@@ -267,6 +267,26 @@ int pfr_layernorm(pfr_ctx* ctx, const float* x, int64_t outer, int64_t norm,
 int pfr_layernorm_dev(pfr_ctx* ctx, const float* x, int64_t outer, int64_t norm,
                       const float* scale, const float* bias, float epsilon, float* y);
 
+/* ---- per-tensor quantize / dequantize ------------------------------------ */
+
+/* QuantizeLinear and Quantize (cpu_quantize_linear, quantized_ops.cpp:284-315;
+ * cpu_quantize, :35-55): quantize_tensor with per-tensor parameters
+ * (quant_ops.cpp:15-57): q = clamp((int32) round(x * (1 / scale)) + zero_point)
+ * to int8 (out_dtype PFR_I8) or uint8 (PFR_U8); bit-exact.  scale must be
+ * positive and finite (QuantParams::per_tensor, quant_params.hpp:60-82).
+ * Host pointers; _dev: device pointers, no synchronisation. */
+int pfr_quantize_linear(pfr_ctx* ctx, const float* x, int64_t n, float scale,
+                        int32_t zero_point, pfr_dtype out_dtype, void* y);
+int pfr_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, float scale,
+                            int32_t zero_point, pfr_dtype out_dtype, void* y);
+/* DequantizeLinear and Dequantize (cpu_dequantize_linear, :321-347;
+ * cpu_dequantize, :57-70): dequantize_tensor per tensor (quant_ops.cpp:
+ * 129-157): y = ((float) q - (float) zero_point) * scale; q int8 or uint8. */
+int pfr_dequantize_linear(pfr_ctx* ctx, const void* q, pfr_dtype q_dtype, int64_t n,
+                          float scale, int32_t zero_point, float* y);
+int pfr_dequantize_linear_dev(pfr_ctx* ctx, const void* q, pfr_dtype q_dtype, int64_t n,
+                              float scale, int32_t zero_point, float* y);
+
 /* ---- dynamic activation quantization -------------------------------------- */
 
 /* DynamicQuantizeLinear (cpu_dynamic_quantize_linear, quantized_ops.cpp:

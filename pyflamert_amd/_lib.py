@@ -80,6 +80,10 @@ SIGNATURES = {
     "pfr_gelu_dev": (_INT, [_P, _P, _I64, _P]),
     "pfr_add": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
     "pfr_add_dev": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
+    "pfr_quantize_linear": (_INT, [_P, _P, _I64, _F, _I32, _INT, _P]),
+    "pfr_quantize_linear_dev": (_INT, [_P, _P, _I64, _F, _I32, _INT, _P]),
+    "pfr_dequantize_linear": (_INT, [_P, _P, _INT, _I64, _F, _I32, _P]),
+    "pfr_dequantize_linear_dev": (_INT, [_P, _P, _INT, _I64, _F, _I32, _P]),
     "pfr_layernorm": (_INT, [_P, _P, _I64, _I64, _P, _P, _F, _P]),
     "pfr_layernorm_dev": (_INT, [_P, _P, _I64, _I64, _P, _P, _F, _P]),
 }

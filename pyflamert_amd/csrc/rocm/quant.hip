@@ -1,3 +1,5 @@
+// Per-tensor QuantizeLinear / DequantizeLinear (and the Quantize /
+// Dequantize ops, which take the same parameters from attributes), and
 // DynamicQuantizeLinear on the GPU (cpu_dynamic_quantize_linear,
 // quantized_ops.cpp:251-278): per-tensor uint8 asymmetric parameters from
 // the data, then the quantized tensor.
@@ -115,6 +117,68 @@ __global__ __launch_bounds__(256) void k_dql_quant(const float* __restrict__ x, 
     y[i] = (uint8_t)q;
 }
 
+// Per-tensor quantize (quantize_tensor, quant_ops.cpp:15-57): inv = 1 /
+// scale, q = (int32) round(x * inv) + zero point (x86 conversion and
+// wrapping add), clamped to [-128, 127] or [0, 255].
+template <bool U8>
+__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, int64_t n, float inv, int32_t zp,
+                                                  void* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(x[i] * inv)) + (uint32_t)zp);
+    if (U8) {
+        q = q < 0 ? 0 : (q > 255 ? 255 : q);
+        static_cast<uint8_t*>(y)[i] = (uint8_t)q;
+    } else {
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        static_cast<int8_t*>(y)[i] = (int8_t)q;
+    }
+}
+
+// Per-tensor dequantize (dequantize_tensor, quant_ops.cpp:129-157):
+// ((float) q - (float) zero point) * scale.
+template <bool U8>
+__global__ __launch_bounds__(256) void k_dequantize(const void* __restrict__ q, int64_t n, float scale, float zpf,
+                                                    float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = U8 ? (float)static_cast<const uint8_t*>(q)[i] : (float)static_cast<const int8_t*>(q)[i];
+    y[i] = (v - zpf) * scale;
+}
+
+// QuantParams::per_tensor (quant_params.hpp:60-82): the checks and texts.
+void per_tensor_checks(float scale, pfr_dtype dt) {
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        throw pfr::Error(PFR_ERR_INVALID_ARG, "QuantParams::per_tensor: scale must be positive and finite");
+    if (dt != PFR_I8 && dt != PFR_U8)
+        throw pfr::Error(PFR_ERR_INVALID_ARG, "QuantParams::per_tensor: dtype must be Int8 or UInt8");
+}
+
+void quantize_dev(pfr_ctx* ctx, const float* x, int64_t n, float scale, int32_t zp, pfr_dtype dt, void* y) {
+    pfr::require(n >= 0, "negative element count");
+    per_tensor_checks(scale, dt);
+    if (n == 0) return;
+    pfr::require(x && y, "null x/y");
+    const float inv = 1.0f / scale;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (dt == PFR_U8) hipLaunchKernelGGL(k_quantize<true>, grid, dim3(256), 0, ctx->stream, x, n, inv, zp, y);
+    else hipLaunchKernelGGL(k_quantize<false>, grid, dim3(256), 0, ctx->stream, x, n, inv, zp, y);
+    PFR_HIP(hipGetLastError());
+}
+
+void dequantize_dev(pfr_ctx* ctx, const void* q, pfr_dtype dt, int64_t n, float scale, int32_t zp, float* y) {
+    pfr::require(n >= 0, "negative element count");
+    per_tensor_checks(scale, dt);  // the parameters are built before dequantize_tensor runs
+    if (n == 0) return;
+    pfr::require(q && y, "null q/y");
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (dt == PFR_U8)
+        hipLaunchKernelGGL(k_dequantize<true>, grid, dim3(256), 0, ctx->stream, q, n, scale, (float)zp, y);
+    else
+        hipLaunchKernelGGL(k_dequantize<false>, grid, dim3(256), 0, ctx->stream, q, n, scale, (float)zp, y);
+    PFR_HIP(hipGetLastError());
+}
+
 void dql_dev(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y, float* scale, uint8_t* zp, int32_t* status) {
     pfr::require(n >= 0, "negative element count");
     pfr::require(scale && zp, "null scale/zero-point output");
@@ -137,6 +201,56 @@ int pfr_dynamic_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, uin
     return pfr::guarded([&] {
         pfr::bind(ctx);
         dql_dev(ctx, x, n, y, scale, zero_point, status);
+    });
+}
+
+int pfr_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, float scale, int32_t zero_point,
+                            pfr_dtype out_dtype, void* y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        quantize_dev(ctx, x, n, scale, zero_point, out_dtype, y);
+    });
+}
+
+int pfr_quantize_linear(pfr_ctx* ctx, const float* x, int64_t n, float scale, int32_t zero_point,
+                        pfr_dtype out_dtype, void* y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        per_tensor_checks(scale, out_dtype);
+        if (n == 0) return;
+        pfr::require(x && y, "null x/y");
+        float* dx = static_cast<float*>(ctx->scratch[0].ensure((size_t)n * 4));
+        void* dy = ctx->scratch[2].ensure((size_t)n);
+        PFR_HIP(hipMemcpyAsync(dx, x, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+        quantize_dev(ctx, dx, n, scale, zero_point, out_dtype, dy);
+        PFR_HIP(hipMemcpyAsync(y, dy, (size_t)n, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+int pfr_dequantize_linear_dev(pfr_ctx* ctx, const void* q, pfr_dtype q_dtype, int64_t n, float scale,
+                              int32_t zero_point, float* y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        dequantize_dev(ctx, q, q_dtype, n, scale, zero_point, y);
+    });
+}
+
+int pfr_dequantize_linear(pfr_ctx* ctx, const void* q, pfr_dtype q_dtype, int64_t n, float scale,
+                          int32_t zero_point, float* y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        per_tensor_checks(scale, q_dtype);
+        if (n == 0) return;
+        pfr::require(q && y, "null q/y");
+        void* dq = ctx->scratch[0].ensure((size_t)n);
+        float* dy = static_cast<float*>(ctx->scratch[2].ensure((size_t)n * 4));
+        PFR_HIP(hipMemcpyAsync(dq, q, (size_t)n, hipMemcpyHostToDevice, ctx->stream));
+        dequantize_dev(ctx, dq, q_dtype, n, scale, zero_point, dy);
+        PFR_HIP(hipMemcpyAsync(y, dy, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
     });
 }
 

@@ -367,6 +367,12 @@ void RocmExecutor::build_plan(const Graph& graph) {
             st.op = PlanStep::Add;
         else if (op == "LayerNormalization" && n->inputs().size() == 3)
             st.op = PlanStep::LayerNorm;
+        else if ((op == "Quantize" && n->inputs().size() == 1) ||
+                 (op == "QuantizeLinear" && n->inputs().size() >= 2 && n->inputs().size() <= 3))
+            st.op = PlanStep::Quant;
+        else if ((op == "Dequantize" && n->inputs().size() == 1) ||
+                 (op == "DequantizeLinear" && n->inputs().size() >= 2 && n->inputs().size() <= 3))
+            st.op = PlanStep::Dequant;
         else if (dynq)
             st.op = PlanStep::DynQuant;
         else
@@ -653,6 +659,67 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 pfr_check(pfr_add_dev(ctx_, static_cast<const float*>(a.p), a.shape.data(), (int)a.shape.size(),
                                       static_cast<const float*>(b.p), b.shape.data(), (int)b.shape.size(),
                                       static_cast<float*>(out.p)));
+                break;
+            }
+            case PlanStep::Quant:
+            case PlanStep::Dequant: {
+                // quantized_ops.cpp:35-70, :284-347: per-tensor parameters from
+                // attributes or from the first elements of the scale and zero
+                // point inputs (read back when a node produced them)
+                const bool q = st.op == PlanStep::Quant;
+                const bool lin = n->op_type().size() > 8 && n->op_type().compare(n->op_type().size() - 6, 6, "Linear") == 0;
+                const DevTensor& x = act_in(0);
+                float scale = n->get_attr<float>("scale", 1.0f);
+                int32_t zp = (int32_t)n->get_attr<int64_t>("zero_point", 0);
+                auto first_bytes = [&](size_t i, void* dst, size_t bytes) {
+                    if (graph.has_initializer(in[i])) {
+                        std::memcpy(dst, initializer_value(graph, in[i]).data(), bytes);
+                    } else {
+                        pfr_check(pfr_copy_to_host(ctx_, dst, act_in(i).p, (int64_t)bytes));
+                    }
+                };
+                auto in_dtype = [&](size_t i) {
+                    return graph.has_initializer(in[i]) ? initializer_value(graph, in[i]).dtype() : act_in(i).dtype;
+                };
+                auto in_numel = [&](size_t i) {
+                    return graph.has_initializer(in[i]) ? initializer_value(graph, in[i]).num_elements()
+                                                        : numel(act_in(i).shape);
+                };
+                if (lin) {
+                    if (in_dtype(1) != DType::Float32 || in_numel(1) < 1)
+                        throw std::invalid_argument(n->op_type() + ": scale must be a float32 tensor");
+                    first_bytes(1, &scale, 4);
+                    zp = 0;
+                    if (in.size() > 2 && in_numel(2) >= 1) {
+                        if (in_dtype(2) == DType::Int8) {
+                            int8_t v;
+                            first_bytes(2, &v, 1);
+                            zp = v;
+                        } else if (in_dtype(2) == DType::UInt8) {
+                            uint8_t v;
+                            first_bytes(2, &v, 1);
+                            zp = v;
+                        }
+                    }
+                }
+                out.shape = x.shape;
+                const int64_t cnt = numel(x.shape);
+                if (q) {
+                    const bool u8 = n->get_attr<std::string>(lin ? "output_dtype" : "dtype", "int8") == "uint8";
+                    const pfr_dtype dt = u8 ? PFR_U8 : PFR_I8;
+                    pfr_check(pfr_quantize_linear_dev(ctx_, nullptr, 0, scale, zp, dt, nullptr));  // parameter checks
+                    if (x.dtype != DType::Float32)
+                        throw std::invalid_argument("quantize_tensor: input must be Float32, got " + dtype_name(x.dtype));
+                    out.dtype = u8 ? DType::UInt8 : DType::Int8;
+                    out.p = device_buffer(st.out, std::max<int64_t>(cnt, 1));
+                    pfr_check(pfr_quantize_linear_dev(ctx_, static_cast<const float*>(x.p), cnt, scale, zp, dt, out.p));
+                } else {
+                    const pfr_dtype dt =
+                        x.dtype == DType::Int8 ? PFR_I8 : (x.dtype == DType::UInt8 ? PFR_U8 : PFR_F32);
+                    out.dtype = DType::Float32;
+                    out.p = device_buffer(st.out, std::max<int64_t>(cnt, 1) * 4);
+                    pfr_check(pfr_dequantize_linear_dev(ctx_, x.p, dt, cnt, scale, zp, static_cast<float*>(out.p)));
+                }
                 break;
             }
             case PlanStep::LayerNorm: {

@@ -14,7 +14,8 @@
 //  * inputs and initializers are not deep-copied on every run;
 //  * from OptLevel::Basic up, a graph whose every node has a device kernel
 //    (pruned Gemm / MatMul / 2:4 QuantizedMatMul, DynamicQuantizeLinear,
-//    Relu, Softmax, Gelu, Add, LayerNormalization) runs as a
+//    Relu, Softmax, Gelu, Add, LayerNormalization, per-tensor Quantize /
+//    Dequantize / QuantizeLinear / DequantizeLinear) runs as a
 //    device-resident plan:
 //    graph inputs are copied to the GPU once per run, the remaining
 //    initializers once per graph, activations stay in device buffers
@@ -87,7 +88,7 @@ public:
 private:
     // One kernel launch of the device plan.
     struct PlanStep {
-        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm } op;
+        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm, Quant, Dequant } op;
         const Node* node;
         int act = 0;      // pfr_act of a following Relu/Gelu run in this step's epilogue
         std::string out;  // tensor the step writes (the activation's output when fused)

@@ -4,7 +4,8 @@
 // C ABI; shapes, attributes and error texts follow the reference kernels
 // (src/backends/cpu/ops/math.cpp:150-226 and :268-438, quantized_ops.cpp:
 // 77-167 and :251-278, activation.cpp:45-60, :157-237 and :239-259,
-// nn.cpp:419-478).
+// nn.cpp:419-478; per-tensor Quantize / Dequantize / QuantizeLinear /
+// DequantizeLinear, quantized_ops.cpp:35-70 and :284-347).
 #include <stdexcept>
 #include <string>
 
@@ -233,6 +234,72 @@ std::vector<Tensor> rocm_layernorm(const std::vector<const Tensor*>& in, const O
     return {std::move(out)};
 }
 
+// Per-tensor quantize and dequantize (quantized_ops.cpp:35-70, :284-347):
+// the parameters from attributes (Quantize, Dequantize) or from the first
+// element of the scale and zero-point inputs (QuantizeLinear,
+// DequantizeLinear; a zero point that is not int8 or uint8 counts as 0, as
+// there).  The scale input must be float32 here (the reference reads its
+// bytes as a float whatever its type).
+float scale_input(const Tensor& s, const char* op) {
+    if (s.dtype() != DType::Float32 || s.num_elements() < 1)
+        throw std::invalid_argument(std::string(op) + ": scale must be a float32 tensor");
+    return s.data_ptr<float>()[0];
+}
+
+int32_t zero_point_input(const std::vector<const Tensor*>& in) {
+    if (in.size() < 3 || in[2] == nullptr || in[2]->num_elements() < 1) return 0;
+    if (in[2]->dtype() == DType::Int8) return static_cast<const int8_t*>(in[2]->data())[0];
+    if (in[2]->dtype() == DType::UInt8) return static_cast<const uint8_t*>(in[2]->data())[0];
+    return 0;
+}
+
+Tensor quantize_call(const Tensor& x, float scale, int32_t zp, DType out) {
+    // QuantParams::per_tensor validates first, then quantize_tensor the input
+    pfr_check(pfr_quantize_linear(exec().ctx(), nullptr, 0, scale, zp, out == DType::UInt8 ? PFR_U8 : PFR_I8, nullptr));
+    if (x.dtype() != DType::Float32)
+        throw std::invalid_argument("quantize_tensor: input must be Float32, got " + dtype_name(x.dtype()));
+    Tensor y(x.shape(), out);
+    pfr_check(pfr_quantize_linear(exec().ctx(), x.data_ptr<float>(), x.num_elements(), scale, zp,
+                                  out == DType::UInt8 ? PFR_U8 : PFR_I8, y.data()));
+    return y;
+}
+
+Tensor dequantize_call(const Tensor& x, float scale, int32_t zp) {
+    const pfr_dtype dt = x.dtype() == DType::Int8 ? PFR_I8 : (x.dtype() == DType::UInt8 ? PFR_U8 : PFR_F32);
+    Tensor y(x.shape(), DType::Float32);
+    pfr_check(pfr_dequantize_linear(exec().ctx(), x.data(), dt, x.num_elements(), scale, zp, y.data_ptr<float>()));
+    return y;
+}
+
+DType quant_dtype_attr(const OpContext& ctx, const char* key) {
+    return ctx.node->get_attr<std::string>(key, "int8") == "uint8" ? DType::UInt8 : DType::Int8;
+}
+
+std::vector<Tensor> rocm_quantize(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 1, "Quantize");
+    const float scale = ctx.node->get_attr<float>("scale", 1.0f);
+    const int32_t zp = (int32_t)ctx.node->get_attr<int64_t>("zero_point", 0);
+    return {quantize_call(*in[0], scale, zp, quant_dtype_attr(ctx, "dtype"))};
+}
+
+std::vector<Tensor> rocm_dequantize(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 1, "Dequantize");
+    const float scale = ctx.node->get_attr<float>("scale", 1.0f);
+    const int32_t zp = (int32_t)ctx.node->get_attr<int64_t>("zero_point", 0);
+    return {dequantize_call(*in[0], scale, zp)};
+}
+
+std::vector<Tensor> rocm_quantize_linear(const std::vector<const Tensor*>& in, const OpContext& ctx) {
+    need_inputs(in, 2, "QuantizeLinear");
+    return {quantize_call(*in[0], scale_input(*in[1], "QuantizeLinear"), zero_point_input(in),
+                          quant_dtype_attr(ctx, "output_dtype"))};
+}
+
+std::vector<Tensor> rocm_dequantize_linear(const std::vector<const Tensor*>& in, const OpContext&) {
+    need_inputs(in, 2, "DequantizeLinear");
+    return {dequantize_call(*in[0], scale_input(*in[1], "DequantizeLinear"), zero_point_input(in))};
+}
+
 struct RocmOpsRegistrar {
     RocmOpsRegistrar() {
         auto& r = OperatorRegistry::instance();
@@ -245,6 +312,10 @@ struct RocmOpsRegistrar {
         r.register_op("rocm::Gelu", rocm_gelu);
         r.register_op("rocm::Add", rocm_add);
         r.register_op("rocm::LayerNormalization", rocm_layernorm);
+        r.register_op("rocm::Quantize", rocm_quantize);
+        r.register_op("rocm::Dequantize", rocm_dequantize);
+        r.register_op("rocm::QuantizeLinear", rocm_quantize_linear);
+        r.register_op("rocm::DequantizeLinear", rocm_dequantize_linear);
     }
 };
 RocmOpsRegistrar registrar;

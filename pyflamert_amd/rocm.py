@@ -164,6 +164,24 @@ class Context:
     def layernorm_dev(self, x_ptr, outer, norm, scale_ptr, bias_ptr, epsilon, y_ptr):
         check(self._lib.pfr_layernorm_dev(self.handle, x_ptr, outer, norm, scale_ptr, bias_ptr, float(epsilon), y_ptr))
 
+    # -- per-tensor quantize / dequantize ----------------------------------
+    def quantize_linear(self, x, scale, zero_point=0, out="i8"):
+        """quantize_tensor with per-tensor parameters: int8 (out="i8") or
+        uint8 (out="u8") of x's shape."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(x.shape, np.uint8 if out == "u8" else np.int8)
+        check(self._lib.pfr_quantize_linear(self.handle, _ptr(x), x.size, float(scale), int(zero_point),
+                                            _lib.PFR_U8 if out == "u8" else _lib.PFR_I8, _ptr(y)))
+        return y
+
+    def dequantize_linear(self, q, scale, zero_point=0):
+        q = np.ascontiguousarray(q)
+        dt = {np.dtype(np.int8): _lib.PFR_I8, np.dtype(np.uint8): _lib.PFR_U8}.get(q.dtype, _lib.PFR_F32)
+        y = np.empty(q.shape, np.float32)
+        check(self._lib.pfr_dequantize_linear(self.handle, _ptr(q), dt, q.size, float(scale), int(zero_point),
+                                              _ptr(y)))
+        return y
+
     # -- dynamic activation quantization ----------------------------------
     def dynamic_quantize_linear(self, x):
         """DynamicQuantizeLinear: (uint8 y of x's shape, float32 scale,

@@ -214,3 +214,81 @@ def test_two_input_quantized_matmul_zero_point(tmp_path):
                         got = O.ref_op_f32("QuantizedMatMul", [q, b], fattrs={"a_scale": float(s[0]), "b_scale": 0.04},
                                            iattrs={"b_zero_point": -9})
                         assert np.array_equal(bits(y), bits(got)), lvl
+
+
+def test_quantize_dequantize_per_tensor(ctx, golden):
+    """Per-tensor quantize_tensor / dequantize_tensor on the GPU: bit-exact
+    against the golden vectors written by the compiled reference (edge
+    values: +-0, halves, overflow, +-inf, NaN) and the oracle on large
+    random inputs; the reference's parameter checks and texts."""
+    g = golden("quant.npz")
+    xs = g["x"]
+    say("QuantizeLinear golden vectors")
+    for dt, zp in ((O.I8, 0), (O.I8, -3), (O.U8, 128), (O.U8, 7)):
+        q = ctx.quantize_linear(xs, 0.05, zp, "u8" if dt == O.U8 else "i8")
+        assert np.array_equal(q, g[f"q_{dt}_{zp}"]), (dt, zp)
+    say("DequantizeLinear golden vectors")
+    assert np.array_equal(bits(ctx.dequantize_linear(np.arange(-128, 128, dtype=np.int8), 0.05, 3)),
+                          bits(g["dq_i8"]))
+    assert np.array_equal(bits(ctx.dequantize_linear(np.arange(0, 256, dtype=np.uint8), 0.1, 128)),
+                          bits(g["dq_u8"]))
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal(1 << 20) * 9).astype(np.float32)
+    x[::1009] = np.nan
+    x[::1013] = np.inf
+    for dt, zp, sc in ((O.I8, 0, 0.07), (O.I8, 100, 3e-3), (O.U8, 128, 0.11), (O.U8, 255, 1e-30), (O.I8, -7, 7e30)):
+        say(f"quantize 1M values dtype={dt} zp={zp} scale={sc}")
+        q = ctx.quantize_linear(x, sc, zp, "u8" if dt == O.U8 else "i8")
+        assert np.array_equal(q, O.orc_quantize(x, [sc], [zp], dt)), (dt, zp, sc)
+        q8 = rng.integers(0 if dt == O.U8 else -128, 256 if dt == O.U8 else 128, 100000).astype(
+            np.uint8 if dt == O.U8 else np.int8)
+        assert np.array_equal(bits(ctx.dequantize_linear(q8, sc, zp)), bits(O.orc_dequantize(q8, [sc], [zp], dt)))
+    for bad in (0.0, -1.0, np.inf, np.nan):
+        with pytest.raises(_lib.InvalidArgument, match="scale must be positive and finite"):
+            ctx.quantize_linear(x[:10], bad)
+        with pytest.raises(_lib.InvalidArgument, match="scale must be positive and finite"):
+            ctx.dequantize_linear(np.zeros(4, np.int8), bad)
+    with pytest.raises(_lib.InvalidArgument, match="dtype must be Int8 or UInt8"):
+        ctx.dequantize_linear(np.zeros(4, np.float32), 0.5)
+    assert ctx.quantize_linear(np.zeros(0, np.float32), 0.5).size == 0
+
+
+def test_quantize_ops_in_sessions(tmp_path):
+    """Quantize / Dequantize (attributes) and QuantizeLinear /
+    DequantizeLinear (scale and zero-point inputs, constant or produced by a
+    DynamicQuantizeLinear) in device-resident plans and node by node: the
+    oracle's per-tensor results bit for bit."""
+    from pyflamert_amd import pfm, session
+
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((64, 300)) * 4).astype(np.float32)
+    sc = np.array([0.03], np.float32)
+    zp = np.array([5], np.int8)
+    m = {"name": "qdq", "inputs": [("x", 0, [64, 300])],
+         "outputs": [("a", 7, [64, 300]), ("b", 0, [64, 300]), ("c", 8, [64, 300]), ("d", 0, [64, 300]),
+                     ("e", 0, [64, 300])],
+         "initializers": {"s": sc, "z": zp},
+         "nodes": [("q1", "QuantizeLinear", ["x", "s", "z"], ["a"], {}),
+                   ("d1", "DequantizeLinear", ["a", "s", "z"], ["b"], {}),
+                   ("q2", "Quantize", ["x"], ["c"], {"scale": 0.07, "zero_point": 128, "dtype": "uint8"}),
+                   ("d2", "Dequantize", ["c"], ["d"], {"scale": 0.07, "zero_point": 128}),
+                   ("dq", "DynamicQuantizeLinear", ["x"], ["y", "ys", "yz"], {}),
+                   ("d3", "DequantizeLinear", ["y", "ys", "yz"], ["e"], {})]}
+    p = str(tmp_path / "qdq.pfm")
+    pfm.save(m, p)
+    a_ref = O.orc_quantize(x, sc, [5], O.I8)
+    b_ref = O.orc_dequantize(a_ref, sc, [5], O.I8)
+    c_ref = O.orc_quantize(x, [0.07], [128], O.U8)
+    d_ref = O.orc_dequantize(c_ref, [0.07], [128], O.U8)
+    ys, yz = O.orc_dynamic_params(x.ravel(), O.U8, symmetric=False)
+    e_ref = O.orc_dequantize(O.orc_quantize(x, [ys], [yz], O.U8), [ys], [yz], O.U8)
+    for lvl in (2, 0):
+        say(f"quantize ops session, optimization level {lvl}")
+        s = session.InferenceSession(p, session.SessionOptions(optimization_level=lvl))
+        a, b, c, d, e = s.run(None, {"x": x})
+        assert s.device_plan()[0] == (lvl > 0)
+        assert a.dtype == np.int8 and np.array_equal(a, a_ref)
+        assert np.array_equal(bits(b), bits(b_ref))
+        assert c.dtype == np.uint8 and np.array_equal(c, c_ref)
+        assert np.array_equal(bits(d), bits(d_ref))
+        assert np.array_equal(bits(e), bits(e_ref))
