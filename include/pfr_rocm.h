@@ -226,6 +226,21 @@ int pfr_sp24_gemm_q_dev(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtyp
                         int out_kind, float out_scale, int32_t out_zp, void* Y,
                         int64_t ldy);
 
+/* The x . W form (the layout a Linear layer exports): Y[T, M] (float) =
+ * X[T, K] . W^T with the packed 2:4 weight W[M, K] as the second operand of
+ * QuantizedMatMul (quantization::quantized_matmul, quant_ops.cpp:387-506,
+ * with the operands' roles swapped: per output column m the product is
+ * (float) sum_k (x[t, k] - x_zero_point) * w[m, k] * (x_scale * w_scale[m])),
+ * bit-exact.  X is row-major int8 or uint8 (ldx >= K), Y row-major (ldy >=
+ * M); scale and zero point from host values or device scalars, as in
+ * pfr_sp24_gemm_q_dev.  Host pointers: pfr_sp24_gemm_qt. */
+int pfr_sp24_gemm_qt(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype,
+                     int64_t T, float x_scale, int32_t x_zero_point, float* Y);
+int pfr_sp24_gemm_qt_dev(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype,
+                         int64_t T, int64_t ldx, float x_scale, int32_t x_zero_point,
+                         const float* x_scale_dev, const uint8_t* x_zero_point_dev,
+                         float* Y, int64_t ldy);
+
 /* Y[M, N] (float) = W[M, K] . X[K, N] with bf16 operands and fp32
  * accumulation: cpu_gemm on bf16-rounded operands
  * (half_types.cpp:132-174 then math.cpp:377-438), within the bf16

@@ -80,6 +80,8 @@ SIGNATURES = {
     "pfr_gelu_dev": (_INT, [_P, _P, _I64, _P]),
     "pfr_add": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
     "pfr_add_dev": (_INT, [_P, _P, _P, _INT, _P, _P, _INT, _P]),
+    "pfr_sp24_gemm_qt": (_INT, [_P, _P, _P, _INT, _I64, _F, _I32, _P]),
+    "pfr_sp24_gemm_qt_dev": (_INT, [_P, _P, _P, _INT, _I64, _I64, _F, _I32, _P, _P, _P, _I64]),
     "pfr_quantize_linear": (_INT, [_P, _P, _I64, _F, _I32, _INT, _P]),
     "pfr_quantize_linear_dev": (_INT, [_P, _P, _I64, _F, _I32, _INT, _P]),
     "pfr_dequantize_linear": (_INT, [_P, _P, _INT, _I64, _F, _I32, _P]),

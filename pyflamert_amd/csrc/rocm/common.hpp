@@ -97,7 +97,8 @@ struct pfr_ctx {
     // scratch[0..1]: staged inputs, scratch[2]: staged output, scratch[3]:
     // transposed activations of the Gemm form, scratch[4]: the magnitude
     // mask's selection state (histogram, counters, per-block tie counts).
-    pfr::DevBuf scratch[5];
+    // scratch[5]: the product before its transpose in the 2:4 x . W form.
+    pfr::DevBuf scratch[6];
 };
 
 struct pfr_csr {

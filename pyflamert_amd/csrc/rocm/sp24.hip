@@ -691,6 +691,69 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     PFR_HIP(hipGetLastError());
 }
 
+// The activation of the x . W form, act[T, K] row-major, as the kernel's
+// K-contiguous B operand XT (Np x Kp): XT[n][k] = act[n][k] (with the sign
+// bit flipped for uint8: the signed MFMA takes x - 128), zero outside T x K.
+template <bool FLIP>
+__global__ __launch_bounds__(256) void k_pad_act(const uint8_t* __restrict__ X, int64_t T, int64_t K, int64_t ldx,
+                                                 uint8_t* __restrict__ xt, int64_t Kp, int64_t Np) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= Np * Kp) return;
+    const int64_t n = i / Kp, k = i % Kp;
+    uint8_t v = 0;
+    if (n < T && k < K) v = FLIP ? (uint8_t)(X[n * ldx + k] ^ 0x80u) : X[n * ldx + k];
+    xt[i] = v;
+}
+
+// Y[t, m] = Yp[m, t] for m < M, t < T (the x . W product's transpose).
+__global__ __launch_bounds__(256) void k_transpose_out(const float* __restrict__ Yp, int64_t M, int64_t T,
+                                                       int64_t ldyp, float* __restrict__ Y, int64_t ldy) {
+    __shared__ float tile[64][65];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int64_t t0 = (int64_t)blockIdx.x * 64, m0 = (int64_t)blockIdx.y * 64;
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t m = m0 + i, t = t0 + tx;
+        if (m < M && t < T) tile[i][tx] = Yp[m * ldyp + t];
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t t = t0 + i, m = m0 + tx;
+        if (m < M && t < T) Y[t * ldy + m] = tile[tx][i];
+    }
+}
+
+// Y[T, M] (float) = act[T, K] . W^T with the 2:4 weight W[M, K] as the
+// second operand (the x . W form of a Linear layer), act int8 or uint8 with
+// a zero point: the W . X product on XT = act, then its transpose.
+void gemm_qt_dev(pfr_ctx* ctx, const pfr_sp24* W, const uint8_t* X, bool x_u8, int64_t T, int64_t ldx,
+                 float x_scale, int32_t x_zp, const float* xs_dev, const uint8_t* zp_dev, float* Y, int64_t ldy) {
+    check_i8(W);
+    pfr::require(W->K < (1 << 17), "K must be below 2^17 for exact int32 accumulation");
+    pfr::require(x_u8 ? (x_zp >= 0 && x_zp <= 255) : (x_zp >= -128 && x_zp <= 127),
+                 "activation zero point outside the activation type's range");
+    pfr::require(T >= 0 && T < INT32_MAX, "bad row count");
+    pfr::require(ldx >= W->K && ldy >= W->M, "leading dimension smaller than the row");
+    if (W->M == 0 || T == 0) return;
+    pfr::require(X != nullptr && Y != nullptr, "null X/Y");
+    if (!xs_dev) pfr::require(x_scale > 0.0f && std::isfinite(x_scale), "x_scale must be positive and finite");
+    const int64_t Kp = W->Kp, Np = round_up(T, kI8TileN), ldyp = round_up(T, 16);
+    uint8_t* xt = static_cast<uint8_t*>(ctx->scratch[3].ensure((size_t)(Np * Kp)));
+    float* yp = static_cast<float*>(ctx->scratch[5].ensure((size_t)(W->M * ldyp) * 4));
+    const unsigned pb = (unsigned)((Np * Kp + 255) / 256);
+    if (x_u8) hipLaunchKernelGGL(k_pad_act<true>, dim3(pb), dim3(256), 0, ctx->stream, X, T, W->K, ldx, xt, Kp, Np);
+    else hipLaunchKernelGGL(k_pad_act<false>, dim3(pb), dim3(256), 0, ctx->stream, X, T, W->K, ldx, xt, Kp, Np);
+    PFR_HIP(hipGetLastError());
+    const int ntn = (int)(Np / kI8TileN);
+    hipLaunchKernelGGL((k_sp24_i8<PFR_SP24_OUT_F32, false>), dim3((unsigned)(W->Mp / kI8TileM * ntn)),
+                       dim3(kI8Threads), 0, ctx->stream, (int)(Kp / 128), static_cast<const v4i*>(W->a), W->idx,
+                       reinterpret_cast<const int8_t*>(xt), Kp, (int)W->M, (int)T, W->w_scale, x_scale, 1.0f, 0,
+                       static_cast<void*>(yp), ldyp, 1, ntn, x_zp, x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum);
+    PFR_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_transpose_out, dim3((unsigned)((T + 63) / 64), (unsigned)((W->M + 63) / 64)), dim3(256), 0,
+                       ctx->stream, yp, W->M, T, ldyp, Y, ldy);
+    PFR_HIP(hipGetLastError());
+}
+
 void gemm_bf16_dev(pfr_ctx* ctx, const pfr_sp24* W, const uint16_t* X, int64_t N, int64_t ldx, float* Y,
                    int64_t ldy) {
     pfr::require(W != nullptr, "null 2:4 weight handle");
@@ -817,6 +880,37 @@ int pfr_sp24_gemm_q(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_
         void* dY = ctx->scratch[2].ensure(yb);
         if (xb) PFR_HIP(hipMemcpyAsync(dX, X, xb, hipMemcpyHostToDevice, s));
         gemm_i8_dev(ctx, W, dX, N, N, x_scale, out_kind, out_scale, out_zp, dY, N, x_dtype == PFR_U8, x_zero_point);
+        PFR_HIP(hipMemcpyAsync(Y, dY, yb, hipMemcpyDeviceToHost, s));
+        PFR_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int pfr_sp24_gemm_qt_dev(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype, int64_t T,
+                         int64_t ldx, float x_scale, int32_t x_zero_point, const float* x_scale_dev,
+                         const uint8_t* x_zero_point_dev, float* Y, int64_t ldy) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(x_dtype == PFR_I8 || x_dtype == PFR_U8, "activation must be int8 or uint8");
+        gemm_qt_dev(ctx, W, static_cast<const uint8_t*>(X), x_dtype == PFR_U8, T, ldx, x_scale, x_zero_point,
+                    x_scale_dev, x_zero_point_dev, Y, ldy);
+    });
+}
+
+int pfr_sp24_gemm_qt(pfr_ctx* ctx, const pfr_sp24* W, const void* X, pfr_dtype x_dtype, int64_t T, float x_scale,
+                     int32_t x_zero_point, float* Y) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        check_i8(W);
+        pfr::require(x_dtype == PFR_I8 || x_dtype == PFR_U8, "activation must be int8 or uint8");
+        pfr::require(T >= 0, "bad row count");
+        const size_t xb = (size_t)(W->K * T), yb = 4 * (size_t)(W->M * T);
+        if (yb == 0) return;
+        pfr::require(Y != nullptr && (X != nullptr || xb == 0), "null X/Y");
+        hipStream_t s = ctx->stream;
+        uint8_t* dX = static_cast<uint8_t*>(ctx->scratch[0].ensure(xb ? xb : 4));
+        float* dY = static_cast<float*>(ctx->scratch[2].ensure(yb));
+        if (xb) PFR_HIP(hipMemcpyAsync(dX, X, xb, hipMemcpyHostToDevice, s));
+        gemm_qt_dev(ctx, W, dX, x_dtype == PFR_U8, T, W->K, x_scale, x_zero_point, nullptr, nullptr, dY, W->M);
         PFR_HIP(hipMemcpyAsync(Y, dY, yb, hipMemcpyDeviceToHost, s));
         PFR_HIP(hipStreamSynchronize(s));
     });

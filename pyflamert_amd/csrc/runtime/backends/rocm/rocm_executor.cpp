@@ -157,7 +157,7 @@ const Tensor& RocmExecutor::initializer_value(const Graph& graph, const std::str
 void RocmExecutor::prepare_sparse_views(const Graph& graph) {
     for (const auto& kv : weights_) {
         const Node* n = kv.first;
-        const int slot = kv.second.kind == DeviceWeight::CsrB ? 1 : 0;
+        const int slot = kv.second.kind == DeviceWeight::CsrB || kv.second.kind == DeviceWeight::Sp24B ? 1 : 0;
         const std::string& nm = n->inputs()[(size_t)slot];
         const SparseInitializer* s = graph.get_sparse_initializer(nm);
         if (s && !sparse_views_.count(nm))
@@ -237,6 +237,10 @@ std::vector<std::string> RocmExecutor::get_supported_ops() const {
 //  QuantizedMatMul(W, B)    W int8 2-D 2:4 along K, a_zero_point 0
 //                           -> 2:4 compressed, per-tensor scale a_scale or
 //                              per-channel a_scales
+//  QuantizedMatMul(A, W)    A an activation, W int8 2-D (K x N, or N x K
+//                           with transB = 1) 2:4 along K, b_zero_point 0
+//                           -> 2:4 compressed W^T, per-tensor b_scale or
+//                              per-output-column b_scales
 namespace {
 // The weight scales of a QuantizedMatMul: a_scales (one per row) when set,
 // else the per-tensor a_scale.
@@ -249,6 +253,17 @@ std::vector<float> weight_scales(const Node& n, int64_t rows) {
         return *v;
     }
     return {n.get_attr<float>("a_scale", 1.0f)};
+}
+
+std::vector<float> weight_scales_b(const Node& n, int64_t cols) {
+    auto v = n.get_attr<std::vector<float>>("b_scales");
+    if (v) {
+        if ((int64_t)v->size() != cols)
+            throw std::invalid_argument("QuantizedMatMul: b_scales has " + std::to_string(v->size()) +
+                                        " entries for " + std::to_string(cols) + " columns");
+        return *v;
+    }
+    return {n.get_attr<float>("b_scale", 1.0f)};
 }
 }  // namespace
 
@@ -301,6 +316,22 @@ void RocmExecutor::prepare(const Graph& graph) {
                 const Tensor& A = *init(0);
                 pfr_check(pfr_csr_from_dense(ctx_, A.data_ptr<float>(), A.shape()[0], A.shape()[1], 0, 0.0f, &w.csr));
                 w.kind = DeviceWeight::CsrA;
+            } else if (n->op_type() == "QuantizedMatMul" && !init(0) && !sparse(0) &&
+                       ((sparse(1) && sparse(1)->format == SparseInitializer::Nm24) ||
+                        (init(1) && init(1)->ndim() == 2 &&
+                         (init(1)->dtype() == DType::Int8 || init(1)->dtype() == DType::UInt8))) &&
+                       n->get_attr<int64_t>("b_zero_point", 0) == 0) {
+                // the weight as the second operand: pack W^T (N x K), 2:4 along K
+                const Tensor B = sparse(1) ? sparse(1)->to_dense() : init(1)->clone();
+                const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
+                const int64_t Nn = tb ? B.shape()[0] : B.shape()[1], Kk = tb ? B.shape()[1] : B.shape()[0];
+                std::vector<int8_t> wt((size_t)(Nn * Kk));
+                const int8_t* src = static_cast<const int8_t*>(B.data());
+                for (int64_t r = 0; r < Nn; ++r)
+                    for (int64_t c = 0; c < Kk; ++c) wt[(size_t)(r * Kk + c)] = tb ? src[r * Kk + c] : src[c * Nn + r];
+                const std::vector<float> sc = weight_scales_b(*n, Nn);
+                const int st = pfr_sp24_pack(ctx_, Nn, Kk, wt.data(), PFR_I8, sc.data(), (int64_t)sc.size(), &w.sp24);
+                if (st == PFR_OK) w.kind = DeviceWeight::Sp24B;
             } else if (n->op_type() == "QuantizedMatMul" && init(0) && init(0)->ndim() == 2 &&
                        (init(0)->dtype() == DType::Int8 || init(0)->dtype() == DType::UInt8) &&
                        n->get_attr<int64_t>("a_zero_point", 0) == 0) {
@@ -357,6 +388,8 @@ void RocmExecutor::build_plan(const Graph& graph) {
             st.op = PlanStep::MatMulA;
         else if (op == "QuantizedMatMul" && w && w->kind == DeviceWeight::Sp24A)
             st.op = PlanStep::QMatMul;
+        else if (op == "QuantizedMatMul" && w && w->kind == DeviceWeight::Sp24B)
+            st.op = PlanStep::QMatMulT;
         else if (op == "Relu" && n->inputs().size() == 1)
             st.op = PlanStep::Relu;
         else if (op == "Softmax" && n->inputs().size() == 1)
@@ -404,7 +437,8 @@ void RocmExecutor::build_plan(const Graph& graph) {
         if (dropped[i]) continue;
         const PlanStep& st = steps[i];
         const auto& in = st.node->inputs();
-        const int weight_slot = (st.op == PlanStep::Gemm || st.op == PlanStep::MatMulB)   ? 1
+        const int weight_slot = (st.op == PlanStep::Gemm || st.op == PlanStep::MatMulB || st.op == PlanStep::QMatMulT)
+                                    ? 1
                                 : (st.op == PlanStep::MatMulA || st.op == PlanStep::QMatMul) ? 0
                                                                                              : -1;
         for (size_t k = 0; k < in.size(); ++k) {
@@ -580,6 +614,52 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 out.p = device_buffer(st.out, M * N * 4);
                 pfr_check(pfr_sp24_gemm_q_dev(ctx_, weight(n)->sp24, b.p, bdt, N, N, b_scale, b_zp, s_dev, z_dev,
                                               PFR_SP24_OUT_F32, 1.0f, 0, out.p, N));
+                break;
+            }
+            case PlanStep::QMatMulT: {
+                // the x . W form: A the activation, B the 2:4 weight (our
+                // extension of quantized_ops.cpp:77-167 to a weight in the B
+                // position, transB and per-column b_scales)
+                need_inputs(2, "QuantizedMatMul");
+                const DevTensor& a = act_in(0);
+                if (a.dtype != DType::Int8 && a.dtype != DType::UInt8)
+                    throw std::invalid_argument("QuantizedMatMul: input A must be Int8 or UInt8");
+                const Tensor& b = init_in(1);
+                const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
+                const int64_t Kb = tb ? b.shape()[1] : b.shape()[0], N = tb ? b.shape()[0] : b.shape()[1];
+                if (a.shape.size() != 2)
+                    throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D activation A with a 2:4 "
+                                             "weight B");
+                if (a.shape[1] != Kb)
+                    throw std::invalid_argument("QuantizedMatMul: inner dimensions must match (got " +
+                                                std::to_string(a.shape[1]) + " and " + std::to_string(Kb) + ")");
+                float a_scale = n->get_attr<float>("a_scale", 1.0f);
+                int32_t a_zp = (int32_t)n->get_attr<int64_t>("a_zero_point", 0);
+                const float* s_dev = nullptr;
+                const uint8_t* z_dev = nullptr;
+                pfr_dtype adt = PFR_I8;
+                if (in.size() >= 4) {
+                    const DevTensor& s = act_in(2);
+                    const DevTensor& z = act_in(3);
+                    if (s.dtype != DType::Float32 || numel(s.shape) != 1)
+                        throw std::invalid_argument("QuantizedMatMul: a_scale input must be one float32");
+                    if ((z.dtype != DType::UInt8 && z.dtype != DType::Int8) || numel(z.shape) != 1)
+                        throw std::invalid_argument("QuantizedMatMul: a_zero_point input must be one int8 or uint8");
+                    s_dev = static_cast<const float*>(s.p);
+                    if (z.dtype == DType::UInt8) {
+                        z_dev = static_cast<const uint8_t*>(z.p);
+                    } else {
+                        int8_t zv = 0;
+                        pfr_check(pfr_copy_to_host(ctx_, &zv, z.p, 1));
+                        a_zp = zv;
+                    }
+                    adt = a.dtype == DType::UInt8 ? PFR_U8 : PFR_I8;
+                }
+                const int64_t T = a.shape[0];
+                out.shape = {T, N};
+                out.p = device_buffer(st.out, std::max<int64_t>(T * N, 1) * 4);
+                pfr_check(pfr_sp24_gemm_qt_dev(ctx_, weight(n)->sp24, a.p, adt, T, Kb, a_scale, a_zp, s_dev, z_dev,
+                                               static_cast<float*>(out.p), N));
                 break;
             }
             case PlanStep::DynQuant: {
@@ -803,7 +883,7 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
         std::vector<const Tensor*> ins;
         ins.reserve(node->inputs().size());
         const DeviceWeight* w = weight(node.get());
-        const int wslot = !w ? -1 : (w->kind == DeviceWeight::CsrB ? 1 : 0);
+        const int wslot = !w ? -1 : (w->kind == DeviceWeight::CsrB || w->kind == DeviceWeight::Sp24B ? 1 : 0);
         for (size_t i = 0; i < node->inputs().size(); ++i) {
             const std::string& nm = node->inputs()[i];
             auto it = view.find(nm);

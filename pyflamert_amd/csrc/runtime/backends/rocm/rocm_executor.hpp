@@ -58,9 +58,9 @@ LayerNormExtent layernorm_extent(const std::vector<int64_t>& x_shape, int64_t sc
 class RocmExecutor : public Backend {
 public:
     struct DeviceWeight {
-        enum Kind { None, CsrB, CsrA, Sp24A } kind = None;
+        enum Kind { None, CsrB, CsrA, Sp24A, Sp24B } kind = None;
         pfr_csr* csr = nullptr;    // CsrB: CSR of op(B)^T; CsrA: CSR of A
-        pfr_sp24* sp24 = nullptr;  // Sp24A: 2:4-compressed int8 A
+        pfr_sp24* sp24 = nullptr;  // Sp24A: 2:4-compressed int8 A; Sp24B: B^T (N x K), 2:4 along K
     };
 
     // opt: None runs node by node through the OpFuncs; Basic adds the
@@ -88,7 +88,7 @@ public:
 private:
     // One kernel launch of the device plan.
     struct PlanStep {
-        enum Op { Gemm, MatMulB, MatMulA, QMatMul, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm, Quant, Dequant } op;
+        enum Op { Gemm, MatMulB, MatMulA, QMatMul, QMatMulT, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm, Quant, Dequant } op;
         const Node* node;
         int act = 0;      // pfr_act of a following Relu/Gelu run in this step's epilogue
         std::string out;  // tensor the step writes (the activation's output when fused)

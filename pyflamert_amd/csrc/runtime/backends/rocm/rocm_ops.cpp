@@ -126,6 +126,36 @@ std::vector<Tensor> rocm_qmatmul(const std::vector<const Tensor*>& in, const OpC
         throw std::invalid_argument("QuantizedMatMul: input B must be Int8 or UInt8");
     if (a.ndim() < 2 || b.ndim() < 2)
         throw std::invalid_argument("QuantizedMatMul: inputs must have at least 2 dimensions");
+    if (w && w->kind == RocmExecutor::DeviceWeight::Sp24B) {
+        // the x . W form: the activation is A, the 2:4 weight B (K x N, or
+        // N x K with transB = 1), per-column b_scales
+        const bool tb = ctx.node->get_attr<int64_t>("transB", 0) != 0;
+        const int64_t Kb = tb ? b.shape()[1] : b.shape()[0], N = tb ? b.shape()[0] : b.shape()[1];
+        if (a.ndim() != 2)
+            throw std::runtime_error("QuantizedMatMul: the rocm backend needs a 2-D activation A with a 2:4 weight B");
+        if (a.shape()[1] != Kb)
+            throw std::invalid_argument("QuantizedMatMul: inner dimensions must match (got " +
+                                        std::to_string(a.shape()[1]) + " and " + std::to_string(Kb) + ")");
+        float a_scale = ctx.node->get_attr<float>("a_scale", 1.0f);
+        int64_t a_zp = ctx.node->get_attr<int64_t>("a_zero_point", 0);
+        pfr_dtype adt = PFR_I8;
+        if (in.size() >= 4) {
+            const Tensor& s = *in[2];
+            const Tensor& z = *in[3];
+            if (s.dtype() != DType::Float32 || s.num_elements() != 1)
+                throw std::invalid_argument("QuantizedMatMul: a_scale input must be one float32");
+            if ((z.dtype() != DType::UInt8 && z.dtype() != DType::Int8) || z.num_elements() != 1)
+                throw std::invalid_argument("QuantizedMatMul: a_zero_point input must be one int8 or uint8");
+            a_scale = s.data_ptr<float>()[0];
+            a_zp = z.dtype() == DType::UInt8 ? (int64_t) static_cast<const uint8_t*>(z.data())[0]
+                                             : (int64_t) static_cast<const int8_t*>(z.data())[0];
+            adt = a.dtype() == DType::UInt8 ? PFR_U8 : PFR_I8;
+        }
+        const int64_t T = a.shape()[0];
+        Tensor out({T, N}, DType::Float32);
+        pfr_check(pfr_sp24_gemm_qt(ex.ctx(), w->sp24, a.data(), adt, T, a_scale, (int32_t)a_zp, out.data_ptr<float>()));
+        return {std::move(out)};
+    }
     const int64_t K = a.shape().back(), Kb = b.shape()[b.ndim() - 2];
     if (K != Kb)
         throw std::invalid_argument("QuantizedMatMul: inner dimensions must match (got " + std::to_string(K) +

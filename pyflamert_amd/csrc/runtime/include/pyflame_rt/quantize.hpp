@@ -26,7 +26,17 @@ struct QuantizeStats {
 // (compute_dynamic_params_per_channel, quant_ops.cpp:321-381, with
 // QuantParams::compute_per_channel, quant_params.cpp:57-106, then
 // quantize_tensor's per-channel branch, quant_ops.cpp:56-124), stored as a
-// 2:4 record when its width is a multiple of 4.  Other nodes are copied.
+// 2:4 record when its width is a multiple of 4.
+//
+// The x . W form -- MatMul(X, W) with W K x N, and Gemm(X, W[, b]) with
+// transA 0, alpha 1, beta 1 and a bias of N floats (W N x K when transB) --
+// whose W is 2:4 along K becomes
+//   DynamicQuantizeLinear(X) -> (X_q, X_scale, X_zero_point)
+//   QuantizedMatMul(X_q, W_q^T, X_scale, X_zero_point)  transB = 1,
+//                                           b_scales = per-output-column
+//   Add(product, b)                         (Gemm with a bias)
+// with W_q^T (N x K) the per-column quantization of W.  Other nodes are
+// copied.
 std::unique_ptr<Graph> quantize_dynamic_int8(const Graph& g, QuantizeStats* stats = nullptr);
 
 }  // namespace pyflame_rt

@@ -1,5 +1,5 @@
-// The dynamic int8 rewrite of 2:4-pruned MatMul(W, X) nodes (declared in
-// quantize.hpp).
+// The dynamic int8 rewrite of 2:4-pruned MatMul(W, X), MatMul(X, W) and
+// Gemm(X, W[, b]) nodes (declared in quantize.hpp).
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -82,6 +82,21 @@ SparseInitializer nm24_record(const std::vector<int8_t>& q, int64_t rows, int64_
     return s;
 }
 
+// A float weight initializer (dense, or a CSR record expanded) as a 2-D
+// float32 tensor, or null.
+const Tensor* float_weight(const Graph& g, const std::string& name, Tensor& keep) {
+    if (auto t = g.get_initializer(name)) {
+        const Tensor* w = &t->get();
+        return w->dtype() == DType::Float32 && w->ndim() == 2 && w->shape()[0] > 0 && w->shape()[1] > 0 ? w : nullptr;
+    }
+    if (const SparseInitializer* s = g.get_sparse_initializer(name))
+        if (s->format == SparseInitializer::Csr) {
+            keep = s->to_dense();
+            return keep.dtype() == DType::Float32 && keep.shape()[0] > 0 && keep.shape()[1] > 0 ? &keep : nullptr;
+        }
+    return nullptr;
+}
+
 std::string fresh(const Graph& g, const std::unordered_map<std::string, int>& taken, const std::string& base) {
     std::string n = base;
     for (int i = 1; taken.count(n) || g.has_initializer(n); ++i) n = base + "_" + std::to_string(i);
@@ -161,6 +176,89 @@ std::unique_ptr<Graph> quantize_dynamic_int8(const Graph& g, QuantizeStats* stat
                 ++consumed[wn];
                 ++st.rewritten;
                 done = true;
+            }
+        }
+        // The x . W form: MatMul(X, W) with W K x N, or Gemm(X, W[, b]) with
+        // transA 0, alpha 1, beta 1 and a bias of N floats; W 2:4 along K.
+        // The weight goes in as W^T (N x K, transB = 1) with per-output-column
+        // scales; a Gemm bias becomes an Add (Gemm's bias modulo is numpy
+        // broadcasting for a bias of N elements).
+        const bool mm = n.op_type() == "MatMul" && n.inputs().size() == 2;
+        const bool gm = n.op_type() == "Gemm" && (n.inputs().size() == 2 || n.inputs().size() == 3) &&
+                        n.get_attr<int64_t>("transA", 0) == 0 && n.get_attr<float>("alpha", 1.0f) == 1.0f &&
+                        (n.inputs().size() == 2 || n.get_attr<float>("beta", 1.0f) == 1.0f);
+        if (!done && (mm || gm) && n.outputs().size() == 1 && !g.has_initializer(n.inputs()[0]) &&
+            !g.get_sparse_initializer(n.inputs()[0])) {
+            const std::string& wn = n.inputs()[1];
+            Tensor keep;
+            const Tensor* w = float_weight(g, wn, keep);
+            const bool tb = gm && n.get_attr<int64_t>("transB", 0) != 0;
+            const Tensor* bias = nullptr;
+            if (w && gm && n.inputs().size() == 3) {
+                auto c = g.get_initializer(n.inputs()[2]);
+                const int64_t N = tb ? w->shape()[0] : w->shape()[1];
+                if (c && c->get().dtype() == DType::Float32 && c->get().num_elements() == N &&
+                    (c->get().ndim() == 1 || (c->get().ndim() == 2 && c->get().shape()[0] == 1)))
+                    bias = &c->get();
+                else
+                    w = nullptr;  // another bias shape: left as it is
+            }
+            if (w) {
+                const int64_t N = tb ? w->shape()[0] : w->shape()[1], K = tb ? w->shape()[1] : w->shape()[0];
+                std::vector<float> wt((size_t)(N * K));  // W^T, N x K
+                const float* src = w->data_ptr<float>();
+                for (int64_t r = 0; r < N; ++r)
+                    for (int64_t c = 0; c < K; ++c) wt[(size_t)(r * K + c)] = tb ? src[r * K + c] : src[c * N + r];
+                if (at_most_two_per_four(wt.data(), N, K)) {
+                    std::vector<float> scales;
+                    std::vector<int8_t> q;
+                    quantize_rows(wt.data(), N, K, scales, q);
+                    const std::string base = n.name();
+                    const std::string wq = fresh(g, names, wn + "_int8_t");
+                    names[wq] = 1;
+                    if (K % 4 == 0) {
+                        SparseInitializer rec = nm24_record(q, N, K);
+                        st.int8_bytes += (int64_t)rec.stored_bytes();
+                        out->add_sparse_initializer(wq, std::move(rec));
+                    } else {
+                        Tensor t({N, K}, DType::Int8);
+                        std::memcpy(t.data(), q.data(), q.size());
+                        st.int8_bytes += (int64_t)q.size();
+                        out->add_initializer(wq, std::move(t));
+                    }
+                    st.int8_bytes += 4 * N;
+                    st.float_bytes += 4 * N * K;
+                    std::vector<std::string> qo;
+                    for (const char* suffix : {"_quantized", "_scale", "_zero_point"}) {
+                        qo.push_back(fresh(g, names, n.inputs()[0] + "/" + base + suffix));
+                        names[qo.back()] = 1;
+                    }
+                    const std::string dq_name = fresh(g, names, base + "_quantize_input");
+                    names[dq_name] = 1;
+                    nodes.push_back(std::make_shared<Node>(dq_name, "DynamicQuantizeLinear",
+                                                           std::vector<std::string>{n.inputs()[0]}, qo));
+                    std::vector<std::string> qmm_out = n.outputs();
+                    if (bias) {
+                        qmm_out = {fresh(g, names, n.outputs()[0] + "/" + base + "_product")};
+                        names[qmm_out[0]] = 1;
+                    }
+                    auto qmm = std::make_shared<Node>(bias ? fresh(g, names, base + "_product") : base,
+                                                      "QuantizedMatMul",
+                                                      std::vector<std::string>{qo[0], wq, qo[1], qo[2]}, qmm_out);
+                    names[qmm->name()] = 1;
+                    qmm->set_attr("b_scales", scales);
+                    qmm->set_attr("b_zero_point", (int64_t)0);
+                    qmm->set_attr("transB", (int64_t)1);
+                    nodes.push_back(qmm);
+                    if (bias) {
+                        nodes.push_back(std::make_shared<Node>(base, "Add",
+                                                               std::vector<std::string>{qmm_out[0], n.inputs()[2]},
+                                                               n.outputs()));
+                    }
+                    ++consumed[wn];
+                    ++st.rewritten;
+                    done = true;
+                }
             }
         }
         if (!done) nodes.push_back(std::make_shared<Node>(n));

@@ -292,3 +292,66 @@ def test_quantize_ops_in_sessions(tmp_path):
         assert c.dtype == np.uint8 and np.array_equal(c, c_ref)
         assert np.array_equal(bits(d), bits(d_ref))
         assert np.array_equal(bits(e), bits(e_ref))
+
+
+def test_dynamic_int8_session_xw(tmp_path):
+    """quantization="dynamic_int8" on the x . W form (Gemm with transB and a
+    bias, MatMul(x, W)): DynamicQuantizeLinear + QuantizedMatMul with the 2:4
+    weight as the second operand, on the device-resident plan and node by
+    node, bit-exact against the oracle applied node by node (per output
+    column: quantization::quantized_matmul of the quantized activation with
+    that column); the Gemm whose bias is not a vector stays fp32."""
+    from pyflamert_amd import pfm, session
+
+    sys.path.insert(0, str(__import__("pathlib").Path(__file__).parent))
+    from test_runtime_cpu import xw_graph
+
+    rng = np.random.default_rng(13)
+    T, K, N1, N2 = 70, 512, 384, 256
+    m, w1, b1, w2 = xw_graph(rng, T=T, K=K, N1=N1, N2=N2)
+    p = str(tmp_path / "xw.pfm")
+    pfm.save(m, p)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+
+    def qmm_xw(act, wt):
+        N, Kk = wt.shape
+        s, _ = O.orc_dynamic_params_per_channel(wt.reshape(1, N, Kk))
+        q = O.orc_quantize(wt, s, np.zeros(N, np.int32), O.I8, (1, N, Kk))
+        aq, xs, xz = dql_oracle(act.ravel())
+        aq = aq.reshape(act.shape)
+        cols = [O.orc_quantized_matmul(aq, np.ascontiguousarray(q[n:n + 1].T), xs, np.float32(s[n]), int(xz), 0)
+                for n in range(N)]
+        return np.concatenate(cols, axis=1)
+
+    h = O.orc_add(qmm_xw(x, w1), b1)
+    y_ref = qmm_xw(O.orc_relu(h), np.ascontiguousarray(w2.T))
+    z_ref = O.orc_gemm(x, m["initializers"]["w4"], m["initializers"]["c4"])
+    for lvl in (2, 0):
+        say(f"dynamic int8 x . W session, optimization level {lvl}")
+        s = session.InferenceSession(p, session.SessionOptions(quantization="dynamic_int8", optimization_level=lvl))
+        y, z = s.run(None, {"x": x})
+        assert s.device_plan()[0] == (lvl > 0)
+        assert np.array_equal(bits(y), bits(y_ref)), lvl
+        assert np.array_equal(bits(z), bits(z_ref)), lvl
+
+
+def test_sp24_xw_entry_point(ctx):
+    """pfr_sp24_gemm_qt directly: int8 and uint8 activations with zero points,
+    row counts that are not multiples of the tile, against the per-column
+    oracle."""
+    rng = np.random.default_rng(17)
+    for T, K, M in ((1, 512, 256), (37, 300, 200), (130, 1024, 512)):
+        q, s = rand_24(rng, M, K)
+        W = ctx.sp24_pack(q, s)
+        for u8 in (False, True):
+            act = (rng.integers(0, 256, (T, K)).astype(np.uint8) if u8
+                   else rng.integers(-128, 128, (T, K)).astype(np.int8))
+            zp = 131 if u8 else -5
+            say(f"2:4 x . W T={T} K={K} M={M} {'uint8' if u8 else 'int8'}")
+            Y = np.empty((T, M), np.float32)
+            _lib.check(ctx._lib.pfr_sp24_gemm_qt(ctx.handle, W.handle, act.ctypes.data, _lib.PFR_U8 if u8 else _lib.PFR_I8,
+                                                 T, 0.03, zp, Y.ctypes.data))
+            for n in rng.choice(M, 8, replace=False):
+                ref = O.orc_quantized_matmul(act, np.ascontiguousarray(q[n:n + 1].T), np.float32(0.03), np.float32(s[n]),
+                                             zp, 0)
+                assert np.array_equal(bits(Y[:, n:n + 1]), bits(ref)), (T, n, u8)

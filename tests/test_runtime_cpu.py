@@ -291,6 +291,54 @@ def quant_graph(rng, K=64, M1=48, M2=32, N=5, keep_dense=False):
     return m, w1, w2
 
 
+def xw_graph(rng, T=6, K=64, N1=48, N2=32):
+    """The x . W form: Gemm(x, W1 N1 x K, transB 1, bias) -> Relu ->
+    MatMul(., W2 N1 x N2), both 2:4 along K, plus a Gemm whose bias is not a
+    vector of N (left alone)."""
+    def pruned24(m, k):
+        w = rng.standard_normal((m, k)).astype(np.float32)
+        return O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(m, k))
+    w1 = pruned24(N1, K)                          # stored N x K (transB = 1)
+    w2 = np.ascontiguousarray(pruned24(N2, N1).T)  # stored K x N, groups along K
+    b1 = rng.standard_normal(N1).astype(np.float32)
+    w4 = np.ascontiguousarray(pruned24(9, K).T)
+    m = {"name": "xw", "inputs": [("x", 0, [T, K])], "outputs": [("y", 0, [T, N2]), ("z", 0, [T, 9])],
+         "initializers": {"w1": w1, "b1": b1, "w2": w2, "w4": w4, "c4": np.ones((T, 9), np.float32)},
+         "nodes": [("fc1", "Gemm", ["x", "w1", "b1"], ["h"], {"transB": 1}), ("r", "Relu", ["h"], ["a"], {}),
+                   ("fc2", "MatMul", ["a", "w2"], ["y"], {}), ("fc4", "Gemm", ["x", "w4", "c4"], ["z"], {})]}
+    return m, w1, b1, w2
+
+
+def test_dynamic_int8_rewrite_xw(tmp_path):
+    """The x . W form of the rewrite: Gemm(x, W, b) with transB and
+    MatMul(x, W) become DynamicQuantizeLinear + QuantizedMatMul(X_q, W_q^T)
+    (transB 1, per-output-column b_scales) [+ Add(bias)], with W_q^T the
+    per-column quantization of W (oracle, on W^T's rows); a Gemm whose bias is
+    not a vector of N stays."""
+    rng = np.random.default_rng(3)
+    m, w1, b1, w2 = xw_graph(rng)
+    p = write(tmp_path, "xw.pfm", m)
+    out = str(tmp_path / "xw_int8.pfm")
+    assert session.quantize_model(p, out) == 2
+    q = pfm.load(out)
+    ops = [n[1] for n in q["nodes"]]
+    assert ops == ["DynamicQuantizeLinear", "QuantizedMatMul", "Add", "Relu", "DynamicQuantizeLinear",
+                   "QuantizedMatMul", "Gemm"]
+    assert q["nodes"][2][3] == ["h"] and q["nodes"][2][2][1] == "b1" and q["nodes"][5][3] == ["y"]
+    assert "w1" not in q["initializers"] and "w2" not in q["initializers"] and "w4" in q["initializers"]
+    for dq, node in ((q["nodes"][0], q["nodes"][1]), (q["nodes"][4], q["nodes"][5])):
+        assert node[2][0] == dq[3][0] and node[2][2:] == dq[3][1:]  # X_q, X_scale, X_zero_point
+    for wt, node in ((w1, q["nodes"][1]), (np.ascontiguousarray(w2.T), q["nodes"][5])):
+        N, K = wt.shape
+        s_ref, _ = O.orc_dynamic_params_per_channel(wt.reshape(1, N, K))
+        q_ref = O.orc_quantize(wt, s_ref, np.zeros(N, np.int32), O.I8, (1, N, K))
+        rec = q["sparse_initializers"][node[2][1]]
+        assert rec["format"] == "2:4" and np.array_equal(pfm.record_to_dense(rec), q_ref)
+        assert np.array_equal(np.array(node[4]["b_scales"], np.float32).view(np.uint32),
+                              np.asarray(s_ref, np.float32).view(np.uint32))
+        assert node[4]["transB"] == 1 and node[4]["b_zero_point"] == 0
+
+
 def test_dynamic_int8_rewrite(tmp_path):
     """The rewrite replaces the 2:4 MatMul(W, X) nodes by
     DynamicQuantizeLinear + QuantizedMatMul with the per-row int8 weights and
