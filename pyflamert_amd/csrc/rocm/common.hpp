@@ -119,7 +119,8 @@ struct pfr_csr {
     bool cols_sorted = false;
     // Sliced-ELL copy of a float32 weight for the column-slice kernel (null
     // when the shape does not qualify).  Rows are reordered into slabs of
-    // kSellRows; K is cut into chunks of sell_kc rows.  For slab s and chunk
+    // kSellRows; K is cut into chunks of sell_kc rows (a multiple of 16, at
+    // most kSellMaxKC; the last chunk may be partial).  For slab s and chunk
     // c, sell_soff[s * (sell_nch + 1) + c] is the first int4 of its run of
     // 8-step groups (the run ends at entry c + 1).  A group is 64 int4: entry
     // 4*r + j holds steps 2j and 2j+1 of the slab's row r as {byte offset of
@@ -157,8 +158,8 @@ constexpr int kChainRows = 64;     // rows per row-chain slab of the global-gath
 constexpr int kChainXMax = 16384;  // x staged in LDS (with its zero slot) below this K
 constexpr int kSellRows = 16;      // rows per slab (one wave: 4 lanes x 4 columns per row)
 constexpr int kSellCols = 16;      // columns of X per workgroup slice
-constexpr int kSellMaxKC = 2048;   // K rows per LDS chunk (2048 x 64 B = 128 KiB)
-constexpr int kSellStepPad = 16;   // steps per (slab, chunk) run are a multiple of this
+constexpr int kSellMaxKC = 1024;   // K rows per LDS chunk (1024 x 64 B = 64 KiB, two buffers)
+constexpr int kSellStepPad = 8;    // steps per (slab, chunk) run are a multiple of this (one group)
 constexpr int kSellTail = 128;     // int4 after the last run, read by the unconditional prefetch
 }
 

@@ -71,7 +71,9 @@ void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vecto
                 const float* vals, hipStream_t s) {
     const int64_t M = w->M, K = w->K;
     if (M == 0 || K == 0 || w->nnz == 0) return;
-    const int64_t kc = std::min<int64_t>(K, pfr::kSellMaxKC);
+    // chunks of whole 16-row LDS loads: the staging of a chunk never reaches
+    // the zero row that follows it
+    const int64_t kc = std::min<int64_t>((K + 15) / 16 * 16, pfr::kSellMaxKC);
     const int64_t nch = (K + kc - 1) / kc;
     if (M * nch > (int64_t(1) << 26)) return;  // count table too large: keep the row kernels
     for (int64_t r = 0; r < M; ++r)

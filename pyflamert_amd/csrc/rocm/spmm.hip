@@ -870,101 +870,183 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Column-slice kernel over the sliced-ELL copy (layout at pfr_csr::sell_blk).
 // A workgroup of W waves owns W slabs (16 rows each) and one 16-column slice
-// of X.  For every K chunk it stages X[chunk rows, slice] (64 B per row) in
-// LDS, then each wave walks its slab: lane 4r+q accumulates columns 4q..4q+3
-// of slab row r.  The pairs of a step come from one int4 per lane per eight
-// steps, broadcast to the row's four lanes with quad_perm DPP (which the
-// compiler folds into the address add and the multiply).  Products are added
-// in the row's storage order, so strict mode matches the row kernels bit for
-// bit; padding steps add RN(+0 * +0) = +0, which leaves any sum unchanged
-// (an accumulator that starts at +0 never becomes -0 under RN addition).
+// of X.  X is staged chunk by chunk (kc rows of 64 B) into two LDS buffers:
+// while the waves walk chunk c in one buffer, the 16-row loads of chunk c + 1
+// go straight from global memory into the other (global_load_lds, one 1 KiB
+// load per wave instruction), interleaved with the walk.  Each wave walks its
+// slab: lane 4r+q accumulates columns 4q..4q+3 of slab row r.  The pairs of a
+// step come from one int4 per lane per eight steps, broadcast to the row's
+// four lanes with quad_perm DPP (which the compiler folds into the address
+// add and the multiply).  Products are added in the row's storage order, so
+// strict mode matches the row kernels bit for bit; padding steps add
+// RN(+0 * +0) = +0, which leaves any sum unchanged (an accumulator that
+// starts at +0 never becomes -0 under RN addition).
+template <int W>
+constexpr int sell_loads_per_iter() {
+    // a chunk's 16-row loads per wave, spread over about six iterations of
+    // the walk (two groups each); the rest are issued after the walk
+    return (pfr::kSellMaxKC / 16 / W + 5) / 6;
+}
+
+using lds_char = __attribute__((address_space(3))) char;
+
+// One (slab, chunk) run of the column-slice kernel: T groups of 8 steps, two
+// per iteration and a last single one when T is odd, the next group always
+// loaded one group ahead, past the run's end into the next run or the tail,
+// and never used there.  xb is the lane's view of the chunk's X rows.  With
+// MORE, the walk also copies DPI 16-row blocks of the next chunk per
+// iteration into nxt, through registers: loaded in one iteration, written to
+// LDS in the next, so each wait is for loads one iteration old.  Block i is
+// rows 16j .. 16j+15, j = min(j0 + jstep * i, jmax); lane 4r+q copies row
+// min(16j + r, last) of src (which points at the lane's four columns) to
+// nxt + 1024 j + 16 lane.  The loads are unconditional (clamped), so no
+// branch splits the load queue; d counts the blocks issued.
+template <bool FAST, bool MORE, int DPI>
+__device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, int T, const char* __restrict__ xb,
+                                          float4* __restrict__ nxt, const float* __restrict__ src, int64_t ldx,
+                                          int lane, int j0, int jstep, int jmax, int last, int& d, float& a0,
+                                          float& a1, float& a2, float& a3) {
+    auto comp = [&](const int4 w) {
+        float4 xv[8];
+        static_for<0, 8>([&](auto tc) {
+            constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;  // quad_perm [j,j,j,j]
+            const int o = __builtin_amdgcn_mov_dpp((t & 1) ? w.z : w.x, ctrl, 0xF, 0xF, true);
+            xv[t] = *reinterpret_cast<const float4*>(xb + o);
+        });
+        static_for<0, 8>([&](auto tc) {
+            constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+            const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
+            a0 = madd<FAST>(a0, wv, xv[t].x);
+            a1 = madd<FAST>(a1, wv, xv[t].y);
+            a2 = madd<FAST>(a2, wv, xv[t].z);
+            a3 = madd<FAST>(a3, wv, xv[t].w);
+        });
+    };
+    const int r = lane >> 2;
+    constexpr int ND = MORE ? DPI : 1;
+    using f4 = float __attribute__((ext_vector_type(4)));  // a plain vector: stays in registers
+    f4 st[ND];
+    int js[ND];
+    int4 wa = blk[p], wb;
+    if constexpr (MORE) {
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+            js[i] = min(j0 + jstep * (d + i), jmax);
+            st[i] = *reinterpret_cast<const f4*>(src + (int64_t)min(js[i] * 16 + r, last) * ldx);
+        }
+        d += ND;
+    }
+    int t = 0;
+    for (; t + 2 <= T; t += 2) {
+        wb = blk[p + 64];
+        asm volatile("" ::: "memory");  // keep the prefetch ahead of the LDS reads
+        comp(wa);
+        if constexpr (MORE) {
+#pragma unroll
+            for (int i = 0; i < ND; ++i) *reinterpret_cast<f4*>(nxt + js[i] * 64 + lane) = st[i];
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                js[i] = min(j0 + jstep * (d + i), jmax);
+                st[i] = *reinterpret_cast<const f4*>(src + (int64_t)min(js[i] * 16 + r, last) * ldx);
+            }
+            d += ND;
+        }
+        wa = blk[p + 128];
+        asm volatile("" ::: "memory");
+        comp(wb);
+        p += 128;
+    }
+    if (t < T) comp(wa);  // an odd count: the last group is already loaded
+    if constexpr (MORE) {
+#pragma unroll
+        for (int i = 0; i < ND; ++i) *reinterpret_cast<f4*>(nxt + js[i] * 64 + lane) = st[i];
+    }
+}
+
 template <bool FAST, bool XVEC, int W>
 __global__ __launch_bounds__(64 * W) void k_spmm_sell(
     int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ soff, const int4* __restrict__ blk, const float* __restrict__ X,
     int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, int yvec,
     const float* __restrict__ bias, int64_t c_size, float beta, int act) {
-    extern __shared__ float4 xs[];  // [(kc + 1) * 4]: kc rows of 16 floats, then a zero row
+    // two buffers of kc + 1 rows of 16 floats; row kc of each is zero
+    extern __shared__ float4 xs[];
     constexpr int NT = 64 * W;
+    constexpr int DPI = sell_loads_per_iter<W>();
     const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, q = lane & 3;
-    const int slab = __builtin_amdgcn_readfirstlane((int)blockIdx.x * W + (tid >> 6));
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slab = __builtin_amdgcn_readfirstlane((int)blockIdx.x * W + wave);
     const int n0 = (int)blockIdx.y * pfr::kSellCols;
-    const char* xb = reinterpret_cast<const char*>(xs) + q * 16;
+    const int bufq = (kc + 1) * 4;  // float4 per buffer
+    if (tid < 8) xs[(tid >> 2) * bufq + kc * 4 + (tid & 3)] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    if (tid < 4) xs[kc * 4 + tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const int slots = kc * 4;
-    for (int c = 0; c < nch; ++c) {
-        if (c) __syncthreads();  // every wave is done with the previous chunk
-        const int k0 = c * kc;
-        const int rows = min(kc, K - k0);
-        for (int base = 0; base < slots; base += 8 * NT) {
-            float4 st[8];
-            if constexpr (XVEC) {
-                // unconditional loads from clamped addresses, selected afterwards,
-                // so the eight loads are in flight together
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int e = min(base + tid + i * NT, slots - 1);
-                    const int k = k0 + min(e >> 2, rows - 1);
-                    const int n = min(n0 + (e & 3) * 4, N - 4);
-                    st[i] = *reinterpret_cast<const float4*>(X + (int64_t)k * ldx + n);
-                }
+
+    // Load i of this wave for chunk c: rows 16j .. 16j+15 of the chunk, lane
+    // 4r+q copying row 16j+r, columns n0+4q .. n0+4q+3, to LDS bytes
+    // j*1024 + 16*lane of the chunk's buffer.  Loads past the wave's share
+    // repeat its last one, rows past K repeat the chunk's last row and
+    // columns past N repeat the last four; nothing reads those copies.
+    const int nld = kc / 16;
+    const int nd = (nld + W - 1) / W;
+    const float* xcol = X + min(n0 + q * 4, N - 4);
+    auto dma = [&](int c, int i) {
+        const int j = min(wave + W * i, nld - 1);
+        const int k0 = c * kc, last = min(kc, K - k0) - 1;
+        const float* src = xcol + (int64_t)(k0 + min(j * 16 + r, last)) * ldx;
+        lds_char* dst = (lds_char*)(xs + (c & 1) * bufq) + j * 1024;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    };
+    // Register staging (any N and alignment) of chunk c into its buffer.
+    auto stage_regs = [&](int c) {
+        const int k0 = c * kc, rows = min(kc, K - k0);
+        float4* xb = xs + (c & 1) * bufq;
+        for (int e = tid; e < kc * 4; e += NT) {
+            const int kr = e >> 2, n = n0 + (e & 3) * 4;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (kr < rows) {
+                const float* xr = X + (int64_t)(k0 + kr) * ldx;
+                if (n < N) v.x = xr[n];
+                if (n + 1 < N) v.y = xr[n + 1];
+                if (n + 2 < N) v.z = xr[n + 2];
+                if (n + 3 < N) v.w = xr[n + 3];
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int e = base + tid + i * NT;
-                if (e < slots) {
-                    const int kr = e >> 2, n = n0 + (e & 3) * 4;
-                    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    if (kr < rows) {
-                        const float* xr = X + (int64_t)(k0 + kr) * ldx;
-                        if constexpr (XVEC) {
-                            if (n < N) v = st[i];
-                        } else {
-                            if (n < N) v.x = xr[n];
-                            if (n + 1 < N) v.y = xr[n + 1];
-                            if (n + 2 < N) v.z = xr[n + 2];
-                            if (n + 3 < N) v.w = xr[n + 3];
-                        }
-                    }
-                    xs[e] = v;
-                }
-            }
+            xb[e] = v;
         }
+    };
+    auto sync_chunk = [&]() {
+        if constexpr (XVEC) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads have landed
         __syncthreads();
+    };
+
+    if constexpr (XVEC) {
+        for (int i = 0; i < nd; ++i) dma(0, i);
+    } else {
+        stage_regs(0);
+    }
+    sync_chunk();
+    for (int c = 0; c < nch; ++c) {
+        const char* xb = reinterpret_cast<const char*>(xs + (c & 1) * bufq) + q * 16;
+        int d = 0;  // loads of chunk c + 1 issued by this wave
+        const bool more = c + 1 < nch;
         if (slab < nslab) {
             const int s0 = soff[slab * (nch + 1) + c], s1 = soff[slab * (nch + 1) + c + 1];
-            auto comp = [&](const int4 w) {
-                float4 xv[8];
-                static_for<0, 8>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;  // quad_perm [j,j,j,j]
-                    const int o = __builtin_amdgcn_mov_dpp((t & 1) ? w.z : w.x, ctrl, 0xF, 0xF, true);
-                    xv[t] = *reinterpret_cast<const float4*>(xb + o);
-                });
-                static_for<0, 8>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
-                    const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
-                    a0 = madd<FAST>(a0, wv, xv[t].x);
-                    a1 = madd<FAST>(a1, wv, xv[t].y);
-                    a2 = madd<FAST>(a2, wv, xv[t].z);
-                    a3 = madd<FAST>(a3, wv, xv[t].w);
-                });
-            };
-            // groups of 8 steps, two per iteration (runs are a multiple of 16
-            // steps); the next group is always loaded one group ahead, past
-            // the run's end into the next run or the tail, and never used there
             const int T = __builtin_amdgcn_readfirstlane((s1 - s0) / 64);
-            int p = s0 + lane;
-            int4 wa = blk[p], wb;
-            for (int t = 0; t < T; t += 2) {
-                wb = blk[p + 64];
-                asm volatile("" ::: "memory");  // keep the prefetch ahead of the LDS reads
-                comp(wa);
-                wa = blk[p + 128];
-                asm volatile("" ::: "memory");
-                comp(wb);
-                p += 128;
+            const int k1 = (c + 1) * kc;
+            float4* nxt = xs + ((c + 1) & 1) * bufq;
+            if (XVEC && more)
+                sell_walk<FAST, true, DPI>(blk, s0 + lane, T, xb, nxt, xcol + (int64_t)k1 * ldx, ldx, lane, wave, W,
+                                           nld - 1, min(kc, K - k1) - 1, d, a0, a1, a2, a3);
+            else
+                sell_walk<FAST, false, DPI>(blk, s0 + lane, T, xb, nxt, xcol, ldx, lane, wave, W, nld - 1, 0, d, a0,
+                                            a1, a2, a3);
+        }
+        if (more) {
+            if constexpr (XVEC) {
+                for (; d < nd; ++d) dma(c + 1, d);
+            } else {
+                stage_regs(c + 1);  // the other buffer: last read in chunk c - 1
             }
+            sync_chunk();
         }
     }
     if (slab < nslab) {
@@ -1007,19 +1089,19 @@ int next_pow2(int n) {
 }
 
 
-// Column-slice kernel launch; false when the weight has no sliced-ELL copy.
+// Column-slice kernel launch with W waves per workgroup.
 template <bool FAST, bool XVEC, int W>
 void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
                    int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
     auto kern = k_spmm_sell<FAST, XVEC, W>;
-    const size_t lds = (size_t)(Wt->sell_kc + 1) * 64;
+    const size_t lds = (size_t)(Wt->sell_kc + 1) * 64 * 2;
     // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
     static uint64_t allowed = 0;  // bit d: done on device d (< 64)
     const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
     if (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit)) {
         PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        if (bit && lds == (size_t)(pfr::kSellMaxKC + 1) * 64) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
+        if (bit && lds == (size_t)(pfr::kSellMaxKC + 1) * 64 * 2) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
     }
     dim3 grid((unsigned)((Wt->sell_nslab + W - 1) / W), (unsigned)((N + pfr::kSellCols - 1) / pfr::kSellCols));
     hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, ctx->stream, N, (int)Wt->K, Wt->sell_kc, Wt->sell_nch,
@@ -1030,14 +1112,16 @@ void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
 template <bool FAST, bool XVEC>
 void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
                    int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
-    // 16 waves per workgroup when that still gives a workgroup per CU,
-    // otherwise smaller workgroups to spread the slabs over more CUs
+    // The most waves per workgroup (one workgroup per CU: its LDS takes most
+    // of the CU) that still gives every CU a workgroup, and at least four:
+    // the workgroup's waves share the staging of its X slice.
     const int64_t slices = (N + pfr::kSellCols - 1) / pfr::kSellCols;
-    const int64_t wg16 = (Wt->sell_nslab + 15) / 16 * slices;
-    if (wg16 >= ctx->num_cu)
-        launch_sell_w<FAST, XVEC, 16>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
-    else
-        launch_sell_w<FAST, XVEC, 4>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
+    auto wgs = [&](int64_t w) { return (Wt->sell_nslab + w - 1) / w * slices; };
+#define PFR_SELLW(WV) launch_sell_w<FAST, XVEC, WV>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act)
+    if (wgs(16) >= ctx->num_cu) PFR_SELLW(16);
+    else if (wgs(8) >= ctx->num_cu) PFR_SELLW(8);
+    else PFR_SELLW(4);  // fewer waves would each stage more of X than they walk
+#undef PFR_SELLW
 }
 
 void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
