@@ -868,39 +868,28 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// Column-slice kernel over the sliced-ELL copy (layout at pfr_csr::sell_blk).
-// A workgroup of W waves owns W slabs (16 rows each) and one 16-column slice
-// of X.  X is staged chunk by chunk (kc rows of 64 B) into two LDS buffers:
-// while the waves walk chunk c in one buffer, the 16-row loads of chunk c + 1
-// go straight from global memory into the other (global_load_lds, one 1 KiB
-// load per wave instruction), interleaved with the walk.  Each wave walks its
-// slab: lane 4r+q accumulates columns 4q..4q+3 of slab row r.  The pairs of a
-// step come from one int4 per lane per eight steps, broadcast to the row's
-// four lanes with quad_perm DPP (which the compiler folds into the address
-// add and the multiply).  Products are added in the row's storage order, so
-// strict mode matches the row kernels bit for bit; padding steps add
-// RN(+0 * +0) = +0, which leaves any sum unchanged (an accumulator that
-// starts at +0 never becomes -0 under RN addition).
 template <int W>
 constexpr int sell_loads_per_iter() {
-    // a chunk's 16-row loads per wave, spread over about six iterations of
-    // the walk (two groups each); the rest are issued after the walk
-    return (pfr::kSellMaxKC / 16 / W + 5) / 6;
+    // a chunk's 16-row loads per wave, spread over about three iterations of
+    // the walk (four groups each); the rest are issued after the walk
+    return (pfr::kSellMaxKC / 16 / W + 2) / 3;
 }
 
 using lds_char = __attribute__((address_space(3))) char;
 
-// One (slab, chunk) run of the column-slice kernel: T groups of 8 steps, two
-// per iteration and a last single one when T is odd, the next group always
-// loaded one group ahead, past the run's end into the next run or the tail,
-// and never used there.  xb is the lane's view of the chunk's X rows.  With
-// MORE, the walk also copies DPI 16-row blocks of the next chunk per
-// iteration into nxt, through registers: loaded in one iteration, written to
-// LDS in the next, so each wait is for loads one iteration old.  Block i is
-// rows 16j .. 16j+15, j = min(j0 + jstep * i, jmax); lane 4r+q copies row
-// min(16j + r, last) of src (which points at the lane's four columns) to
-// nxt + 1024 j + 16 lane.  The loads are unconditional (clamped), so no
-// branch splits the load queue; d counts the blocks issued.
+// One (slab, chunk) run of the column-slice kernel: T groups of 8 steps.
+// The groups' int4 sit in a ring of four registers: four groups per
+// iteration, each reloaded with the group four ahead as soon as it is used
+// (so loads run three groups ahead), past the run's end into the next run or
+// the tail, and never used there; a last partial iteration uses what is
+// already loaded.  xb is the lane's view of the chunk's X rows.  With MORE,
+// the walk also copies DPI 16-row blocks of the next chunk per iteration
+// into nxt, through registers: loaded in one iteration, written to LDS in the
+// next, so each wait is for loads one iteration old.  Block i is rows 16j ..
+// 16j+15, j = min(j0 + jstep * i, jmax); lane 4r+q copies row min(16j + r,
+// last) of src (which points at the lane's four columns) to nxt + 1024 j +
+// 16 lane.  The loads are unconditional (clamped), so no branch splits the
+// load queue; d counts the blocks issued.
 template <bool FAST, bool MORE, int DPI>
 __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, int T, const char* __restrict__ xb,
                                           float4* __restrict__ nxt, const float* __restrict__ src, int64_t ldx,
@@ -927,42 +916,59 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
     using f4 = float __attribute__((ext_vector_type(4)));  // a plain vector: stays in registers
     f4 st[ND];
     int js[ND];
-    int4 wa = blk[p], wb;
-    if constexpr (MORE) {
+    auto load_next = [&]() {
 #pragma unroll
         for (int i = 0; i < ND; ++i) {
             js[i] = min(j0 + jstep * (d + i), jmax);
             st[i] = *reinterpret_cast<const f4*>(src + (int64_t)min(js[i] * 16 + r, last) * ldx);
         }
         d += ND;
-    }
-    int t = 0;
-    for (; t + 2 <= T; t += 2) {
-        wb = blk[p + 64];
-        asm volatile("" ::: "memory");  // keep the prefetch ahead of the LDS reads
-        comp(wa);
-        if constexpr (MORE) {
-#pragma unroll
-            for (int i = 0; i < ND; ++i) *reinterpret_cast<f4*>(nxt + js[i] * 64 + lane) = st[i];
-#pragma unroll
-            for (int i = 0; i < ND; ++i) {
-                js[i] = min(j0 + jstep * (d + i), jmax);
-                st[i] = *reinterpret_cast<const f4*>(src + (int64_t)min(js[i] * 16 + r, last) * ldx);
-            }
-            d += ND;
-        }
-        wa = blk[p + 128];
-        asm volatile("" ::: "memory");
-        comp(wb);
-        p += 128;
-    }
-    if (t < T) comp(wa);  // an odd count: the last group is already loaded
-    if constexpr (MORE) {
+    };
+    auto store_next = [&]() {
 #pragma unroll
         for (int i = 0; i < ND; ++i) *reinterpret_cast<f4*>(nxt + js[i] * 64 + lane) = st[i];
+    };
+    int4 w0 = blk[p], w1 = blk[p + 64], w2 = blk[p + 128], w3 = blk[p + 192];
+    if constexpr (MORE) load_next();
+    int t = 0;
+    for (; t + 4 <= T; t += 4) {
+        comp(w0);
+        w0 = blk[p + 256];
+        asm volatile("" ::: "memory");  // keep each reload ahead of the next group's LDS reads
+        comp(w1);
+        w1 = blk[p + 320];
+        asm volatile("" ::: "memory");
+        if constexpr (MORE) {
+            store_next();
+            load_next();
+        }
+        comp(w2);
+        w2 = blk[p + 384];
+        asm volatile("" ::: "memory");
+        comp(w3);
+        w3 = blk[p + 448];
+        asm volatile("" ::: "memory");
+        p += 256;
     }
+    if (t < T) comp(w0);
+    if (t + 1 < T) comp(w1);
+    if (t + 2 < T) comp(w2);
+    if constexpr (MORE) store_next();
 }
 
+// Column-slice kernel over the sliced-ELL copy (layout at pfr_csr::sell_blk).
+// A workgroup of W waves owns W slabs (16 rows each) and one 16-column slice
+// of X.  X is staged chunk by chunk (kc rows of 64 B) into two LDS buffers:
+// while the waves walk chunk c in one buffer, the 16-row loads of chunk c + 1
+// go straight from global memory into the other (global_load_lds, one 1 KiB
+// load per wave instruction), interleaved with the walk.  Each wave walks its
+// slab: lane 4r+q accumulates columns 4q..4q+3 of slab row r.  The pairs of a
+// step come from one int4 per lane per eight steps, broadcast to the row's
+// four lanes with quad_perm DPP (which the compiler folds into the address
+// add and the multiply).  Products are added in the row's storage order, so
+// strict mode matches the row kernels bit for bit; padding steps add
+// RN(+0 * +0) = +0, which leaves any sum unchanged (an accumulator that
+// starts at +0 never becomes -0 under RN addition).
 template <bool FAST, bool XVEC, int W>
 __global__ __launch_bounds__(64 * W) void k_spmm_sell(
     int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
@@ -1033,7 +1039,9 @@ __global__ __launch_bounds__(64 * W) void k_spmm_sell(
             const int T = __builtin_amdgcn_readfirstlane((s1 - s0) / 64);
             const int k1 = (c + 1) * kc;
             float4* nxt = xs + ((c + 1) & 1) * bufq;
-            if (XVEC && more)
+            // the 16-wave launch (four waves per SIMD hide each other's
+            // latencies) stages whole chunks between walks instead
+            if (XVEC && W <= 8 && more)
                 sell_walk<FAST, true, DPI>(blk, s0 + lane, T, xb, nxt, xcol + (int64_t)k1 * ldx, ldx, lane, wave, W,
                                            nld - 1, min(kc, K - k1) - 1, d, a0, a1, a2, a3);
             else
