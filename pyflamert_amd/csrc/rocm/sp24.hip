@@ -360,9 +360,22 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     const float xs_eff = xs_dev ? *xs_dev : xs;
     const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
     const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
-    // the exact accumulator of row m (int32 wrap-around arithmetic; the true
+    // This lane's 16 rows: their scales (and row sums, for a zero-point
+    // correction) loaded together, from clamped rows, so the epilogue waits
+    // for one load latency rather than one per row.
+    float wsv[4][4];
+    uint32_t rsv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = min((int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r, M - 1);
+            if constexpr (OUT != PFR_SP24_OUT_I32) wsv[i][r] = ws[m];
+            rsv[i][r] = zcorr ? (uint32_t)row_sum[m] : 0u;
+        }
+    // the exact accumulator of a row (int32 wrap-around arithmetic; the true
     // value is within int32 for K < 2^17)
-    auto exact = [&](int32_t a, int m) { return zcorr ? (int32_t)((uint32_t)a - zcorr * (uint32_t)row_sum[m]) : a; };
+    auto exact = [&](int32_t a, uint32_t rs) { return (int32_t)((uint32_t)a - zcorr * rs); };
     if constexpr (OUT == PFR_SP24_OUT_I8) {
         // requantise into an LDS tile [256][128] (stage 0), then store 16-byte row pieces
         char* tile = st0;
@@ -372,10 +385,10 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
             for (int r = 0; r < 4; ++r) {
                 const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
                 const int m = (int)(mb0 * 16) + ml;
-                const float sab = m < M ? ws[m] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
+                const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float f = (float)exact(acc[i][j][r], m) * sab;
+                    const float f = (float)exact(acc[i][j][r], rsv[i][r]) * sab;
                     const float prod = f * inv_out;
                     int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
                     q = q < -128 ? -128 : (q > 127 ? 127 : q);
@@ -406,12 +419,12 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
                 const int m = (int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r;
                 if (m >= M) continue;
                 float sab = 1.0f;
-                if constexpr (OUT == PFR_SP24_OUT_F32) sab = ws[m] * xs_eff;
+                if constexpr (OUT == PFR_SP24_OUT_F32) sab = wsv[i][r] * xs_eff;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int64_t n = n0 + wn * 64 + 16 * j + c;
                     if (n >= N) continue;
-                    const int32_t v = exact(acc[i][j][r], m);
+                    const int32_t v = exact(acc[i][j][r], rsv[i][r]);
                     const int64_t o = (int64_t)m * ldy + n;
                     if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
                     else static_cast<float*>(Y)[o] = (float)v * sab;
