@@ -60,13 +60,30 @@ std::vector<int32_t> spmv_blocks(const std::vector<int32_t>& rowptr, int64_t M) 
     return starts;
 }
 
+// Row order of the sliced-ELL copy over b[0, n): the rows of a slab should
+// have similar counts in every chunk, which keeps the padding to the slab
+// maximum small.  A k-d split: the range is sorted by one chunk's count
+// (cycling through the chunks with the depth) and cut at a multiple of the
+// slab height near its middle, down to single slabs.  On the 4096 x 4096,
+// 10 % workload (four chunks) the stored steps are 1.079 x nnz, against 1.107
+// for sorting by chunk 0, then by chunk 1 within 8 buckets, and so on.
+void sell_order(const std::vector<int32_t>& cnt, int64_t nch, int32_t* b, int64_t n, int64_t depth) {
+    const int64_t R = pfr::kSellRows;
+    if (n <= R) return;
+    const int64_t c = depth % nch;
+    std::stable_sort(b, b + n, [&](int32_t x, int32_t y) {
+        return cnt[(size_t)(x * nch + c)] > cnt[(size_t)(y * nch + c)];
+    });
+    const int64_t h = (n / 2 + R - 1) / R * R;  // R <= h < n for n > R
+    sell_order(cnt, nch, b, h, depth + 1);
+    sell_order(cnt, nch, b + h, n - h, depth + 1);
+}
+
 // Sliced-ELL copy (layout described at pfr_csr::sell_blk).  Each row keeps
 // its storage order inside a chunk and chunks are visited in order, so the
 // copy needs the chunk index to be non-decreasing along every row (always
-// true for one chunk, and for ascending columns).  Rows are ordered so that
-// the rows of a slab have similar counts in every chunk, which keeps the
-// padding to the slab maximum small: sorted by their chunk-0 count, then
-// within 8 buckets by their chunk-1 count, within 64 by chunk 2, and so on.
+// true for one chunk, and for ascending columns).  Rows are ordered by
+// sell_order.
 void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
                 const float* vals, hipStream_t s) {
     const int64_t M = w->M, K = w->K;
@@ -86,17 +103,7 @@ void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vecto
     const int64_t nslab = (M + R - 1) / R;
     std::vector<int32_t> order((size_t)M);
     std::iota(order.begin(), order.end(), 0);
-    int64_t group = M;
-    for (int64_t c = 0; c < nch && group >= R; ++c) {
-        for (int64_t g0 = 0; g0 < M; g0 += group) {
-            const int64_t g1 = std::min(M, g0 + group);
-            std::stable_sort(order.begin() + g0, order.begin() + g1, [&](int32_t a, int32_t b) {
-                return cnt[(size_t)(a * nch + c)] > cnt[(size_t)(b * nch + c)];
-            });
-        }
-        group = std::max<int64_t>(R, (group / 8 + R - 1) / R * R);
-        if (group == R) break;
-    }
+    sell_order(cnt, nch, order.data(), M, 0);
     std::vector<int64_t> off((size_t)(nslab * nch + 1), 0);
     for (int64_t sl = 0; sl < nslab; ++sl)
         for (int64_t c = 0; c < nch; ++c) {
