@@ -1120,15 +1120,19 @@ void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
 template <bool FAST, bool XVEC>
 void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
                    int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
-    // The most waves per workgroup (one workgroup per CU: its LDS takes most
-    // of the CU) that still gives every CU a workgroup, and at least four:
-    // the workgroup's waves share the staging of its X slice.
+    // One workgroup runs per CU (its LDS takes most of the CU), so the launch
+    // takes ceil(workgroups / CUs) rounds.  A round of 4-, 8- and 16-wave
+    // workgroups takes about 1 : 1.30 : 2.14 (measured on the 4096 x 4096,
+    // 10 % weight at N = 64, 128 and 256, one round each); the wave count
+    // with the fewest estimated clocks runs, the larger on a tie.  Fewer than
+    // four waves lose: each wave then stages more of X than it walks.
     const int64_t slices = (N + pfr::kSellCols - 1) / pfr::kSellCols;
-    auto wgs = [&](int64_t w) { return (Wt->sell_nslab + w - 1) / w * slices; };
+    auto rounds = [&](int64_t w) { return ((Wt->sell_nslab + w - 1) / w * slices + ctx->num_cu - 1) / ctx->num_cu; };
+    const int64_t c16 = rounds(16) * 214, c8 = rounds(8) * 130, c4 = rounds(4) * 100;
 #define PFR_SELLW(WV) launch_sell_w<FAST, XVEC, WV>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act)
-    if (wgs(16) >= ctx->num_cu) PFR_SELLW(16);
-    else if (wgs(8) >= ctx->num_cu) PFR_SELLW(8);
-    else PFR_SELLW(4);  // fewer waves would each stage more of X than they walk
+    if (c16 <= c8 && c16 <= c4) PFR_SELLW(16);
+    else if (c8 <= c4) PFR_SELLW(8);
+    else PFR_SELLW(4);
 #undef PFR_SELLW
 }
 
