@@ -361,6 +361,23 @@ template <int R>
 constexpr int chain_ch() { return 32; }  // quad rows per chunk (a multiple of 16: the fold's batches)
 constexpr int kChainXUnroll = 6;
 
+// x[0 .. K) (stride ldx) into LDS as xs[0 .. K) plus a zero at xs[K], by NT
+// threads: eight loads per thread in flight (clamped addresses), then the
+// stores, instead of one load latency per element a thread stages.
+template <int NT>
+__device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, int K, int64_t ldx, int tid) {
+    for (int k0 = 0; k0 <= K; k0 += 8 * NT) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = x[(int64_t)min(k0 + tid + NT * i, K - 1) * ldx];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = k0 + tid + NT * i;
+            if (k <= K) xs[k] = k < K ? t[i] : 0.0f;
+        }
+    }
+}
+
 template <bool I8, int R>
 __global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
     int K, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm, const void* __restrict__ vals,
@@ -383,7 +400,7 @@ __global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
     // >= nch + 1 (the last fold needs one more barrier), a multiple of the unroll
     const int iters = (nch + kChainXUnroll) / kChainXUnroll * kChainXUnroll;
     if (wave == 0) {
-        for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
+        stage_x<64 * (1 + P)>(xs, x, K, ldx, tid);
         __syncthreads();
         // The fold is bound by the latency of its dependent adds; the LDS
         // reads of the next eight quad rows are issued before the adds of the
@@ -476,7 +493,7 @@ __global__ __launch_bounds__(64 * (1 + R / 8)) void k_spmv_chain_x(
     // latencies overlap
     load(0, v0, c0);
     load(min(1, nch - 1), v1, c1);
-    for (int k = tid; k <= K; k += 64 * (1 + P)) xs[k] = k < K ? x[(int64_t)k * ldx] : 0.0f;
+    stage_x<64 * (1 + P)>(xs, x, K, ldx, tid);
     __syncthreads();
     for (int i = 0; i < iters; i += 6) {
         chunk(i, v0, c0, v2, c2);
@@ -786,6 +803,104 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
         const int64_t f = (int64_t)row * ldy_r + (int64_t)lane * ldy_c;
         Y[f] = bias_add(v, f, bias, c_size, beta, act);
     }
+}
+
+// Fast mode, N = 1, over the row-chain copy with x staged in LDS (a zero at
+// index K for the padding steps): a workgroup of W waves per slab of R rows.
+// A wave instruction covers 64 / R consecutive quad rows (64 consecutive
+// records: coalesced 4-byte int8 or 16-byte float values and 8-byte offset
+// loads); lane l takes row l % R of quad rows G (w + W i) + l / R.  Each lane
+// issues the loads of U groups at once (quad rows clamped into the slab, so
+// every load is unconditional), then gathers their x values from LDS and
+// accumulates with fused multiply-adds into four partial sums; a clamped
+// load repeats a real record, so the terms of quad rows past the slab are
+// dropped whole (their x may be inf or NaN).  Partial sums meet across the
+// lane groups (shuffles) and the waves (LDS); an int8 row's sum is scaled
+// once at the end.  The sum is reassociated, so this kernel serves the fast
+// mode only.  (Cutting the slabs of the longest rows into parts combined by
+// a second launch measured slower overall on the decode shapes; combining
+// inside the launch would need device-scope fences between workgroups, which
+// write back and invalidate each XCD's L2.)
+template <bool I8, int R, int W, int U>
+__global__ __launch_bounds__(64 * W) void k_spmv_chain_fast(
+    int K, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm, const void* __restrict__ vals,
+    const uint32_t* __restrict__ cols, const float* __restrict__ rs, const float* __restrict__ x, int ldx,
+    float* __restrict__ y, int64_t ldy_r, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    constexpr int G = 64 / R;  // quad rows per wave instruction
+    extern __shared__ float4 dyn[];
+    float* const xs = reinterpret_cast<float*>(dyn);  // [K + 1]
+    __shared__ float part[W][R];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.x;
+    const int qb = q0[s], nq = q0[s + 1] - qb;
+    stage_x<64 * W>(xs, x, K, ldx, tid);
+    __syncthreads();
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const char* xb = reinterpret_cast<const char*>(xs);
+    const int r = lane % R, sub = lane / R;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
+        const int g0 = b + sub;
+        ValT v[U];
+        uint2 c[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t at = (int64_t)(qb + min(g0 + G * W * u, nq - 1)) * R + r;
+            v[u] = V[at];
+            c[u] = Cl[at];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float x0 = *reinterpret_cast<const float*>(xb + (c[u].x & 0xFFFF));
+            const float x1 = *reinterpret_cast<const float*>(xb + (c[u].x >> 16));
+            const float x2 = *reinterpret_cast<const float*>(xb + (c[u].y & 0xFFFF));
+            const float x3 = *reinterpret_cast<const float*>(xb + (c[u].y >> 16));
+            float w0, w1, w2, w3;
+            if constexpr (I8) {
+                w0 = (float)(int8_t)(v[u] & 0xFF);
+                w1 = (float)(int8_t)((v[u] >> 8) & 0xFF);
+                w2 = (float)(int8_t)((v[u] >> 16) & 0xFF);
+                w3 = (float)(int8_t)(v[u] >> 24);
+            } else {
+                w0 = v[u].x; w1 = v[u].y; w2 = v[u].z; w3 = v[u].w;
+            }
+            const bool in = g0 + G * W * u < nq;
+            a0 = in ? __builtin_fmaf(w0, x0, a0) : a0;
+            a1 = in ? __builtin_fmaf(w1, x1, a1) : a1;
+            a2 = in ? __builtin_fmaf(w2, x2, a2) : a2;
+            a3 = in ? __builtin_fmaf(w3, x3, a3) : a3;
+        }
+    }
+    float acc = (a0 + a1) + (a2 + a3);
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane < R) part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= R) return;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) sum += part[w][lane];
+    const int row = perm[s * R + lane];
+    if (row >= 0) {
+        if constexpr (I8) sum *= rs[row];
+        const int64_t f = (int64_t)row * ldy_r;
+        y[f] = bias_add(sum, f, bias, c_size, beta, act);
+    }
+}
+
+constexpr int kChainFastW = 16, kChainFastU = 4;  // measured best of W 4..16, U 4..16 on the decode shapes
+
+template <bool I8, int R>
+void launch_chain_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, float* Y, int64_t ldy_r,
+                       const float* bias, int64_t c_size, float beta, int act) {
+    const size_t lds = (size_t)(W->K + 1) * 4;  // K < kChainXMax: at most 64 KiB
+    hipLaunchKernelGGL((k_spmv_chain_fast<I8, R, kChainFastW, kChainFastU>), dim3((unsigned)W->chain_nslab),
+                       dim3(64 * kChainFastW), lds, ctx->stream, (int)W->K, W->chain_q0, W->chain_perm, W->chain_val,
+                       static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size,
+                       beta, act);
 }
 
 // At[k, i] = RN(alpha * A[i, k]) for A rows x cols (At cols x rows).
@@ -1157,7 +1272,11 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     hipStream_t s = ctx->stream;
     const void* val = W->val;
     const float* rs = W->row_scale;
-    if (FAST && N <= 8) {
+    if (FAST && N == 1 && W->chain_q0 != nullptr && W->chain_xlds && ldx < INT32_MAX) {
+        if (W->chain_rows == 16) launch_chain_fast<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+        else if (W->chain_rows == 32) launch_chain_fast<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+        else launch_chain_fast<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (FAST && N <= 8) {
         const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
         const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);
         // a workgroup per row when rows are long (mean of at least 2048

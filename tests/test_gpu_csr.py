@@ -271,6 +271,71 @@ def test_column_slice_layout_cases(ctx):
     assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
 
 
+def test_fast_vector_row_chains(ctx):
+    """The fast N = 1 kernel over the row-chain copy (x staged in LDS): long
+    rows (16- and 32-row slabs), short rows (64-row slabs), int8 with row
+    scales and fp32, empty rows (slabs with no quad rows), a strided x, NaN
+    and infinity in x, and the fused bias / activation epilogue.  Normwise
+    within 1e-5 of the strict oracle; NaN exactly where the oracle has it."""
+    import torch
+
+    rng = np.random.default_rng(12)
+
+    def check(Y, R):
+        assert np.array_equal(np.isnan(Y), np.isnan(R))
+        fin = ~np.isnan(R)
+        scale = np.abs(R[fin & np.isfinite(R)]).max()
+        assert np.array_equal(Y[np.isinf(R)], R[np.isinf(R)])
+        ok = fin & np.isfinite(R)
+        assert np.abs(Y[ok] - R[ok]).max() <= 1e-5 * scale
+
+    cases = [("int8 long rows", 600, 6000, True), ("fp32 long rows", 700, 5000, False),
+             ("int8 short rows", 3000, 2000, True)]
+    for name, M, K, i8 in cases:
+        dens = 0.3 if "long" in name else 0.1
+        if i8:
+            ip, ix, q, sc = workloads.csr_int8_lognormal(M, K, dens, 0.5, 0.02, seed=M)
+            vals = workloads.dequant_rows(ip, q, sc)
+        else:
+            ip, ix, vals = workloads.csr_lognormal_rows(M, K, dens, 0.5, 0.02, seed=M)
+        cnt = np.diff(ip)
+        cnt[-40:] = 0  # empty rows: sorted last, a slab of them holds no quad rows
+        mask = np.ones(len(ix), bool)
+        for r in range(M - 40, M):
+            mask[ip[r]:ip[r + 1]] = False
+        ix, vals = ix[mask], vals[mask]
+        if i8:
+            q = q[mask]
+        ip = np.zeros(M + 1, np.int64)
+        np.cumsum(cnt, out=ip[1:])
+        W = ctx.csr_upload(M, K, ip, ix, q, row_scales=sc) if i8 else ctx.csr_upload(M, K, ip, ix, vals)
+        x = rng.standard_normal(K).astype(np.float32)
+        say(f"fast row chains: {name} M={M} K={K}")
+        check(W.spmm(x, mode="fast"), O.orc_csr_spmv(M, K, ip, ix, vals, x))
+        x2 = x.copy()
+        x2[ix[0]] = np.nan
+        x2[ix[len(ix) // 2]] = np.inf
+        check(W.spmm(x2, mode="fast"), O.orc_csr_spmv(M, K, ip, ix, vals, x2))
+        # strided x (every third element of a device buffer), relu epilogue
+        dX = torch.from_numpy(np.repeat(x[:, None], 3, axis=1)).cuda()
+        dY = torch.zeros((M, 2), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        W.spmm_dev(dX.data_ptr(), 1, dY.data_ptr(), ldx=3, ldy=2, mode="fast", relu=True)
+        ctx.synchronize()
+        R = O.orc_csr_spmv(M, K, ip, ix, vals, x)
+        check(dY[:, 0].cpu().numpy(), relu_ref(R))
+        assert not dY[:, 1].cpu().numpy().any()
+        W.free()
+    # 32-row slabs: long rows and more rows than 16-row slabs for 4 per CU
+    M, K = 16 * 4 * torch.cuda.get_device_properties(0).multi_processor_count + 300, 1300
+    ip, ix, vals = workloads.csr_uniform(M, K, 0.85, 0.02, seed=77)
+    W = ctx.csr_upload(M, K, ip, ix, vals)
+    x = rng.standard_normal(K).astype(np.float32)
+    say(f"fast row chains: 32-row slabs M={M} K={K}")
+    check(W.spmm(x, mode="fast"), O.orc_csr_spmv(M, K, ip, ix, vals, x))
+    W.free()
+
+
 def test_strict_vector_row_chains(ctx):
     """The strict N = 1 kernel over the row-sorted chain copy: row lengths at
     the 4-step and 256-step chunk edges and past several chunks, empty rows,
