@@ -189,17 +189,17 @@ void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vect
                  const void* vals, hipStream_t s) {
     const int64_t M = w->M;
     if (M == 0 || w->nnz == 0) return;
-    // Slab height: the staged-x kernel's per-CU LDS traffic and producer work
-    // per step grow with the rows a workgroup folds, so matrices with long
-    // rows and few of them use 16-row slabs (which also spreads them over
-    // every CU).  Short rows (mean under 1024) keep 64-row slabs: there every
-    // workgroup's start (staging x, the first loads) outweighs the fold, and
-    // fewer workgroups start fewer times.  The global-gather kernel takes 64.
+    // Slab height: the staged-x kernels' per-CU traffic and producer work per
+    // step grow with the rows a workgroup folds, so the slabs are as short as
+    // keeps about four workgroups per CU: 16 rows (which also lets the strict
+    // 2 <= N <= 8 kernel run), else 32, else 64.  Measured on 4096 x 4096 at
+    // 10 %: strict N = 1 8.47 -> 7.52 us and strict N = 2 / 8 69 / 57 ->
+    // 9.9 / 12.7 us against 64-row slabs (which this rule used to keep for
+    // short rows while x was staged one load at a time).  The global-gather
+    // kernel takes 64.
     w->chain_xlds = w->K < pfr::kChainXMax;
     const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
-    const bool long_rows = w->nnz >= 1024 * M;
-    const int64_t R = !w->chain_xlds || !long_rows ? pfr::kChainRows
-                                                    : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
+    const int64_t R = !w->chain_xlds ? pfr::kChainRows : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
     w->chain_rows = (int32_t)R;
     std::vector<int32_t> order((size_t)M);
     std::iota(order.begin(), order.end(), 0);

@@ -273,10 +273,11 @@ def test_column_slice_layout_cases(ctx):
 
 def test_fast_vector_row_chains(ctx):
     """The fast N = 1 kernel over the row-chain copy (x staged in LDS): long
-    rows (16- and 32-row slabs), short rows (64-row slabs), int8 with row
-    scales and fp32, empty rows (slabs with no quad rows), a strided x, NaN
-    and infinity in x, and the fused bias / activation epilogue.  Normwise
-    within 1e-5 of the strict oracle; NaN exactly where the oracle has it."""
+    and short rows, int8 with row scales and fp32, empty rows (slabs with no
+    quad rows), a strided x, NaN and infinity in x, and the fused bias /
+    activation epilogue; then matrices with enough rows for 32- and 64-row
+    slabs, strict (bit-exact) and fast.  Fast results are normwise within
+    1e-5 of the strict oracle, with NaN exactly where the oracle has it."""
     import torch
 
     rng = np.random.default_rng(12)
@@ -326,14 +327,18 @@ def test_fast_vector_row_chains(ctx):
         check(dY[:, 0].cpu().numpy(), relu_ref(R))
         assert not dY[:, 1].cpu().numpy().any()
         W.free()
-    # 32-row slabs: long rows and more rows than 16-row slabs for 4 per CU
-    M, K = 16 * 4 * torch.cuda.get_device_properties(0).multi_processor_count + 300, 1300
-    ip, ix, vals = workloads.csr_uniform(M, K, 0.85, 0.02, seed=77)
-    W = ctx.csr_upload(M, K, ip, ix, vals)
-    x = rng.standard_normal(K).astype(np.float32)
-    say(f"fast row chains: 32-row slabs M={M} K={K}")
-    check(W.spmm(x, mode="fast"), O.orc_csr_spmv(M, K, ip, ix, vals, x))
-    W.free()
+    # 32- and 64-row slabs: more rows than 16-row (32-row) slabs give four
+    # workgroups per CU
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    for rows, M, K, dens in ((32, 16 * 4 * cu + 300, 1300, 0.3), (64, 32 * 4 * cu + 100, 300, 0.05)):
+        ip, ix, vals = workloads.csr_uniform(M, K, dens, 0.02, seed=rows)
+        W = ctx.csr_upload(M, K, ip, ix, vals)
+        x = rng.standard_normal(K).astype(np.float32)
+        say(f"row chains: {rows}-row slabs M={M} K={K}")
+        R = O.orc_csr_spmv(M, K, ip, ix, vals, x)
+        check(W.spmm(x, mode="fast"), R)
+        assert bits_equal(W.spmm(x), R)
+        W.free()
 
 
 def test_strict_vector_row_chains(ctx):
