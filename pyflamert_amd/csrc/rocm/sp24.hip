@@ -16,6 +16,7 @@
 // The weight is packed once, on the host, into that register order, so each
 // lane fetches its A operand with one 16-byte load.
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -379,23 +380,32 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     if constexpr (OUT == PFR_SP24_OUT_I8) {
         // requantise into an LDS tile [256][128] (stage 0), then store 16-byte row pieces
         char* tile = st0;
+        // ZERO: no zero-point correction and output zero point 0 (the usual
+        // symmetric case; the terms it drops are exact identities), chosen
+        // once per workgroup so the per-output work shrinks
+        auto requant = [&](auto zero) {
+            constexpr bool ZERO = decltype(zero)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
-                const int m = (int)(mb0 * 16) + ml;
-                const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
+                for (int r = 0; r < 4; ++r) {
+                    const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
+                    const int m = (int)(mb0 * 16) + ml;
+                    const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float f = (float)exact(acc[i][j][r], rsv[i][r]) * sab;
-                    const float prod = f * inv_out;
-                    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
-                    q = q < -128 ? -128 : (q > 127 ? 127 : q);
-                    tile[ml * 128 + wn * 64 + 16 * j + c] = (char)q;
+                    for (int j = 0; j < 4; ++j) {
+                        const int32_t a = ZERO ? acc[i][j][r] : exact(acc[i][j][r], rsv[i][r]);
+                        const float prod = ((float)a * sab) * inv_out;
+                        int32_t q = pfr::f2i_trunc_x86(roundf(prod));
+                        if constexpr (!ZERO) q = (int32_t)((uint32_t)q + (uint32_t)out_zp);
+                        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+                        tile[ml * 128 + wn * 64 + 16 * j + c] = (char)q;
+                    }
                 }
             }
-        }
+        };
+        if (zcorr == 0 && out_zp == 0) requant(std::true_type{});
+        else requant(std::false_type{});
         __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
         __builtin_amdgcn_s_barrier();
 #pragma unroll
