@@ -113,6 +113,41 @@ __global__ __launch_bounds__(256) void k_nm_mask(const float* __restrict__ w, in
     for (int i = 0; i < len; ++i) mask[base + i] = (kept >> i) & 1u ? 1.0f : 0.0f;
 }
 
+// 2:4 over whole groups of 16-byte aligned data: the heap select above
+// worked out for keep = 2 of 4, with the same comparator (|a| > |b|, false
+// for NaN), so every tie goes the same way.  Making the two-element heap
+// leaves the smaller of elements 0 and 1 at the root (element 1 when
+// neither is greater); each later element greater than the root replaces it,
+// and the new root is that element when the other kept one is greater than
+// it, else the other kept one.  One float4 in and one out per thread.
+__global__ __launch_bounds__(256) void k_nm24(const float4* __restrict__ w, int64_t groups,
+                                              float4* __restrict__ mask) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= groups) return;
+    const float4 v = w[g];
+    const float mg[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
+    const bool first = mg[1] > mg[0];
+    int root = first ? 0 : 1, other = first ? 1 : 0;
+    float mr = first ? mg[0] : mg[1], mo = first ? mg[1] : mg[0];
+#pragma unroll
+    for (int i = 2; i < 4; ++i) {
+        if (mg[i] > mr) {
+            if (mo > mg[i]) {
+                root = i;
+                mr = mg[i];
+            } else {
+                root = other;
+                mr = mo;
+                other = i;
+                mo = mg[i];
+            }
+        }
+    }
+    const uint32_t kept = (1u << root) | (1u << other);
+    mask[g] = make_float4(kept & 1u ? 1.0f : 0.0f, kept & 2u ? 1.0f : 0.0f, kept & 4u ? 1.0f : 0.0f,
+                          kept & 8u ? 1.0f : 0.0f);
+}
+
 // ---- magnitude --------------------------------------------------------------
 
 // Selection state, in scratch: hist[256], then the words below, then the
@@ -327,8 +362,19 @@ void nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, floa
     if (total == 0) return;
     pfr::require(w && mask, "null w/mask");
     const int64_t groups = (total + m - 1) / m;
-    hipLaunchKernelGGL(k_nm_mask, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, ctx->stream, w, total, n,
-                       m, groups, mask);
+    const bool a16 = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(mask)) & 15) == 0;
+    if (n == 2 && m == 4 && a16 && total >= 4) {
+        // whole groups vectorised; a partial last group through the general kernel
+        const int64_t full = total / 4;
+        hipLaunchKernelGGL(k_nm24, dim3((unsigned)((full + 255) / 256)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const float4*>(w), full, reinterpret_cast<float4*>(mask));
+        if (total > full * 4)
+            hipLaunchKernelGGL(k_nm_mask, dim3(1), dim3(256), 0, ctx->stream, w + full * 4, total - full * 4, n, m,
+                               (int64_t)1, mask + full * 4);
+    } else {
+        hipLaunchKernelGGL(k_nm_mask, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, ctx->stream, w, total,
+                           n, m, groups, mask);
+    }
     PFR_HIP(hipGetLastError());
 }
 
