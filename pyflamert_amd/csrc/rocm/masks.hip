@@ -22,8 +22,11 @@
 //   positions, then every later position that compares ahead of the heap
 //   top replaces it) followed by a sort of the heap, which does not change
 //   the kept set.  One thread runs that heap select on its group's indices.
+#include <algorithm>
 #include <cmath>
 #include <vector>
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -150,10 +153,10 @@ __global__ __launch_bounds__(256) void k_nm24(const float4* __restrict__ w, int6
 
 // ---- magnitude --------------------------------------------------------------
 
-// Selection state, in scratch: hist[256], then the words below, then the
-// per-block tie counts and their exclusive prefix.
+// Selection state, in scratch, followed by the per-block tie counts (then
+// their exclusive prefix), the per-block counts of keys at or below the
+// threshold, and the histogram blocks' rows of 256 counts.
 struct MagState {
-    uint32_t hist[256];
     uint32_t prefix;   // high bits of the threshold found so far
     uint32_t pad;
     uint64_t k;        // rank still to find among keys matching the prefix
@@ -162,7 +165,6 @@ struct MagState {
 };
 
 __global__ __launch_bounds__(256) void k_mag_init(MagState* st, uint64_t k, uint64_t target) {
-    st->hist[threadIdx.x] = 0;
     if (threadIdx.x == 0) {
         st->prefix = 0;
         st->k = k;
@@ -171,86 +173,162 @@ __global__ __launch_bounds__(256) void k_mag_init(MagState* st, uint64_t k, uint
     }
 }
 
+// The 16 keys a thread owns from `start` (consecutive elements): four
+// 16-byte loads when VEC (w 16-byte aligned) and all 16 lie below n, else
+// one element at a time; keys past n are 0 (and `valid` says how many).
+template <bool VEC>
+__device__ __forceinline__ int load_keys16(const float* __restrict__ w, int64_t n, int64_t start, uint32_t* keys) {
+    if (VEC && start + kMaskPerThread <= n) {
+        const float4* w4 = reinterpret_cast<const float4*>(w + start);
+#pragma unroll
+        for (int j = 0; j < kMaskPerThread / 4; ++j) {
+            const float4 v = w4[j];
+            keys[4 * j] = mag_bits(v.x);
+            keys[4 * j + 1] = mag_bits(v.y);
+            keys[4 * j + 2] = mag_bits(v.z);
+            keys[4 * j + 3] = mag_bits(v.w);
+        }
+        return kMaskPerThread;
+    }
+    int valid = 0;
+#pragma unroll
+    for (int i = 0; i < kMaskPerThread; ++i) {
+        const int64_t e = start + i;
+        keys[i] = e < n ? mag_bits(w[e]) : 0u;
+        valid += e < n;
+    }
+    return valid;
+}
+
 // Histogram of digit `pass` (bits 31-8*pass .. 24-8*pass) over keys whose
 // higher bits equal the prefix.
+template <bool VEC>
 __global__ __launch_bounds__(kMaskThreads) void k_mag_hist(const float* __restrict__ w, int64_t n, int pass,
-                                                            MagState* __restrict__ st) {
-    __shared__ uint32_t h[256];
-    h[threadIdx.x] = 0;
+                                                            const MagState* __restrict__ st, int64_t nchunks,
+                                                            uint32_t* __restrict__ part) {
+    // 32 sub-histograms, lane l counting into copy l % 32, rows 257 words
+    // apart: the first pass bins by exponent, where a wave's keys share a
+    // few bins, and with one copy per half-wave lane those atomics neither
+    // collide nor share a bank
+    constexpr int kCopies = 32, kPitch = 257;
+    __shared__ uint32_t h[kCopies * kPitch];
+#pragma unroll
+    for (int c = 0; c < kCopies; ++c) h[c * kPitch + threadIdx.x] = 0;
     __syncthreads();
     const int shift = 24 - 8 * pass;
     const uint32_t prefix = st->prefix;
-    const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock;
-    for (int i = 0; i < kMaskPerThread; ++i) {
-        const int64_t e = start + (int64_t)i * kMaskThreads + threadIdx.x;
-        if (e < n) {
-            const uint32_t key = mag_bits(w[e]);
-            const bool match = pass == 0 || (key >> (shift + 8)) == prefix;
-            if (match) atomicAdd(&h[(key >> shift) & 255u], 1u);
+    uint32_t* hc = h + (threadIdx.x & (kCopies - 1)) * kPitch;
+    for (int64_t chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
+        const int64_t start = chunk * kMaskPerBlock + (int64_t)threadIdx.x * kMaskPerThread;
+        uint32_t keys[kMaskPerThread];
+        const int valid = load_keys16<VEC>(w, n, start, keys);
+#pragma unroll
+        for (int i = 0; i < kMaskPerThread; ++i) {
+            const bool match = i < valid && (pass == 0 || (keys[i] >> (shift + 8)) == prefix);
+            if (match) atomicAdd(&hc[(keys[i] >> shift) & 255u], 1u);
         }
     }
     __syncthreads();
-    if (h[threadIdx.x]) atomicAdd(&st->hist[threadIdx.x], h[threadIdx.x]);
+    uint32_t tot = 0;
+#pragma unroll
+    for (int c = 0; c < kCopies; ++c) tot += h[c * kPitch + threadIdx.x];
+    // the block's row of counts (plain stores: global atomics on 256
+    // addresses from every block serialise)
+    part[(int64_t)blockIdx.x * 256 + threadIdx.x] = tot;
 }
 
-// One block: the bucket holding rank k, then the histogram cleared for the
-// next pass.
-__global__ __launch_bounds__(256) void k_mag_pick(MagState* st) {
+// One block of 1024 threads: the histogram (the sum of the hist blocks'
+// rows: thread q * 256 + t adds rows q, q + 4, ... of bin t, sixteen loads
+// in flight), then, in the first 256 threads, the bucket holding rank k.
+__global__ __launch_bounds__(1024) void k_mag_pick(MagState* st, const uint32_t* __restrict__ part, int64_t nrows) {
     __shared__ uint64_t cum[256];
-    const int t = threadIdx.x;
-    cum[t] = st->hist[t];
+    __shared__ uint64_t quarter[4][256];
+    const int t = threadIdx.x & 255, qd = threadIdx.x >> 8;
+    uint64_t sum = 0;
+    for (int64_t r0 = qd; r0 < nrows; r0 += 4 * 16) {
+        uint32_t v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int64_t r = r0 + 4 * i;
+            v[i] = r < nrows ? part[r * 256 + t] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum += v[i];
+    }
+    quarter[qd][t] = sum;
+    __syncthreads();
+    // every thread stays for the barriers; the first 256 do the scan
+    const bool lead = qd == 0;
+    if (lead) cum[t] = quarter[0][t] + quarter[1][t] + quarter[2][t] + quarter[3][t];
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
-        const uint64_t v = t >= off ? cum[t - off] : 0;
+        const uint64_t v = lead && t >= off ? cum[t - off] : 0;
         __syncthreads();
-        cum[t] += v;
+        if (lead) cum[t] += v;
         __syncthreads();
     }
     const uint64_t k = st->k;
-    const uint64_t before = t ? cum[t - 1] : 0;
-    const bool here = before <= k && k < cum[t];
+    const uint64_t before = lead && t ? cum[t - 1] : 0;
+    const bool here = lead && before <= k && k < cum[t];
     __syncthreads();
     if (here) {
         st->prefix = (st->prefix << 8) | (uint32_t)t;
         st->k = k - before;
     }
-    st->hist[t] = 0;
 }
 
 // Per block: keys equal to the threshold (in the block's flat range) and,
 // across blocks, keys at or below it.
+template <bool VEC>
 __global__ __launch_bounds__(kMaskThreads) void k_mag_count(const float* __restrict__ w, int64_t n,
-                                                             MagState* __restrict__ st, uint32_t* __restrict__ ties) {
+                                                             const MagState* __restrict__ st,
+                                                             uint32_t* __restrict__ ties, uint32_t* __restrict__ les) {
     __shared__ uint32_t s_tie, s_le;
     if (threadIdx.x == 0) s_tie = s_le = 0;
     __syncthreads();
     const uint32_t thr = st->prefix;
     const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock + (int64_t)threadIdx.x * kMaskPerThread;
+    uint32_t keys[kMaskPerThread];
+    const int valid = load_keys16<VEC>(w, n, start, keys);
     uint32_t tie = 0, le = 0;
+#pragma unroll
     for (int i = 0; i < kMaskPerThread; ++i) {
-        const int64_t e = start + i;
-        if (e < n) {
-            const uint32_t key = mag_bits(w[e]);
-            tie += key == thr;
-            le += key <= thr;
-        }
+        tie += i < valid && keys[i] == thr;
+        le += i < valid && keys[i] <= thr;
     }
-    if (tie) atomicAdd(&s_tie, tie);
-    if (le) atomicAdd(&s_le, le);
+    // one LDS atomic per wave, not per thread
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        tie += __shfl_xor(tie, o, 64);
+        le += __shfl_xor(le, o, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        if (tie) atomicAdd(&s_tie, tie);
+        if (le) atomicAdd(&s_le, le);
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         ties[blockIdx.x] = s_tie;
-        if (s_le) atomicAdd(reinterpret_cast<unsigned long long*>(&st->zeros), (unsigned long long)s_le);
+        les[blockIdx.x] = s_le;  // summed by k_mag_scan (one global atomic per block would serialise)
     }
 }
 
-// One block: exclusive prefix of the per-block tie counts, in place.
-__global__ __launch_bounds__(1024) void k_mag_scan(uint32_t* ties, int64_t nblocks) {
+// One block: exclusive prefix of the per-block tie counts, in place, and
+// the count of keys at or below the threshold (the sum of les).
+__global__ __launch_bounds__(1024) void k_mag_scan(uint32_t* ties, int64_t nblocks, const uint32_t* __restrict__ les,
+                                                   MagState* __restrict__ st) {
     __shared__ uint64_t part[1024];
-    __shared__ uint64_t carry;
+    __shared__ uint64_t carry, le_sum;
     const int t = threadIdx.x;
-    if (t == 0) carry = 0;
+    if (t == 0) carry = le_sum = 0;
     __syncthreads();
+    {
+        uint64_t mine = 0;
+        for (int64_t b = t; b < nblocks; b += 1024) mine += les[b];
+        atomicAdd(reinterpret_cast<unsigned long long*>(&le_sum), (unsigned long long)mine);
+    }
+    __syncthreads();
+    if (t == 0) st->zeros = le_sum;
     for (int64_t b0 = 0; b0 < nblocks; b0 += 1024) {
         const int64_t b = b0 + t;
         const uint64_t v = b < nblocks ? ties[b] : 0;
@@ -273,6 +351,7 @@ __global__ __launch_bounds__(1024) void k_mag_scan(uint32_t* ties, int64_t nbloc
 // mask = key > threshold, plus the first (zeros - target) threshold ties in
 // flat order.  Each thread owns 16 consecutive elements, so flat order is
 // (block, thread, element) order.
+template <bool VEC>
 __global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restrict__ w, int64_t n,
                                                              const MagState* __restrict__ st,
                                                              const uint32_t* __restrict__ tie_off,
@@ -284,13 +363,10 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restr
     const uint64_t restore = zeros > target ? zeros - target : 0;
     const int64_t start = (int64_t)blockIdx.x * kMaskPerBlock + (int64_t)t * kMaskPerThread;
     uint32_t keys[kMaskPerThread];
+    const int valid = load_keys16<VEC>(w, n, start, keys);
     uint32_t mine = 0;
 #pragma unroll
-    for (int i = 0; i < kMaskPerThread; ++i) {
-        const int64_t e = start + i;
-        keys[i] = e < n ? mag_bits(w[e]) : 0u;
-        mine += (e < n) && keys[i] == thr;
-    }
+    for (int i = 0; i < kMaskPerThread; ++i) mine += i < valid && keys[i] == thr;
     scan[t] = mine;
     __syncthreads();
     for (int off = 1; off < kMaskThreads; off <<= 1) {
@@ -300,16 +376,21 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restr
         __syncthreads();
     }
     uint64_t rank = (uint64_t)tie_off[blockIdx.x] + scan[t] - mine;
+    float v[kMaskPerThread];
 #pragma unroll
     for (int i = 0; i < kMaskPerThread; ++i) {
-        const int64_t e = start + i;
-        if (e >= n) break;
-        float v = keys[i] > thr ? 1.0f : 0.0f;
-        if (keys[i] == thr) {
-            if (rank < restore) v = 1.0f;
+        v[i] = keys[i] > thr ? 1.0f : 0.0f;
+        if (keys[i] == thr && i < valid) {
+            if (rank < restore) v[i] = 1.0f;
             ++rank;
         }
-        mask[e] = v;
+    }
+    if (VEC && valid == kMaskPerThread) {
+        float4* m4 = reinterpret_cast<float4*>(mask + start);
+#pragma unroll
+        for (int j = 0; j < kMaskPerThread / 4; ++j) m4[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    } else {
+        for (int i = 0; i < valid; ++i) mask[start + i] = v[i];
     }
 }
 
@@ -338,18 +419,31 @@ void magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float s, float*
     if (k > (uint64_t)(n - 1)) k = (uint64_t)(n - 1);
     const uint64_t target = (uint64_t)((float)n * s);
     const int64_t nblocks = (n + kMaskPerBlock - 1) / kMaskPerBlock;
-    char* scr = static_cast<char*>(ctx->scratch[4].ensure(sizeof(MagState) + 4 * (size_t)nblocks));
+    // histogram blocks: at most two per CU, each looping over chunks
+    const int64_t hblocks = std::min<int64_t>(nblocks, 2 * (int64_t)(ctx->num_cu > 0 ? ctx->num_cu : 256));
+    char* scr = static_cast<char*>(
+        ctx->scratch[4].ensure(sizeof(MagState) + 8 * (size_t)nblocks + 1024 * (size_t)hblocks));
     MagState* st = reinterpret_cast<MagState*>(scr);
     uint32_t* ties = reinterpret_cast<uint32_t*>(scr + sizeof(MagState));
+    uint32_t* les = ties + nblocks;
+    uint32_t* part = les + nblocks;  // [hblocks][256]
     hipStream_t q = ctx->stream;
+    const bool vec = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(mask)) & 15) == 0;
     hipLaunchKernelGGL(k_mag_init, dim3(1), dim3(256), 0, q, st, k, target);
-    for (int pass = 0; pass < 4; ++pass) {
-        hipLaunchKernelGGL(k_mag_hist, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, pass, st);
-        hipLaunchKernelGGL(k_mag_pick, dim3(1), dim3(256), 0, q, st);
-    }
-    hipLaunchKernelGGL(k_mag_count, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties);
-    hipLaunchKernelGGL(k_mag_scan, dim3(1), dim3(1024), 0, q, ties, nblocks);
-    hipLaunchKernelGGL(k_mag_write, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties, mask);
+    auto passes = [&](auto v) {
+        constexpr bool VEC = decltype(v)::value;
+        for (int pass = 0; pass < 4; ++pass) {
+            hipLaunchKernelGGL(k_mag_hist<VEC>, dim3((unsigned)hblocks), dim3(kMaskThreads), 0, q, w, n, pass, st,
+                               nblocks, part);
+            hipLaunchKernelGGL(k_mag_pick, dim3(1), dim3(1024), 0, q, st, part, hblocks);
+        }
+        hipLaunchKernelGGL(k_mag_count<VEC>, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties, les);
+        hipLaunchKernelGGL(k_mag_scan, dim3(1), dim3(1024), 0, q, ties, nblocks, les, st);
+        hipLaunchKernelGGL(k_mag_write<VEC>, dim3((unsigned)nblocks), dim3(kMaskThreads), 0, q, w, n, st, ties,
+                           mask);
+    };
+    if (vec) passes(std::true_type{});
+    else passes(std::false_type{});
     PFR_HIP(hipGetLastError());
 }
 
