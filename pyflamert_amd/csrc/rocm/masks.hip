@@ -314,38 +314,38 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_count(const float* __restr
 }
 
 // One block: exclusive prefix of the per-block tie counts, in place, and
-// the count of keys at or below the threshold (the sum of les).
+// the count of keys at or below the threshold (the sum of les).  Thread t
+// owns a contiguous run of the counts: its run's sum, one scan of the 1024
+// run sums, then the run's prefixes written back.
 __global__ __launch_bounds__(1024) void k_mag_scan(uint32_t* ties, int64_t nblocks, const uint32_t* __restrict__ les,
                                                    MagState* __restrict__ st) {
     __shared__ uint64_t part[1024];
-    __shared__ uint64_t carry, le_sum;
+    __shared__ unsigned long long le_sum;
     const int t = threadIdx.x;
-    if (t == 0) carry = le_sum = 0;
-    __syncthreads();
-    {
-        uint64_t mine = 0;
-        for (int64_t b = t; b < nblocks; b += 1024) mine += les[b];
-        atomicAdd(reinterpret_cast<unsigned long long*>(&le_sum), (unsigned long long)mine);
+    if (t == 0) le_sum = 0;
+    const int64_t per = (nblocks + 1023) / 1024;
+    const int64_t b0 = min<int64_t>(nblocks, t * per), b1 = min<int64_t>(nblocks, b0 + per);
+    uint64_t run = 0, le = 0;
+    for (int64_t b = b0; b < b1; ++b) {
+        run += ties[b];
+        le += les[b];
     }
+    part[t] = run;
     __syncthreads();
+    atomicAdd(&le_sum, (unsigned long long)le);
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan of the run sums
+        const uint64_t u = t >= off ? part[t - off] : 0;
+        __syncthreads();
+        part[t] += u;
+        __syncthreads();
+    }
+    uint64_t excl = part[t] - run;
+    for (int64_t b = b0; b < b1; ++b) {
+        const uint32_t v = ties[b];
+        ties[b] = (uint32_t)excl;  // ranks stay below 2^32 (n < 2^32)
+        excl += v;
+    }
     if (t == 0) st->zeros = le_sum;
-    for (int64_t b0 = 0; b0 < nblocks; b0 += 1024) {
-        const int64_t b = b0 + t;
-        const uint64_t v = b < nblocks ? ties[b] : 0;
-        part[t] = v;
-        __syncthreads();
-        for (int off = 1; off < 1024; off <<= 1) {
-            const uint64_t u = t >= off ? part[t - off] : 0;
-            __syncthreads();
-            part[t] += u;
-            __syncthreads();
-        }
-        const uint64_t excl = carry + part[t] - v;
-        __syncthreads();
-        if (b < nblocks) ties[b] = (uint32_t)excl;  // ranks stay below 2^32 (n < 2^32)
-        if (t == 1023) carry += part[1023];
-        __syncthreads();
-    }
 }
 
 // mask = key > threshold, plus the first (zeros - target) threshold ties in
