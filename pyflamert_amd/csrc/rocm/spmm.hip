@@ -903,6 +903,166 @@ void launch_chain_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t l
                        beta, act);
 }
 
+// Fast mode, 2 <= N <= 8, over the row-chain copy with X staged in LDS as
+// rows of eight floats (columns past N and row K zero; the record offsets,
+// 4 k bytes, become 32 k with a shift): one persistent workgroup of W waves
+// per CU stages X once and walks slabs blockIdx.x, blockIdx.x + gridDim.x,
+// ...  A wave instruction covers 64 / R consecutive quad rows as in
+// k_spmv_chain_fast; each of a record's four nonzeros reads its X row with
+// two 16-byte LDS reads and adds eight fused multiply-adds.  Quad rows past
+// the slab (clamped loads repeat a real record) are dropped whole.  Row sums
+// meet across the lane groups (shuffles) and the waves (LDS); an int8 row's
+// sums are scaled once at the end.  Fast mode only (reassociated sums).
+template <bool I8, int R, int W, int U, bool XV>
+__global__ __launch_bounds__(64 * W) void k_spmm_chain_fast8(
+    int K, int N, int nslab, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm,
+    const void* __restrict__ vals, const uint32_t* __restrict__ cols, const float* __restrict__ rs,
+    const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c,
+    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    constexpr int G = 64 / R, NT = 64 * W;
+    extern __shared__ float4 xs[];  // [(K + 1) * 2]: row k at xs[2k], xs[2k + 1]
+    __shared__ float part[W][R][9];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // stage X: eight 16-byte (XV) or 4-byte loads per thread in flight, clamped
+    const int nq4 = (K + 1) * 2;  // float4 slots
+    for (int e0 = 0; e0 < nq4; e0 += 8 * NT) {
+        float4 t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = min(e0 + tid + NT * i, nq4 - 1);
+            const int k = min(e >> 1, K - 1), c0 = (e & 1) * 4;
+            const float* xr = X + (int64_t)k * ldx;
+            if constexpr (XV) {
+                t[i] = *reinterpret_cast<const float4*>(xr + c0);
+            } else {
+                t[i].x = xr[min(c0, N - 1)];
+                t[i].y = xr[min(c0 + 1, N - 1)];
+                t[i].z = xr[min(c0 + 2, N - 1)];
+                t[i].w = xr[min(c0 + 3, N - 1)];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + tid + NT * i;
+            if (e < nq4) {
+                const int k = e >> 1, c0 = (e & 1) * 4;
+                float4 v = t[i];
+                if (k >= K) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (c0 >= N) v.x = 0.0f;
+                if (c0 + 1 >= N) v.y = 0.0f;
+                if (c0 + 2 >= N) v.z = 0.0f;
+                if (c0 + 3 >= N) v.w = 0.0f;
+                xs[e] = v;
+            }
+        }
+    }
+    __syncthreads();
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const char* xb = reinterpret_cast<const char*>(xs);
+    const int r = lane % R, sub = lane / R;
+    for (int s = blockIdx.x; s < nslab; s += gridDim.x) {
+        const int qb = q0[s], nq = q0[s + 1] - qb;
+        float acc[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
+            const int g0 = b + sub;
+            ValT v[U];
+            uint2 cc[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t at = (int64_t)(qb + min(g0 + G * W * u, nq - 1)) * R + r;
+                v[u] = V[at];
+                cc[u] = Cl[at];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool in = g0 + G * W * u < nq;
+                float w[4];
+                if constexpr (I8) {
+                    w[0] = (float)(int8_t)(v[u] & 0xFF);
+                    w[1] = (float)(int8_t)((v[u] >> 8) & 0xFF);
+                    w[2] = (float)(int8_t)((v[u] >> 16) & 0xFF);
+                    w[3] = (float)(int8_t)(v[u] >> 24);
+                } else {
+                    w[0] = v[u].x; w[1] = v[u].y; w[2] = v[u].z; w[3] = v[u].w;
+                }
+                const uint32_t off[4] = {cc[u].x & 0xFFFF, cc[u].x >> 16, cc[u].y & 0xFFFF, cc[u].y >> 16};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 lo = *reinterpret_cast<const float4*>(xb + (off[j] << 3));
+                    const float4 hi = *reinterpret_cast<const float4*>(xb + (off[j] << 3) + 16);
+                    if (in) {
+                        acc[0] = __builtin_fmaf(w[j], lo.x, acc[0]);
+                        acc[1] = __builtin_fmaf(w[j], lo.y, acc[1]);
+                        acc[2] = __builtin_fmaf(w[j], lo.z, acc[2]);
+                        acc[3] = __builtin_fmaf(w[j], lo.w, acc[3]);
+                        acc[4] = __builtin_fmaf(w[j], hi.x, acc[4]);
+                        acc[5] = __builtin_fmaf(w[j], hi.y, acc[5]);
+                        acc[6] = __builtin_fmaf(w[j], hi.z, acc[6]);
+                        acc[7] = __builtin_fmaf(w[j], hi.w, acc[7]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+#pragma unroll
+            for (int o = R; o < 64; o <<= 1) acc[c] += __shfl_xor(acc[c], o, 64);
+        }
+        if (lane < R) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) part[wave][lane][c] = acc[c];
+        }
+        __syncthreads();
+        if (tid < R * 8) {  // row tid / 8, column tid % 8
+            const int rr = tid >> 3, c = tid & 7;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; ++w) sum += part[w][rr][c];
+            const int row = perm[s * R + rr];
+            if (row >= 0 && c < N) {
+                if constexpr (I8) sum *= rs[row];
+                const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
+                Y[f] = bias_add(sum, f, bias, c_size, beta, act);
+            }
+        }
+        __syncthreads();  // part is rewritten for the next slab
+    }
+}
+
+constexpr int kChainFast8W = 16, kChainFast8U = 2;
+
+// LDS bytes of k_spmm_chain_fast8's X rows, or 0 when they do not fit.
+size_t chain_fast8_lds(int64_t K) {
+    const size_t x = (size_t)(K + 1) * 32;
+    const size_t part = sizeof(float) * kChainFast8W * 16 * 9;
+    return x + part <= 160 * 1024 ? x : 0;
+}
+
+template <bool I8, bool XV>
+void launch_chain_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
+                        int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
+    auto kern = k_spmm_chain_fast8<I8, 16, kChainFast8W, kChainFast8U, XV>;
+    const size_t lds = chain_fast8_lds(W->K);
+    // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
+    static uint64_t allowed = 0;  // bit d: done on device d (< 64)
+    const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
+    if (lds > 65536 && (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit))) {
+        PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)(160 * 1024 - sizeof(float) * kChainFast8W * 16 * 9)));
+        if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
+    }
+    const int grid = (int)std::min<int64_t>(W->chain_nslab, ctx->num_cu > 0 ? ctx->num_cu : 256);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kChainFast8W), lds, ctx->stream, (int)W->K, N,
+                       (int)W->chain_nslab, W->chain_q0, W->chain_perm, W->chain_val,
+                       static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, ldx, Y, ldy_r, ldy_c, bias,
+                       c_size, beta, act);
+}
+
 // At[k, i] = RN(alpha * A[i, k]) for A rows x cols (At cols x rows).
 __global__ __launch_bounds__(256) void k_transpose_scale(const float* __restrict__ A, int64_t rows,
                                                          int64_t cols, float alpha, int scale,
@@ -1276,6 +1436,12 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
         if (W->chain_rows == 16) launch_chain_fast<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else if (W->chain_rows == 32) launch_chain_fast<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else launch_chain_fast<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (FAST && N >= 2 && N <= 8 && W->chain_q0 != nullptr && W->chain_xlds && W->chain_rows == 16 &&
+               chain_fast8_lds(W->K) > 0 && ldx < INT32_MAX) {
+        if (N == 8 && ldx % 4 == 0 && aligned16(X))
+            launch_chain_fast8<I8, true>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        else
+            launch_chain_fast8<I8, false>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else if (FAST && N <= 8) {
         const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
         const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);

@@ -326,6 +326,13 @@ def test_fast_vector_row_chains(ctx):
         R = O.orc_csr_spmv(M, K, ip, ix, vals, x)
         check(dY[:, 0].cpu().numpy(), relu_ref(R))
         assert not dY[:, 1].cpu().numpy().any()
+        # 2 <= N <= 8 (X staged in LDS as rows of eight when K allows)
+        for N in (2, 5, 8):
+            X = rng.standard_normal((K, N)).astype(np.float32)
+            X[ix[1], N - 1] = np.nan
+            X[ix[len(ix) // 3], 0] = -np.inf
+            say(f"fast row chains: {name} N={N}")
+            check(W.spmm(X, mode="fast"), O.orc_csr_spmm(M, K, ip, ix, vals, X))
         W.free()
     # 32- and 64-row slabs: more rows than 16-row (32-row) slabs give four
     # workgroups per CU
