@@ -128,29 +128,55 @@ __global__ __launch_bounds__(kLnThreads) void k_layernorm_lds(const float* __res
     __syncthreads();
     if ((int)threadIdx.x < rows) {
         const float* row = lds + threadIdx.x * stride;
-        const int n4 = norm & ~3;
+        // in element order, 32 at a time: the next 32 are read from LDS into
+        // the other register set while the current 32 are added, so the
+        // dependent adds do not wait on each read
+        const int n32 = norm & ~31;
+        auto rd = [&](int i, float4* v) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const float4*>(row + i + 4 * k);
+        };
+        float4 va[8], vb[8];
         float mean = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < n4; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(row + i);
-            mean = mean + v.x;
-            mean = mean + v.y;
-            mean = mean + v.z;
-            mean = mean + v.w;
+        auto add_sum = [&](const float4* v) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                mean = mean + v[k].x;
+                mean = mean + v[k].y;
+                mean = mean + v[k].z;
+                mean = mean + v[k].w;
+            }
+        };
+        if (n32) rd(0, va);
+        for (int i = 0; i < n32; i += 64) {
+            if (i + 32 < n32) rd(i + 32, vb);
+            add_sum(va);
+            if (i + 32 >= n32) break;
+            if (i + 64 < n32) rd(i + 64, va);
+            add_sum(vb);
         }
-        for (int i = n4; i < norm; ++i) mean = mean + row[i];
+        for (int i = n32; i < norm; ++i) mean = mean + row[i];
         mean = mean / (float)norm;
         float var = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < n4; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(row + i);
-            const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
-            var = var + d0 * d0;
-            var = var + d1 * d1;
-            var = var + d2 * d2;
-            var = var + d3 * d3;
+        auto add_var = [&](const float4* v) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
+                var = var + d0 * d0;
+                var = var + d1 * d1;
+                var = var + d2 * d2;
+                var = var + d3 * d3;
+            }
+        };
+        if (n32) rd(0, va);
+        for (int i = 0; i < n32; i += 64) {
+            if (i + 32 < n32) rd(i + 32, vb);
+            add_var(va);
+            if (i + 32 >= n32) break;
+            if (i + 64 < n32) rd(i + 64, va);
+            add_var(vb);
         }
-        for (int i = n4; i < norm; ++i) {
+        for (int i = n32; i < norm; ++i) {
             const float d = row[i] - mean;
             var = var + d * d;
         }
