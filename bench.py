@@ -8,11 +8,16 @@ kernel launch over one batch, inputs already resident in HBM.  16 distinct
 (W, X, Y) copies rotate so the working set (~350 MB) exceeds the 256 MB
 Infinity Cache.
 
-Prints ONE JSON line.  `value` is effective GFLOP/s (2 * nnz * N per step);
-`roofline` prices the kernel's algorithmic bytes per launch against HBM
-(8 TB/s); `cpu_baseline` is the reference's own sparse_matmul (compiled from
-its sources) -- or the oracle port where that library is absent -- timed
-single-threaded on this host on the same input.
+Prints ONE JSON line.  `value` is effective GFLOP/s (2 * nnz * N per step).
+`roofline` prices the kernel against its binding ceiling: at N = 256 the
+product is fp32-compute-bound (39.3 flop per algorithmic byte, above the
+157.3 / 8 = 19.7 ridge), so `frac` is achieved TFLOP/s over the 157.3 TFLOP/s
+fp32 peak, with the HBM fraction of the algorithmic bytes and the strict
+(separate multiply and add) VALU ceiling beside it.  `cpu_baseline` is the
+reference's own sparse_matmul (compiled from its sources) -- or the oracle
+port where that library is absent -- timed on one pinned core of this host on
+the same input, with the CPU backend's dense cpu_matmul on the zero-filled
+weight ("CPU backend today") beside it.
 """
 import argparse
 import json
@@ -26,6 +31,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (packed FMA)
 STRICT_VALU_CEILING_TFLOPS = 39.3  # one non-packed fp32 op per lane per clock, 256 CUs x 64 lanes x 2.4 GHz
+FMA_VALU_CEILING_TFLOPS = 78.6     # one non-packed fp32 FMA (2 flops) per lane per clock
 INT8_DENSE_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (the 2:4 instruction doubles K per issue)
 M = K = 4096
 DENSITY = 0.1
@@ -485,7 +491,7 @@ def bench_sp24(ctx, args):
     q, s = workloads.sp24_int8_weight(M, K, seed=3)
     X = workloads.quantize_per_tensor(workloads.dense_normal((K, N), 1.0, seed=4), 0.05)
     sets = []
-    for _ in range(8):  # 8 x (22.5 MB values + 5.6 MB indices) > 256 MB cache
+    for _ in range(16):  # 16 x (22.5 MB values + 5.6 MB positions + 2.1 MB X + 5.6 MB Y) > 256 MB cache
         W = ctx.sp24_pack(q, s)
         dX = torch.from_numpy(X).cuda()
         dY = torch.empty((M, N), dtype=torch.int8, device="cuda")
@@ -522,6 +528,69 @@ def bench_sp24(ctx, args):
     for W, _, _ in sets:
         W.free()
     return res
+
+
+def host_cpu_info():
+    """CPU model (the `lscpu` "Model name", read from /proc/cpuinfo), the
+    online CPU count (`nproc` without affinity limits) and the cores this
+    process may run on."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count(), "affinity_cores": len(os.sched_getaffinity(0))}
+
+
+class pinned_core:
+    """Pins the calling thread (the one that runs the CPU kernels) to one
+    core for the duration, as `taskset -c <core>` would, without exec; the
+    previous affinity is restored on exit."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.core = min(self.saved)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+        return False
+
+
+def cpu_dense_today(ip, ix, v, X, budget_s):
+    """"CPU backend today": the reference's registered MatMul op (cpu_matmul,
+    math.cpp:268-374) on the dense zero-filled pruned weight, as the CPU
+    backend runs a pruned model now (every k, zeros included), one thread.
+    Median of >= 5 calls after one warm-up, within about budget_s seconds;
+    each call also builds the two input Tensors (a 64 MiB copy, a few ms)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    if not O.have_ref():
+        return None, None
+    N = X.shape[1]
+    Wd = np.zeros((M, K), np.float32)
+    Wd[np.repeat(np.arange(M), np.diff(ip)), ix] = v
+    Xc = np.ascontiguousarray(X)
+    t0 = time.perf_counter()
+    out = O.ref_op_f32("MatMul", [Wd, Xc])
+    t_one = time.perf_counter() - t0
+    reps = max(5, min(20, int(budget_s / max(t_one, 1e-3))))
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = O.ref_op_f32("MatMul", [Wd, Xc])
+        ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": round(2.0 * len(v) * N / med / 1e9, 3), "unit": "GFLOP/s (effective, 2 * nnz * N)",
+            "ms_per_call": round(med * 1e3, 2), "cores": 1,
+            "sample": f"reference MatMul op (cpu_matmul, math.cpp:268-374) compiled from its sources, on the "
+                      f"dense zero-filled W 4096x4096 x X 4096x{N}; median of {reps} calls after one warm-up"}, out
 
 
 def cpu_baseline(ip, ix, v, X, gpu_Y, budget_s):
@@ -604,8 +673,20 @@ def main():
     Xh = workloads.dense_normal((K, N_MAIN), 1.0, seed=2024)
 
     extra = {}
+    if not args.only_main:
+        # the other workloads first: the headline is timed on a GPU that has
+        # been busy (clocks up), with its own warm-up on top
+        extra["sp24_i8"] = bench_sp24(ctx, args)
+        extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
+        extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
+        extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)
+        extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
+        extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
+        extra["dynamic_int8_node_11008x4096x512"] = bench_dynamic_int8(ctx)
+        extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)
+
     results = {}
-    for N in ((N_MAIN,) if args.only_main else (N_MAIN, 64, 1)):
+    for N in ((N_MAIN,) if args.only_main else (64, 1, N_MAIN)):
         sets = []
         for s in range(N_SETS):
             W = ctx.csr_upload(M, K, ip, ix, v)
@@ -614,6 +695,11 @@ def main():
             sets.append((W, dX, dY))
         torch.cuda.synchronize()
         steps = args.steps if N == N_MAIN else max(200, args.steps // 4)
+        if N == N_MAIN and args.mode == "strict" and not args.only_main:
+            # the fused multiply-add form of the same product (within 1e-5
+            # normwise of the strict result, the fp32 tolerance)
+            msf = time_gpu(sets, N, max(200, steps // 4), args.warmup, "fast")
+            Yf = sets[0][2].cpu().numpy()
         ms = time_gpu(sets, N, steps, args.warmup, args.mode)
         Y0 = sets[0][2].cpu().numpy()
         byts = csr_bytes(nnz, M, K, N)
@@ -626,19 +712,17 @@ def main():
             "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "bytes_per_launch": byts,
             "flop_per_launch": flops,
+            "bound": "fp32 compute" if N == N_MAIN else "hbm",
         }
         log(f"N={N}: {ms * 1e3:.2f} us/launch  {extra[f'N{N}']}")
-        if N == N_MAIN and args.mode == "strict":
-            # the fused multiply-add form of the same product (within 1e-5
-            # normwise of the strict result, the fp32 tolerance)
-            msf = time_gpu(sets, N, max(200, steps // 4), args.warmup, "fast")
-            Yf = sets[0][2].cpu().numpy()
+        if N == N_MAIN and args.mode == "strict" and not args.only_main:
             err = float(np.abs(Yf - Y0).max() / np.abs(Y0).max())
             extra[f"N{N}_fast"] = {
                 "ms_per_launch": round(msf, 5),
                 "gflops": round(flops / (msf * 1e-3) / 1e9, 1),
                 "gbs": round(byts / (msf * 1e-3) / 1e9, 1),
                 "normwise_err_vs_strict": err,
+                "frac_of_fma_ceiling": round(flops / (msf * 1e-3) / 1e12 / FMA_VALU_CEILING_TFLOPS, 4),
             }
             log(f"N={N} fast: {msf * 1e3:.2f} us/launch  {extra[f'N{N}_fast']}")
         for W, _, _ in sets:
@@ -646,26 +730,25 @@ def main():
         del sets
         torch.cuda.empty_cache()
 
-    if not args.only_main:
-        extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)
-        extra["sp24_i8"] = bench_sp24(ctx, args)
-        extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
-        extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
-        extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)
-        extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
-        extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
-        extra["dynamic_int8_node_11008x4096x512"] = bench_dynamic_int8(ctx)
-
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)
     flops = 2.0 * nnz * N_MAIN
     gbs = byts / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
     cpu = None
     parity = None
     if not args.no_cpu:
-        log("CPU baseline ...")
-        cpu, exact = cpu_baseline(ip, ix, v, Xh, Y0, args.cpu_seconds)
+        log("CPU baseline (one pinned core) ...")
+        with pinned_core() as pin:
+            cpu, exact = cpu_baseline(ip, ix, v, Xh, Y0, args.cpu_seconds)
+            dense, dense_out = cpu_dense_today(ip, ix, v, Xh, args.cpu_seconds)
         parity = "bit-exact" if exact else "MISMATCH"
+        cpu["pinned_core"] = pin.core
+        cpu["host"] = host_cpu_info()
+        if dense is not None:
+            dense["bit_exact_vs_gpu"] = bool(np.array_equal(dense_out.view(np.uint32), Y0.view(np.uint32)))
+            cpu["cpu_backend_today"] = dense
+            log(f"CPU backend today (dense cpu_matmul): {dense}")
     out = {
         "metric": "effective GFLOP/s + HBM GB/s (% roofline) for pruned SpMM at 90% sparsity, 1 GPU",
         "value": round(flops / (ms * 1e-3) / 1e9, 2),
@@ -681,22 +764,26 @@ def main():
         "data": "synthetic (seeded numpy: W 10% uniform-random N(0,0.02), X N(0,1))",
         "config": {"workload": "fp32 CSR SpMM W[4096x4096] 90% sparse x X[4096x256]",
                    "nnz": nnz, "N": N_MAIN, "mode": args.mode, "buffer_sets": N_SETS},
+        # N = 256 is compute-bound (arithmetic intensity 39.3 flop/B against a
+        # ridge of 157.3 / 8 = 19.7), so the binding ceiling is the fp32 peak
         "roofline": {
-            "bound": "hbm",
-            "achieved": round(gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bound": "mfma",
+            "achieved": round(tflops, 3),
+            "peak": FP32_VALU_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / FP32_VALU_PEAK_TFLOPS, 4),
             "traffic": recorded_traffic(),
-        },
-        "compute": {
-            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-            "fp32_valu_peak_tflops": FP32_VALU_PEAK_TFLOPS,
-            "strict_valu_ceiling_tflops": STRICT_VALU_CEILING_TFLOPS,
-            "frac_of_strict_ceiling": round(flops / (ms * 1e-3) / 1e12 / STRICT_VALU_CEILING_TFLOPS, 4),
-            "note": "strict mode issues a separate v_mul_f32 and v_add_f32 per term (no FMA, no packed "
-                    "FP32), so each useful flop is one non-packed VALU lane-op: 256 CUs x 64 lanes x "
-                    "2.4 GHz = 39.3 TFLOP/s, 1/4 of the packed-FMA peak",
+            "note": "fp32 compute-bound: 157.3 TFLOP/s is MI355X's fp32 peak (matrix cores and packed-FMA "
+                    "vector issue alike); the kernel runs on the vector ALUs",
+            "hbm": {"achieved_gbs": round(gbs, 1), "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "algorithmic_bytes": byts},
+            "strict_ceiling": {
+                "tflops": STRICT_VALU_CEILING_TFLOPS,
+                "frac": round(tflops / STRICT_VALU_CEILING_TFLOPS, 4),
+                "note": "strict mode issues a separate v_mul_f32 and v_add_f32 per term (no FMA, no packed "
+                        "FP32), so each useful flop is one non-packed VALU lane-op: 256 CUs x 64 lanes x "
+                        "2.4 GHz = 39.3 TFLOP/s, 1/4 of the fp32 peak",
+            },
         },
         "parity": parity,
         "cpu_baseline": cpu,
