@@ -167,6 +167,22 @@ int pfr_gemm_csr_act_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
                          const float* C, int64_t c_size, float* Y, int mode,
                          int act);
 
+/* Allocation-free form of pfr_gemm_csr_act_dev.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results and errors, except that the copy of
+ * op(A)^T that the product reads (made when transA == 0 or alpha != 1) is
+ * staged in a fixed per-device workspace of 4,194,304 floats (16 MiB)
+ * instead of the context's grow-only buffer; K * Mb beyond that is
+ * PFR_ERR_INVALID_ARG, reported before anything is enqueued.  Calls no
+ * hipMalloc or hipFree.  Every call on a GPU shares that GPU's workspace:
+ * calls that overlap on one GPU (other streams or contexts) race; calls on
+ * one stream are ordered. */
+int pfr_gemm_csr_act_noalloc_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
+                                 int transA, const pfr_csr* BT, float alpha, float beta,
+                                 const float* C, int64_t c_size, float* Y, int mode,
+                                 int act);
+
 /* ---- 2:4 structured weights (sparse MFMA, gfx950 smfmac) ------------------- */
 
 /* Pack a dense M x K weight that is 2:4 sparse along K (every group of four

@@ -63,6 +63,7 @@ SIGNATURES = {
     "pfr_gemm_csr": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
     "pfr_gemm_csr_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT]),
     "pfr_gemm_csr_act_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT, _INT]),
+    "pfr_gemm_csr_act_noalloc_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT, _INT]),
     "pfr_sp24_pack": (_INT, [_P, _I64, _I64, _P, _INT, _P, _I64, _PP]),
     "pfr_sp24_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_INT)]),
     "pfr_sp24_free": (_INT, [_P]),

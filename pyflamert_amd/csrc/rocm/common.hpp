@@ -166,4 +166,7 @@ constexpr int kSellTail = 256;     // int4 after the last run, read by the uncon
 namespace pfr {
 // Makes ctx's device current (cheap when it already is).
 void bind(pfr_ctx* ctx);
+// Records, once per device, the workspace address of the allocation-free
+// Gemm entry; `device` must be current.
+void init_noalloc_workspace(int device);
 }  // namespace pfr

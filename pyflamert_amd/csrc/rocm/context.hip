@@ -46,6 +46,7 @@ int pfr_rocm_init(int device, pfr_ctx** out) {
         std::string arch = prop.gcnArchName;
         if (arch.rfind("gfx950", 0) != 0)
             throw pfr::Error(PFR_ERR_UNSUPPORTED, "kernels are built for gfx950, device is " + arch);
+        pfr::init_noalloc_workspace(device);
         auto* ctx = new pfr_ctx();
         ctx->device = device;
         ctx->num_cu = prop.multiProcessorCount;

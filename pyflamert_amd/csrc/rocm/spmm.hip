@@ -8,11 +8,21 @@
 #include <algorithm>
 #include <climits>
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "common.hpp"
 
 #pragma clang fp contract(off)
+
+// Workspace of the allocation-free Gemm entry (pfr_gemm_csr_act_noalloc_dev):
+// the transposed, alpha-scaled activation op(A)^T.  Every device the library
+// runs on holds one copy until the process ends.  In host code `scratch` is a
+// host-side stand-in, not a device address: host code uses only the per-device
+// address that init_noalloc_workspace records.
+constexpr int64_t kNoAllocFloats = int64_t(1) << 22;  // 16 MiB: K * Mb <= 4,194,304
+static __device__ __align__(256) float scratch[kNoAllocFloats];
 
 namespace {
 
@@ -1564,9 +1574,11 @@ void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t
     launch_spmm(ctx, W, X, N, ldx, Y, ldy, 1, nullptr, 0, 0.0f, mode == PFR_MODE_FAST, act);
 }
 
+// ws / ws_floats: a caller-provided workspace for op(A)^T (the
+// allocation-free entry); null uses the context's grow-only buffer.
 void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, const pfr_csr* BT,
               float alpha, float beta, const float* C, int64_t c_size, float* Y, int mode,
-              int act = PFR_ACT_NONE) {
+              int act = PFR_ACT_NONE, float* ws = nullptr, int64_t ws_floats = 0) {
     check_csr(BT);
     check_act(act);
     pfr::require(Mb >= 0 && Mb < INT32_MAX, "bad row count");
@@ -1583,10 +1595,17 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     // At = op(A)^T scaled by alpha: K x Mb, so each k row is contiguous.
     const float* At = A;
     hipStream_t s = ctx->stream;
+    auto tbuf = [&]() -> float* {
+        if (ws == nullptr) return static_cast<float*>(ctx->scratch[3].ensure(sizeof(float) * (size_t)(K * Mb)));
+        pfr::require(K * Mb <= ws_floats,
+                     "allocation-free Gemm: op(A) has K * Mb = " + std::to_string(K * Mb) +
+                         " elements, more than its workspace of " + std::to_string(ws_floats) + " floats");
+        return ws;
+    };
     if (K == 0) {
         // No terms: every output is +0 (+ bias); At is never read.
     } else if (!transA) {
-        float* t = static_cast<float*>(ctx->scratch[3].ensure(sizeof(float) * (size_t)(K * Mb)));
+        float* t = tbuf();
         dim3 grid((unsigned)((K + 63) / 64), (unsigned)((Mb + 63) / 64));
         pfr::require(grid.y < 65536u, "activation too tall for the transpose grid");
         if (Mb % 4 == 0 && K % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0)
@@ -1598,7 +1617,7 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
         PFR_HIP(hipGetLastError());
         At = t;
     } else if (alpha != 1.0f) {
-        float* t = static_cast<float*>(ctx->scratch[3].ensure(sizeof(float) * (size_t)(K * Mb)));
+        float* t = tbuf();
         const int64_t n = K * Mb;
         hipLaunchKernelGGL(k_scale, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, A, n, alpha, t);
         PFR_HIP(hipGetLastError());
@@ -1609,7 +1628,32 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     launch_spmm(ctx, BT, At, Mb, Mb, Y, 1, Nf, C, c_size, beta, mode == PFR_MODE_FAST, act);
 }
 
+std::mutex g_ws_mu;
+std::vector<float*> g_ws_ptr;  // device address of `scratch`, per device
+
+float* noalloc_workspace(int device) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    return device >= 0 && device < (int)g_ws_ptr.size() ? g_ws_ptr[(size_t)device] : nullptr;
+}
+
 }  // namespace
+
+namespace pfr {
+
+// Records the device address of `scratch` on `device`, which must be current;
+// once per device (the context's init calls it).
+void init_noalloc_workspace(int device) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (device < (int)g_ws_ptr.size() && g_ws_ptr[(size_t)device] != nullptr) return;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+        throw Error(PFR_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    if (device >= (int)g_ws_ptr.size()) g_ws_ptr.resize((size_t)device + 1, nullptr);
+    g_ws_ptr[(size_t)device] = static_cast<float*>(p);
+}
+
+}  // namespace pfr
 
 extern "C" {
 
@@ -1662,6 +1706,17 @@ int pfr_gemm_csr_act_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, in
     return pfr::guarded([&] {
         pfr::bind(ctx);
         gemm_dev(ctx, A, Mb, K, transA, BT, alpha, beta, C, c_size, Y, mode, act);
+    });
+}
+
+int pfr_gemm_csr_act_noalloc_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA,
+                                 const pfr_csr* BT, float alpha, float beta, const float* C,
+                                 int64_t c_size, float* Y, int mode, int act) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        float* ws = noalloc_workspace(ctx->device);
+        pfr::require(ws != nullptr, "allocation-free Gemm: no workspace address recorded for this device");
+        gemm_dev(ctx, A, Mb, K, transA, BT, alpha, beta, C, c_size, Y, mode, act, ws, kNoAllocFloats);
     });
 }
 

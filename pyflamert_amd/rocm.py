@@ -217,8 +217,15 @@ class Context:
         check(self._lib.pfr_nm_mask_dev(self.handle, w_ptr, total, int(n), int(m), mask_ptr))
 
     def gemm_csr_dev(self, A_ptr, Mb, K, BT, Y_ptr, alpha=1.0, beta=1.0, C_ptr=None, c_size=0,
-                     transA=False, mode="strict", relu=False, gelu=False):
-        if relu or gelu:
+                     transA=False, mode="strict", relu=False, gelu=False, noalloc=False):
+        """Device-pointer Gemm; noalloc=True calls the allocation-free entry
+        (pfr_gemm_csr_act_noalloc_dev: op(A)^T in the fixed per-device
+        workspace, K * Mb <= 4,194,304 when a copy is needed)."""
+        if noalloc:
+            act = _lib.ACT_GELU if gelu else _lib.ACT_RELU if relu else _lib.ACT_NONE
+            check(self._lib.pfr_gemm_csr_act_noalloc_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
+                                                         alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode], act))
+        elif relu or gelu:
             act = _lib.ACT_GELU if gelu else _lib.ACT_RELU
             check(self._lib.pfr_gemm_csr_act_dev(self.handle, A_ptr, Mb, K, int(bool(transA)), BT.handle,
                                                  alpha, beta, C_ptr, c_size, Y_ptr, _MODES[mode], act))
