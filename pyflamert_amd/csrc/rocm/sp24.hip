@@ -15,6 +15,7 @@
 //                               k 8*(l/16)+e, 8..15 = k 32+8*(l/16)+(e-8).
 // The weight is packed once, on the host, into that register order, so each
 // lane fetches its A operand with one 16-byte load.
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 #include <vector>
@@ -38,6 +39,7 @@ struct pfr_sp24 {
     void* a = nullptr;        // compressed values, [Mp/16][Kp/KT][64][16 B]
     uint32_t* idx = nullptr;  // [Mp/16][Kp/KT (int8) | Kp/128 (bf16)][64]
     float* w_scale = nullptr; // [M] (per-tensor scales expanded)
+    float w_scale_max = 0.0f; // the largest of them
     int32_t* row_sum = nullptr;  // int8: [Mp] sum over k of W[m, k] (the zero-point correction)
 };
 
@@ -75,6 +77,14 @@ bool pick2(IsNz nz, int* p0, int* p1) {
     *p0 = 0;
     *p1 = 1;
     return true;
+}
+
+template <int I, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < E) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, E>(f);
+    }
 }
 
 // ---- kernels ----------------------------------------------------------------
@@ -148,31 +158,41 @@ __global__ __launch_bounds__(256) void k_transpose_i8(const int8_t* __restrict__
     }
 }
 
-// int8 2:4 GEMM, 256 x 128 outputs per workgroup of eight waves in a 4 x 2
-// grid, each owning 64 rows x 64 columns (4 x 4 tiles of 16 x 16, two waves
-// per SIMD).  A k step is 128 wide; its operands live in one of four LDS
-// stages:
+// int8 2:4 GEMM, 256 x 128 outputs per workgroup of four waves, one per
+// SIMD, each owning 64 rows x all 128 columns (4 x 8 tiles of 16 x 16: 128
+// accumulator registers, so the wave runs alone on its SIMD with room for
+// two fragment sets).  A k step is 128 wide; its operands live in one of
+// four LDS stages:
 //   A values  [16 row blocks][64 lanes][16 B]   (the packed register order)
 //   A indices [16 row blocks][64 lanes] u32
 //   B         [128 columns][128 B]: the k bytes of one XT row, its 16-byte
 //             chunk c stored at position c ^ ((column >> 1) & 7), so the 16
 //             lanes of a ds_read_b128 group (16 consecutive columns, one
 //             chunk) hit 16 distinct 4-bank groups.
-// Stages are filled by direct-to-LDS loads (global_load_lds_dword[x4]: each
-// wave instruction writes its lanes' data contiguously) four steps ahead of
-// the MFMAs; each wave reads the next step's fragments into a second
-// register set while the MFMAs of the current step run; one barrier per
-// step.  nkt is a multiple of 4 (packed K is padded to 512), so the loop
-// unrolls over the four stages with each stage's address static, which lets
-// the compiler wait for only the oldest loads (vmcnt) instead of all of them.
-// The last four steps, peeled from the loop, have no stage left to load; they
-// issue the same loads with every lane pointed at one address (one 64-byte
-// request per instruction) into the stage just consumed, so the count of
-// loads per step stays fixed for the vmcnt waits.  (Any branch or select
-// around the loop's loads makes the compiler wait for all of them before
-// every LDS read.)
+// Per k step a workgroup fetches 36 KiB from global memory (16 KiB of A
+// values, 4 KiB of positions, 16 KiB of X), which at the ~56 B per clock a
+// CU's vector memory path delivers (measured with direct-to-LDS loads of
+// L2-resident data) is ~660 clocks against 512 clocks of MFMA work per SIMD;
+// each B fragment is read from LDS by the four waves and each A fragment by
+// one.  Measured per step (s_memtime inside the kernel, 11008 x 4096 x 512):
+// 1163 clocks with the weight streamed from HBM, 898 with it cache-resident;
+// the loads alone take 1229 (HBM) and 659 (L2), the MFMAs and fragment reads
+// alone 711: the step is bound by the operand loads, and with the weight in
+// HBM by their latency (four stages of 36 KiB are all the LDS holds).  Stages are filled by direct-to-LDS loads
+// (global_load_lds_dword[x4]: each wave instruction writes its lanes' data
+// contiguously) four steps ahead of the MFMAs; each wave reads the next
+// step's fragments into a second register set while the current step's
+// MFMAs run; one barrier per step.  nkt is a multiple of 4 (packed K is
+// padded to 512), so the loop unrolls over the four stages with each stage's
+// address static, which lets the compiler wait for only the oldest loads
+// (vmcnt) instead of all of them.  The last four steps, peeled from the
+// loop, have no stage left to load; they issue the same loads with every
+// lane pointed at one address (one 64-byte request per instruction) into the
+// stage just consumed, so the count of loads per step stays fixed for the
+// vmcnt waits.  (Any branch or select around the loop's loads makes the
+// compiler wait for all of them before every LDS read.)
 constexpr int kI8TileM = 256, kI8TileN = 128;
-constexpr int kI8Waves = 8, kI8Threads = 64 * kI8Waves;
+constexpr int kI8Waves = 4, kI8Threads = 64 * kI8Waves;
 constexpr int kLdsA = 16 * 64 * 16, kLdsI = 16 * 64 * 4, kLdsB = 128 * 128;
 constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 
@@ -189,6 +209,128 @@ constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 // chunk gives lane t the eight k values k0 .. k0+7 of column chunk + t.
 __device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((k >> 4) & 1) << 2); }
 
+// quantize_tensor's rounding and cast for an output zero point of 0
+// (quant_ops.cpp:42-47): q = clamp((int32_t)std::round(p), -128, 127) with
+// the x86 conversion (NaN and |p| >= 2^31 give INT32_MIN, so -128).
+// std::round(p) = trunc(p + copysign(0.5 - 2^-25, p)) for every float p:
+// the addend is the largest float below one half, so a fraction of exactly
+// one half still carries (the sum rounds up to the next integer) while the
+// largest fraction below one half does not; from 2^23 up every float is an
+// integer and the addend is below half an ulp.  The clamp runs in float
+// (exact on integers), and one select supplies the x86 value.
+// INRANGE: p is known finite with |p| < 2^31 (the host bounds |acc| * scale
+// * (1 / out_scale) for the whole launch), so the select is not needed.
+template <bool INRANGE>
+__device__ __forceinline__ int32_t round_clamp_i8(float p) {
+    const float r = __builtin_truncf(p + __builtin_copysignf(0.49999997f, p));
+    const float c = __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+    if constexpr (INRANGE) return (int32_t)c;
+    return (int32_t)(__builtin_fabsf(r) < 2147483648.0f ? c : -128.0f);
+}
+
+// The epilogue of the int8 2:4 GEMM: wave w of the workgroup holds the
+// accumulators of tile rows 64w .. 64w + 63 (row blocks 4w + i) x columns
+// 16j + c; tile is an LDS buffer of 256 x 128 bytes no longer in use.
+template <int OUT>
+__device__ __forceinline__ void sp24_i8_epilogue(
+    const v4i (&acc)[4][8], char* tile, int64_t mb0, int64_t n0, int M, int N, const float* __restrict__ ws,
+    float xs, float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec,
+    int32_t x_zp, int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
+    const int32_t* __restrict__ row_sum) {
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+    const int kb = l >> 4, c = l & 15;
+    const float xs_eff = xs_dev ? *xs_dev : xs;
+    const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
+    const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
+    // This lane's 16 rows: their scales (and row sums, for a zero-point
+    // correction) loaded together, from clamped rows, so the epilogue waits
+    // for one load latency rather than one per row.
+    float wsv[4][4];
+    uint32_t rsv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = min((int)(mb0 + w * 4 + i) * 16 + 4 * kb + r, M - 1);
+            if constexpr (OUT != PFR_SP24_OUT_I32) wsv[i][r] = ws[m];
+            rsv[i][r] = zcorr ? (uint32_t)row_sum[m] : 0u;
+        }
+    // the exact accumulator of a row (int32 wrap-around arithmetic; the true
+    // value is within int32 for K < 2^17)
+    auto exact = [&](int32_t a, uint32_t rs) { return (int32_t)((uint32_t)a - zcorr * rs); };
+    if constexpr (OUT == PFR_SP24_OUT_I8) {
+        // requantise into the LDS tile [256][128], then store 16-byte row pieces
+        // ZERO: no zero-point correction and output zero point 0 (the usual
+        // symmetric case; the terms it drops are exact identities), chosen
+        // once per workgroup so the per-output work shrinks
+        auto requant = [&](auto zero, auto inr) {
+            constexpr bool ZERO = decltype(zero)::value, INRANGE = decltype(inr)::value;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ml = (w * 4 + i) * 16 + 4 * kb + r;
+                    const int m = (int)(mb0 * 16) + ml;
+                    const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        int32_t q;
+                        if constexpr (ZERO) {
+                            q = round_clamp_i8<INRANGE>(((float)acc[i][j][r] * sab) * inv_out);
+                        } else {
+                            const float prod = ((float)exact(acc[i][j][r], rsv[i][r]) * sab) * inv_out;
+                            q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
+                            q = q < -128 ? -128 : (q > 127 ? 127 : q);
+                        }
+                        tile[ml * 128 + 16 * j + c] = (char)q;
+                    }
+                }
+            }
+        };
+        if (zcorr == 0 && out_zp == 0) {
+            if (inrange) requant(std::true_type{}, std::true_type{});
+            else requant(std::true_type{}, std::false_type{});
+        } else {
+            requant(std::false_type{}, std::false_type{});
+        }
+        __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // 256 rows x 8 pieces = 8 per thread
+            const int q16 = t + kI8Threads * i, ml = q16 >> 3, cc = q16 & 7;
+            const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
+            if (m >= M) continue;
+            int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
+            const char* src = tile + ml * 128 + 16 * cc;
+            if (yvec && n + 16 <= N) {
+                *reinterpret_cast<v4i*>(yr + n) = *reinterpret_cast<const v4i*>(src);
+            } else {
+                for (int b = 0; b < 16 && n + b < N; ++b) yr[n + b] = src[b];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = (int)(mb0 + w * 4 + i) * 16 + 4 * kb + r;
+                if (m >= M) continue;
+                float sab = 1.0f;
+                if constexpr (OUT == PFR_SP24_OUT_F32) sab = wsv[i][r] * xs_eff;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int64_t n = n0 + 16 * j + c;
+                    if (n >= N) continue;
+                    const int32_t v = exact(acc[i][j][r], rsv[i][r]);
+                    const int64_t o = (int64_t)m * ldy + n;
+                    if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
+                    else static_cast<float*>(Y)[o] = (float)v * sab;
+                }
+            }
+        }
+    }
+}
+
 // Activation zero point: acc = sum_k w[m, k] (x[k, n] - zp) =
 // sum_k w x - zp * row_sum[m], exact in int32.  A uint8 activation arrives
 // as x - 128 (sign bit flipped by k_flip_sign), so its correction uses
@@ -196,18 +338,17 @@ __device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((
 // from xs / x_zp or, when xs_dev / zp_dev are set, from device scalars (the
 // outputs of a DynamicQuantizeLinear on the same stream).
 template <int OUT, bool XROW>
-__global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
+__global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
     int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
     const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
-    float inv_out, int32_t out_zp, void* __restrict__ Y, int64_t ldy, int yvec, int ntn, int32_t x_zp,
-    int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
+    float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec, int ntn,
+    int32_t x_zp, int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
     const int32_t* __restrict__ row_sum) {
     __shared__ __attribute__((aligned(1024))) char st0[kStage];
     __shared__ __attribute__((aligned(1024))) char st1[kStage];
     __shared__ __attribute__((aligned(1024))) char st2[kStage];
     __shared__ __attribute__((aligned(1024))) char st3[kStage];
     const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
-    const int wm = w >> 1, wn = w & 1;
     const int kb = l >> 4, c = l & 15;
     int mt, nt;
     {
@@ -219,18 +360,17 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     }
     const int64_t mb0 = (int64_t)mt * (kI8TileM / 16);
     const int64_t n0 = (int64_t)nt * kI8TileN;
-    // per k step every wave issues six direct-to-LDS loads: A row blocks w
-    // and w + 8 (1 KiB each), index row blocks 2w and 2w + 1 (256 B each), and
-    // B runs w and w + 8 (8 rows of 128 B each, rows 8j .. 8j + 7 of run j)
-    constexpr int kLoads = 6;
+    // per k step every wave issues twelve direct-to-LDS loads: A row blocks
+    // w + 4i (1 KiB each), their index rows (256 B each), and B runs w + 4i
+    // (8 rows of 128 B each, rows 8j .. 8j + 7 of run j), i = 0..3
+    constexpr int kLoads = 12;
     const v4i* asrc = A + ((mb0 + w) * nkt) * 64 + l;
-    const int64_t a_rb8 = (int64_t)8 * nkt * 64;
-    const uint32_t* isrc = I + ((mb0 + 2 * w) * nkt) * 64 + l;
-    const int64_t i_rb1 = (int64_t)nkt * 64;
-    const v4i* bsrc[2];
+    const uint32_t* isrc = I + ((mb0 + w) * nkt) * 64 + l;
+    const int64_t rb4 = (int64_t)4 * nkt * 64;  // elements between row blocks w + 4i and w + 4i + 4
+    const v4i* bsrc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int n = 8 * (w + 8 * i) + (l >> 3);
+    for (int i = 0; i < 4; ++i) {
+        const int n = 8 * (w + 4 * i) + (l >> 3);
         if constexpr (XROW) {
             const int chunk = (l & 7) ^ xrow_swizzle(n);
             bsrc[i] = reinterpret_cast<const v4i*>(B + (int64_t)n * ldb + n0 + 16 * chunk);
@@ -242,28 +382,24 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     const int64_t b_step = XROW ? 128 * ldb / 16 : 8;  // v4i per k step
     auto issue = [&](char* st, int s) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(asrc + i * a_rb8 + (int64_t)s * 64, PFR_LDS(st + (w + 8 * i) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(isrc + i * i_rb1 + (int64_t)s * 64, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(asrc + i * rb4 + (int64_t)s * 64, PFR_LDS(st + (w + 4 * i) * 1024), 16,
+                                             0, 0);
+            __builtin_amdgcn_global_load_lds(isrc + i * rb4 + (int64_t)s * 64, PFR_LDS(st + kLdsA + (w + 4 * i) * 256),
+                                             4, 0, 0);
             __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * b_step,
-                                             PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 8 * i) * 128), 16, 0, 0);
+                                             PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 4 * i) * 128), 16, 0, 0);
+        }
     };
     // the tail's loads: the same instructions, every lane reading A[0]
     auto issue_tail = [&](char* st) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + (w + 8 * i) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + (2 * w + i) * 256), 4, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 8 * i) * 128), 16, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + (w + 4 * i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + (w + 4 * i) * 256), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 4 * i) * 128), 16, 0, 0);
+        }
     };
-    int boff_lo[4], boff_hi[4];  // XT form: the two 16-byte pieces of column n
     // X-row form: transpose read r of this lane starts at row
     // k_r = 16kb + 8(r & 1) + 64(r >> 1) + c/2, bytes 8(c % 2) of the chunk.
     // xrow_swizzle(k_r) is the same for all four reads (bits 1-2 of k_r come
@@ -271,73 +407,88 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     // and one swizzle serve them all.
     const int trk = kLdsA + kLdsI + (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
     const int trf = xrow_swizzle(16 * kb + (c >> 1));
-    if constexpr (!XROW) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = wn * 64 + 16 * j + c, sw = (n >> 1) & 7;
-            boff_lo[j] = kLdsA + kLdsI + n * 128 + 16 * (kb ^ sw);
-            boff_hi[j] = kLdsA + kLdsI + n * 128 + 16 * ((4 + kb) ^ sw);
-        }
-    }
-    v4i acc[4][4];
+    // XT form: the two 16-byte pieces of column n = 16j + c sit at chunks
+    // kb and 4 + kb of its row, swizzled by (n >> 1) & 7 = (c >> 1) for
+    // every j
+    const int xsw = (c >> 1) & 7;
+    const int bxt = kLdsA + kLdsI + c * 128;
+    v4i acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     struct Frag {
         v4i a[4];
         int ix[4];
-        v8i b[4];
+        v8i b[8];
     };
     auto fetch = [&](Frag& f, const char* st) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 8; ++j) {
             if constexpr (XROW) {
-                const int cj = wn * 4 + j;  // 16-column chunk of this fragment
                 v2i q[4];
-                const char* bp = st + trk + 16 * (cj ^ trf);
+                const char* bp = st + trk + 16 * (j ^ trf);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     q[r] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                         (__attribute__((address_space(3))) v2i*)(bp + 1024 * (r & 1) + 8192 * (r >> 1)));
                 f.b[j] = v8i{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
             } else {
-                const v4i lo = *reinterpret_cast<const v4i*>(st + boff_lo[j]);
-                const v4i hi = *reinterpret_cast<const v4i*>(st + boff_hi[j]);
+                const char* bp = st + bxt + j * 16 * 128;
+                const v4i lo = *reinterpret_cast<const v4i*>(bp + 16 * (kb ^ xsw));
+                const v4i hi = *reinterpret_cast<const v4i*>(bp + 16 * ((4 + kb) ^ xsw));
                 f.b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            f.a[i] = *reinterpret_cast<const v4i*>(st + ((wm * 4 + i) * 64 + l) * 16);
-            f.ix[i] = *reinterpret_cast<const int*>(st + kLdsA + ((wm * 4 + i) * 64 + l) * 4);
+            f.a[i] = *reinterpret_cast<const v4i*>(st + ((w * 4 + i) * 64 + l) * 16);
+            f.ix[i] = *reinterpret_cast<const int*>(st + kLdsA + ((w * 4 + i) * 64 + l) * 4);
         }
     };
     auto mma = [&](const Frag& f) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < 4; ++i)
                 acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(f.a[i], f.b[j], acc[i][j], f.ix[i], 0, 0);
     };
     // Step s: fragments of stage s are in registers (cur).  Wait for stage
-    // s+1's loads (vmcnt(12): stages s+2 and s+3 may still be in flight),
+    // s+1's loads (vmcnt(24): stages s+2 and s+3 may still be in flight),
     // barrier (every wave's stage s+1 loads have landed, and every wave has
     // read stage s's fragments, so its LDS buffer is free), start the loads
     // of stage s+4 into that buffer, read stage s+1's fragments into `nxt`
     // while the MFMAs run on `cur`.
-    // vmcnt(12) and lgkmcnt(0): this wave's fragment reads of the previous
+    // vmcnt(24) and lgkmcnt(0): this wave's fragment reads of the previous
     // step have completed before the barrier lets other waves refill a stage
     // (vmcnt holds 6 bits: low 4 in [3:0], high 2 in [15:14])
     auto vm_wait = [](int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (0 << 8); };
     Frag fa, fb;
+    // (sched_barrier keeps each step's loads, reads and MFMAs between its
+    // own barriers: otherwise the scheduler hoists the next step's wait and
+    // barrier above most of this step's MFMAs, exposing the fragment reads'
+    // latency)
     auto step = [&](Frag& cur, Frag& nxt, char* st_cur, char* st_next, int s) {
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(vm_wait(2 * kLoads));
         __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
         if (s >= 0) issue(st_cur, s + 4);  // s is a literal -1 in the peeled tail
         else issue_tail(st_cur);
         fetch(nxt, st_next);
         mma(cur);
+        // the step's 32 MFMAs each followed by one or two of its 40 fragment
+        // reads, and its 12 stage loads spread evenly among them: the LDS and
+        // vector-memory pipes stay busy while the MFMA pipe runs (a wave
+        // whose loads or reads are issued in a block stalls on their queues
+        // before the MFMAs behind them)
+        static_for<0, 32>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, g < 8 ? 2 : 1, 0);   // DS read
+            if constexpr ((g + 1) * 12 / 32 > g * 12 / 32)
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);           // VMEM read (stage load)
+        });
     };
     issue(st0, 0);
     issue(st1, 1);
@@ -358,90 +509,8 @@ __global__ __launch_bounds__(kI8Threads) void k_sp24_i8(
     step(fb, fa, st3, st0, -1);
     __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
     __builtin_amdgcn_s_barrier();
-    const float xs_eff = xs_dev ? *xs_dev : xs;
-    const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
-    const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
-    // This lane's 16 rows: their scales (and row sums, for a zero-point
-    // correction) loaded together, from clamped rows, so the epilogue waits
-    // for one load latency rather than one per row.
-    float wsv[4][4];
-    uint32_t rsv[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = min((int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r, M - 1);
-            if constexpr (OUT != PFR_SP24_OUT_I32) wsv[i][r] = ws[m];
-            rsv[i][r] = zcorr ? (uint32_t)row_sum[m] : 0u;
-        }
-    // the exact accumulator of a row (int32 wrap-around arithmetic; the true
-    // value is within int32 for K < 2^17)
-    auto exact = [&](int32_t a, uint32_t rs) { return (int32_t)((uint32_t)a - zcorr * rs); };
-    if constexpr (OUT == PFR_SP24_OUT_I8) {
-        // requantise into an LDS tile [256][128] (stage 0), then store 16-byte row pieces
-        char* tile = st0;
-        // ZERO: no zero-point correction and output zero point 0 (the usual
-        // symmetric case; the terms it drops are exact identities), chosen
-        // once per workgroup so the per-output work shrinks
-        auto requant = [&](auto zero) {
-            constexpr bool ZERO = decltype(zero)::value;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int ml = (wm * 4 + i) * 16 + 4 * kb + r;
-                    const int m = (int)(mb0 * 16) + ml;
-                    const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int32_t a = ZERO ? acc[i][j][r] : exact(acc[i][j][r], rsv[i][r]);
-                        const float prod = ((float)a * sab) * inv_out;
-                        int32_t q = pfr::f2i_trunc_x86(roundf(prod));
-                        if constexpr (!ZERO) q = (int32_t)((uint32_t)q + (uint32_t)out_zp);
-                        q = q < -128 ? -128 : (q > 127 ? 127 : q);
-                        tile[ml * 128 + wn * 64 + 16 * j + c] = (char)q;
-                    }
-                }
-            }
-        };
-        if (zcorr == 0 && out_zp == 0) requant(std::true_type{});
-        else requant(std::false_type{});
-        __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
-        __builtin_amdgcn_s_barrier();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // 256 rows x 8 pieces = 4 per thread
-            const int q16 = t + kI8Threads * i, ml = q16 >> 3, cc = q16 & 7;
-            const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
-            if (m >= M) continue;
-            int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
-            const char* src = tile + ml * 128 + 16 * cc;
-            if (yvec && n + 16 <= N) {
-                *reinterpret_cast<v4i*>(yr + n) = *reinterpret_cast<const v4i*>(src);
-            } else {
-                for (int b = 0; b < 16 && n + b < N; ++b) yr[n + b] = src[b];
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = (int)(mb0 + wm * 4 + i) * 16 + 4 * kb + r;
-                if (m >= M) continue;
-                float sab = 1.0f;
-                if constexpr (OUT == PFR_SP24_OUT_F32) sab = wsv[i][r] * xs_eff;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int64_t n = n0 + wn * 64 + 16 * j + c;
-                    if (n >= N) continue;
-                    const int32_t v = exact(acc[i][j][r], rsv[i][r]);
-                    const int64_t o = (int64_t)m * ldy + n;
-                    if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
-                    else static_cast<float*>(Y)[o] = (float)v * sab;
-                }
-            }
-        }
-    }
+    sp24_i8_epilogue<OUT>(acc, st0, mb0, n0, M, N, ws, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
+                          xs_dev, zp_dev, row_sum);
 }
 
 // bf16: 16x16x64 tiles, index words hold two k-tiles (abid 0 / 1).
@@ -658,9 +727,17 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     float inv_out = 1.0f;
     if (out_kind != PFR_SP24_OUT_I32 && !xs_dev)
         pfr::require(x_scale > 0.0f && std::isfinite(x_scale), "x_scale must be positive and finite");
+    int inrange = 0;
     if (out_kind == PFR_SP24_OUT_I8) {
         pfr::require(out_scale > 0.0f && std::isfinite(out_scale), "output scale must be positive and finite");
         inv_out = 1.0f / out_scale;  // quant_ops.cpp:41
+        // |acc| <= (K / 2 kept terms) * 128 * 128 per output; with that times
+        // the largest scale product below 2^30 every requantised value is
+        // finite and below 2^31 in magnitude (two float roundings add far
+        // less than the factor of two), so the kernel may clamp directly
+        if (!xs_dev && !x_u8 && x_zp == 0)
+            inrange = (double)W->Kp * 8192.0 * (double)W->w_scale_max * (double)x_scale * (double)inv_out <
+                      1073741824.0;
     }
     if (x_u8) {
         // the signed MFMA takes x - 128; the zero-point correction adds the 128 back
@@ -697,7 +774,7 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
 #define PFR_SP24_LAUNCH_X(OUTK, XR)                                                                             \
     hipLaunchKernelGGL((k_sp24_i8<OUTK, XR>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, B, ldb,    \
-                       (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, Y, ldy, yvec, ntn, x_zp,            \
+                       (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
 #define PFR_SP24_LAUNCH(OUTK)                      \
     do {                                           \
@@ -767,9 +844,10 @@ void gemm_qt_dev(pfr_ctx* ctx, const pfr_sp24* W, const uint8_t* X, bool x_u8, i
     else hipLaunchKernelGGL(k_pad_act<false>, dim3(pb), dim3(256), 0, ctx->stream, X, T, W->K, ldx, xt, Kp, Np);
     PFR_HIP(hipGetLastError());
     const int ntn = (int)(Np / kI8TileN);
+    const int nkt = (int)(Kp / 128);
     hipLaunchKernelGGL((k_sp24_i8<PFR_SP24_OUT_F32, false>), dim3((unsigned)(W->Mp / kI8TileM * ntn)),
-                       dim3(kI8Threads), 0, ctx->stream, (int)(Kp / 128), static_cast<const v4i*>(W->a), W->idx,
-                       reinterpret_cast<const int8_t*>(xt), Kp, (int)W->M, (int)T, W->w_scale, x_scale, 1.0f, 0,
+                       dim3(kI8Threads), 0, ctx->stream, nkt, static_cast<const v4i*>(W->a), W->idx,
+                       reinterpret_cast<const int8_t*>(xt), Kp, (int)W->M, (int)T, W->w_scale, x_scale, 1.0f, 0, 0,
                        static_cast<void*>(yp), ldyp, 1, ntn, x_zp, x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum);
     PFR_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_transpose_out, dim3((unsigned)((T + 63) / 64), (unsigned)((W->M + 63) / 64)), dim3(256), 0,
@@ -818,6 +896,7 @@ int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype d
         }
         pfr_sp24* w = dtype == PFR_I8 ? pack_i8(ctx, M, K, static_cast<const int8_t*>(W))
                                       : pack_bf16(ctx, M, K, static_cast<const uint16_t*>(W));
+        for (float v : scales) w->w_scale_max = std::max(w->w_scale_max, v);
         try {
             PFR_HIP(hipMalloc(&w->w_scale, sizeof(float) * (size_t)(M > 0 ? M : 1)));
             if (M) PFR_HIP(hipMemcpy(w->w_scale, scales.data(), sizeof(float) * (size_t)M, hipMemcpyHostToDevice));

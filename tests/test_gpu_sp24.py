@@ -78,6 +78,25 @@ def test_i8_rowscale_float_and_requant(ctx):
     assert np.array_equal(Q, O.orc_quantize(R, [np.float32(os_) / np.float32(7.0)], [0], O.I8))
 
 
+def test_i8_requant_extreme_scales(ctx):
+    """Requantisation at output scales that push RN(RN((float)acc * s) * (1 /
+    out_scale)) past the int32 range or to infinity: quantize_tensor's x86
+    cast gives INT32_MIN there, so -128 after the clamp, whatever the sign
+    (quant_ops.cpp:42-47); and at a scale where it stays in range.  Both
+    requant forms of the kernel (the bounded one and the one with the range
+    select) against the oracle."""
+    rng = np.random.default_rng(13)
+    M, K, N = 300, 1024, 128
+    q, s = rand_24_int8(rng, M, K)
+    X = O.orc_quantize(rng.standard_normal((K, N)).astype(np.float32), [0.05], [0], O.I8)
+    W = ctx.sp24_pack(q, s)
+    R = O.orc_quantized_matmul_rowscale(q, X, s, 0.05)
+    for os_ in (1e-30, 1e-12, 2e-9, 3e-6, 0.05, 7.0):
+        say(f"sp24 i8 requant out_scale={os_}")
+        Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=os_, out_zp=0)
+        assert np.array_equal(Q, O.orc_quantize(R, [np.float32(os_)], [0], O.I8)), os_
+
+
 def test_i8_golden(ctx, golden):
     """quantized_matmul with a per-tensor 2:4 weight and its requant, exactly
     as the compiled reference produced them."""
