@@ -151,6 +151,27 @@ struct pfr_csr {
     int32_t chain_rows = 64;
     bool chain_c16 = false;
     bool chain_xlds = false;
+    // nnz-balanced copy for the fast kernels with few columns (N <= 8): rows
+    // sorted by count (descending) and cut into groups of a power-of-two
+    // number of rows R <= 64, as many as keep the group's records under a
+    // common budget, so every workgroup streams about the same number of
+    // nonzeros.  K is cut into bal_nchunk chunks of bal_kcw columns (the
+    // last may be shorter; a chunk's X rows of eight floats fit LDS).  Group
+    // g is bal_meta[g] = {log2 R, first bal_perm entry, first record, quad
+    // rows}; its records run chunk by chunk, chunk c's starting at
+    // bal_cmeta[g * bal_nchunk + c].x and spanning .y quad rows: record
+    // (start + q * R + lane) holds entries 4q .. 4q+3 of the group's row
+    // `lane` among those with a column in chunk c, as values (as val) and
+    // uint16 byte offsets into x staged chunk by chunk with a zero after
+    // each chunk (at most 16384 floats): column k of chunk c at float
+    // c * (bal_kcw + 1) + k - c * bal_kcw; padding is value 0 at the chunk's
+    // zero, float c * (bal_kcw + 1) + bal_kcw.
+    int4* bal_meta = nullptr;      // [bal_ngroup]
+    int2* bal_cmeta = nullptr;     // [bal_ngroup * bal_nchunk]
+    int32_t* bal_perm = nullptr;   // [M] row of each group lane
+    void* bal_val = nullptr;
+    uint16_t* bal_col = nullptr;
+    int32_t bal_ngroup = 0, bal_nchunk = 0, bal_kcw = 0;
 };
 
 namespace pfr {
@@ -161,6 +182,7 @@ constexpr int kSellCols = 16;      // columns of X per workgroup slice
 constexpr int kSellMaxKC = 1024;   // K rows per LDS chunk (1024 x 64 B = 64 KiB, two buffers)
 constexpr int kSellStepPad = 8;    // steps per (slab, chunk) run are a multiple of this (one group)
 constexpr int kSellTail = 256;     // int4 after the last run, read by the unconditional prefetch
+constexpr int kBalChunk = 4096;    // most columns per chunk of the balanced copy
 }
 
 namespace pfr {

@@ -34,7 +34,8 @@ void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
                     (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0, (void*)w->col16,
-                    (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col})
+                    (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col, (void*)w->bal_meta,
+                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -226,6 +227,123 @@ void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vect
     }
 }
 
+// nnz-balanced copy (layout described at pfr_csr::bal_meta).  Rows are taken
+// longest first; each group takes as many rows as the largest power of two
+// (at most 64 and at most the rows left) whose padded records -- R times the
+// sum over chunks of its longest row there -- fit the budget, so a row
+// longer than the budget makes a group of its own.  The budget is the
+// smallest that keeps the group count at most two per CU.  Only for K whose
+// chunks, each with its zero slot, fit 64 KiB of staged x (the N = 1
+// kernel stages all of x at once).
+template <class V>
+void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
+               hipStream_t s) {
+    const int64_t M = w->M, K = w->K;
+    if (M == 0 || w->nnz == 0 || K == 0) return;
+    const int64_t C = (K + pfr::kBalChunk - 1) / pfr::kBalChunk, kcw = (K + C - 1) / C;
+    if (C * (kcw + 1) * 4 > 65536) return;
+    std::vector<int32_t> order((size_t)M);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+        return rowptr[a + 1] - rowptr[a] > rowptr[b + 1] - rowptr[b];
+    });
+    // quad rows per (sorted position, chunk)
+    std::vector<int32_t> qz((size_t)(M * C), 0);
+    for (int64_t i = 0; i < M; ++i) {
+        const int32_t r = order[(size_t)i];
+        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++qz[(size_t)(i * C + col[j] / kcw)];
+        for (int64_t c = 0; c < C; ++c) qz[(size_t)(i * C + c)] = (qz[(size_t)(i * C + c)] + 3) / 4;
+    }
+    auto recs = [&](int64_t i, int64_t p) {  // padded records of rows i .. i+p-1 as one group
+        int64_t t = 0;
+        for (int64_t c = 0; c < C; ++c) {
+            int32_t mx = 0;
+            for (int64_t j = i; j < i + p; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
+            t += mx;
+        }
+        return p * t;
+    };
+    auto cut = [&](int64_t budget, std::vector<int>* out) {
+        int64_t n = 0;
+        for (int64_t i = 0; i < M;) {
+            int p = 64;
+            while (p > 1 && (p > M - i || recs(i, p) > budget)) p >>= 1;
+            if (out) out->push_back(p);
+            i += p;
+            ++n;
+        }
+        return n;
+    };
+    const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
+    int64_t lo = 1, hi = 1;
+    for (int64_t i = 0; i < M; ++i) lo = std::max(lo, recs(i, 1));
+    hi = std::max<int64_t>(64 * lo, 1);
+    while (lo < hi) {  // smallest budget with at most two groups per CU
+        const int64_t mid = lo + (hi - lo) / 2;
+        if (cut(mid, nullptr) <= 2 * cu) hi = mid;
+        else lo = mid + 1;
+    }
+    std::vector<int> groups;
+    cut(lo, &groups);
+    const int64_t G = (int64_t)groups.size();
+    std::vector<int4> meta((size_t)G);
+    std::vector<int2> cmeta((size_t)(G * C));
+    int64_t nrec = 0;
+    {
+        int64_t i = 0;
+        for (int64_t g = 0; g < G; ++g) {
+            const int R = groups[(size_t)g];
+            for (int64_t c = 0; c < C; ++c) {
+                int32_t mx = 0;
+                for (int64_t j = i; j < i + R; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
+                cmeta[(size_t)(g * C + c)] = make_int2((int)nrec, mx);
+                nrec += (int64_t)R * mx;
+            }
+            i += R;
+        }
+    }
+    if ((nrec + 64) * 4 > INT32_MAX || G > INT32_MAX) return;
+    std::vector<int32_t> perm((size_t)M, -1);
+    // one spare record per lane after the last group
+    std::vector<V> v((size_t)((nrec + 64) * 4), V(0));
+    std::vector<uint16_t> cidx((size_t)((nrec + 64) * 4), (uint16_t)(4 * kcw));  // chunk 0's zero
+    std::vector<int32_t> k_in((size_t)C);
+    int64_t i = 0;
+    for (int64_t g = 0; g < G; ++g) {
+        const int R = groups[(size_t)g];
+        int lg = 0;
+        while ((1 << lg) < R) ++lg;
+        int nq = 0;
+        for (int64_t c = 0; c < C; ++c) {
+            const int2 cm = cmeta[(size_t)(g * C + c)];
+            nq += cm.y;
+            for (int64_t e = (int64_t)cm.x * 4; e < ((int64_t)cm.x + (int64_t)R * cm.y) * 4; ++e)
+                cidx[(size_t)e] = (uint16_t)(4 * (c * (kcw + 1) + kcw));  // padding: this chunk's zero
+        }
+        meta[(size_t)g] = make_int4(lg, (int)i, cmeta[(size_t)(g * C)].x, nq);
+        for (int lane = 0; lane < R; ++lane, ++i) {
+            const int32_t row = order[(size_t)i];
+            perm[(size_t)i] = row;
+            std::fill(k_in.begin(), k_in.end(), 0);
+            for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
+                const int64_t c = col[j] / kcw, k = k_in[(size_t)c]++;
+                const size_t at = (size_t)(((cmeta[(size_t)(g * C + c)].x + (k / 4) * R + lane) * 4) + k % 4);
+                v[at] = vals[j];
+                cidx[at] = (uint16_t)(4 * (c * (kcw + 1) + col[j] - c * kcw));
+            }
+        }
+    }
+    w->bal_meta = dev_alloc_copy(meta.data(), G, s);
+    w->bal_cmeta = dev_alloc_copy(cmeta.data(), G * C, s);
+    w->bal_perm = dev_alloc_copy(perm.data(), M, s);
+    w->bal_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
+    w->bal_col = dev_alloc_copy(cidx.data(), (int64_t)cidx.size(), s);
+    w->bal_ngroup = (int32_t)G;
+    w->bal_nchunk = (int32_t)C;
+    w->bal_kcw = (int32_t)kcw;
+    PFR_HIP(hipStreamSynchronize(s));  // the host vectors go out of scope here
+}
+
 pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
                const std::vector<int32_t>& col, const void* vals, pfr_dtype vdt,
                const float* row_scales) {
@@ -262,6 +380,8 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
         w->cols_sorted = sorted;
         if (vdt == PFR_F32) build_sell(w, rowptr, col, static_cast<const float*>(vals), s);
         build_chain(w, rowptr, col, vals, s);
+        if (vdt == PFR_F32) build_bal(w, rowptr, col, static_cast<const float*>(vals), s);
+        else build_bal(w, rowptr, col, static_cast<const int8_t*>(vals), s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {

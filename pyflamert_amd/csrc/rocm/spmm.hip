@@ -815,262 +815,372 @@ __global__ __launch_bounds__(256) void k_spmv_fast(
     }
 }
 
-// Fast mode, N = 1, over the row-chain copy with x staged in LDS (a zero at
-// index K for the padding steps): a workgroup of W waves per slab of R rows.
-// A wave instruction covers 64 / R consecutive quad rows (64 consecutive
-// records: coalesced 4-byte int8 or 16-byte float values and 8-byte offset
-// loads); lane l takes row l % R of quad rows G (w + W i) + l / R.  Each lane
-// issues the loads of U groups at once (quad rows clamped into the slab, so
-// every load is unconditional), then gathers their x values from LDS and
-// accumulates with fused multiply-adds into four partial sums; a clamped
-// load repeats a real record, so the terms of quad rows past the slab are
-// dropped whole (their x may be inf or NaN).  Partial sums meet across the
-// lane groups (shuffles) and the waves (LDS); an int8 row's sum is scaled
-// once at the end.  The sum is reassociated, so this kernel serves the fast
-// mode only.  (Cutting the slabs of the longest rows into parts combined by
-// a second launch measured slower overall on the decode shapes; combining
-// inside the launch would need device-scope fences between workgroups, which
-// write back and invalidate each XCD's L2.)
-template <bool I8, int R, int W, int U>
-__global__ __launch_bounds__(64 * W) void k_spmv_chain_fast(
-    int K, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm, const void* __restrict__ vals,
-    const uint32_t* __restrict__ cols, const float* __restrict__ rs, const float* __restrict__ x, int ldx,
-    float* __restrict__ y, int64_t ldy_r, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
-    constexpr int G = 64 / R;  // quad rows per wave instruction
-    extern __shared__ float4 dyn[];
-    float* const xs = reinterpret_cast<float*>(dyn);  // [K + 1]
-    __shared__ float part[W][R];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int s = blockIdx.x;
-    const int qb = q0[s], nq = q0[s + 1] - qb;
-    stage_x<64 * W>(xs, x, K, ldx, tid);
-    __syncthreads();
-    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
-    const ValT* V = static_cast<const ValT*>(vals);
-    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
-    const char* xb = reinterpret_cast<const char*>(xs);
-    const int r = lane % R, sub = lane / R;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
-        const int g0 = b + sub;
-        ValT v[U];
-        uint2 c[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t at = (int64_t)(qb + min(g0 + G * W * u, nq - 1)) * R + r;
-            v[u] = V[at];
-            c[u] = Cl[at];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float x0 = *reinterpret_cast<const float*>(xb + (c[u].x & 0xFFFF));
-            const float x1 = *reinterpret_cast<const float*>(xb + (c[u].x >> 16));
-            const float x2 = *reinterpret_cast<const float*>(xb + (c[u].y & 0xFFFF));
-            const float x3 = *reinterpret_cast<const float*>(xb + (c[u].y >> 16));
-            float w0, w1, w2, w3;
-            if constexpr (I8) {
-                w0 = (float)(int8_t)(v[u] & 0xFF);
-                w1 = (float)(int8_t)((v[u] >> 8) & 0xFF);
-                w2 = (float)(int8_t)((v[u] >> 16) & 0xFF);
-                w3 = (float)(int8_t)(v[u] >> 24);
-            } else {
-                w0 = v[u].x; w1 = v[u].y; w2 = v[u].z; w3 = v[u].w;
-            }
-            const bool in = g0 + G * W * u < nq;
-            a0 = in ? __builtin_fmaf(w0, x0, a0) : a0;
-            a1 = in ? __builtin_fmaf(w1, x1, a1) : a1;
-            a2 = in ? __builtin_fmaf(w2, x2, a2) : a2;
-            a3 = in ? __builtin_fmaf(w3, x3, a3) : a3;
-        }
+// x staged for the balanced copy's N = 1 kernel: chunk c of x (columns
+// c * kcw .. c * kcw + kcw - 1) at xs[c * (kcw + 1) ..], each chunk followed
+// by a zero (the slot its padding entries index), eight loads per thread in
+// flight.
+template <int NT>
+__device__ __forceinline__ void stage_x_chunks(float* xs, const float* __restrict__ x, int K, int64_t ldx, int nch,
+                                               int kcw, int tid) {
+    if (nch == 1) {  // kcw == K: x with its zero at K
+        stage_x<NT>(xs, x, K, ldx, tid);
+        return;
     }
-    float acc = (a0 + a1) + (a2 + a3);
-#pragma unroll
-    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane < R) part[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0 || lane >= R) return;
-    float sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) sum += part[w][lane];
-    const int row = perm[s * R + lane];
-    if (row >= 0) {
-        if constexpr (I8) sum *= rs[row];
-        const int64_t f = (int64_t)row * ldy_r;
-        y[f] = bias_add(sum, f, bias, c_size, beta, act);
-    }
-}
-
-constexpr int kChainFastW = 16, kChainFastU = 4;  // measured best of W 4..16, U 4..16 on the decode shapes
-
-template <bool I8, int R>
-void launch_chain_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, float* Y, int64_t ldy_r,
-                       const float* bias, int64_t c_size, float beta, int act) {
-    const size_t lds = (size_t)(W->K + 1) * 4;  // K < kChainXMax: at most 64 KiB
-    hipLaunchKernelGGL((k_spmv_chain_fast<I8, R, kChainFastW, kChainFastU>), dim3((unsigned)W->chain_nslab),
-                       dim3(64 * kChainFastW), lds, ctx->stream, (int)W->K, W->chain_q0, W->chain_perm, W->chain_val,
-                       static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size,
-                       beta, act);
-}
-
-// Fast mode, 2 <= N <= 8, over the row-chain copy with X staged in LDS as
-// rows of eight floats (columns past N and row K zero; the record offsets,
-// 4 k bytes, become 32 k with a shift): one persistent workgroup of W waves
-// per CU stages X once and walks slabs blockIdx.x, blockIdx.x + gridDim.x,
-// ...  A wave instruction covers 64 / R consecutive quad rows as in
-// k_spmv_chain_fast; each of a record's four nonzeros reads its X row with
-// two 16-byte LDS reads and adds eight fused multiply-adds.  Quad rows past
-// the slab (clamped loads repeat a real record) are dropped whole.  Row sums
-// meet across the lane groups (shuffles) and the waves (LDS); an int8 row's
-// sums are scaled once at the end.  Fast mode only (reassociated sums).
-template <bool I8, int R, int W, int U, bool XV>
-__global__ __launch_bounds__(64 * W) void k_spmm_chain_fast8(
-    int K, int N, int nslab, const int32_t* __restrict__ q0, const int32_t* __restrict__ perm,
-    const void* __restrict__ vals, const uint32_t* __restrict__ cols, const float* __restrict__ rs,
-    const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c,
-    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
-    constexpr int G = 64 / R, NT = 64 * W;
-    extern __shared__ float4 xs[];  // [(K + 1) * 2]: row k at xs[2k], xs[2k + 1]
-    __shared__ float part[W][R][9];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // stage X: eight 16-byte (XV) or 4-byte loads per thread in flight, clamped
-    const int nq4 = (K + 1) * 2;  // float4 slots
-    for (int e0 = 0; e0 < nq4; e0 += 8 * NT) {
-        float4 t[8];
+    const int n = nch * (kcw + 1);
+    // e / (kcw + 1) as a multiply-high by a rounded-up reciprocal: exact for
+    // e < 2^16 and a divisor below 2^13
+    const uint32_t inv = 0xFFFFFFFFu / (uint32_t)(kcw + 1) + 1u;
+    for (int e0 = 0; e0 < n; e0 += 8 * NT) {
+        float t[8];
+        int k[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int e = min(e0 + tid + NT * i, nq4 - 1);
-            const int k = min(e >> 1, K - 1), c0 = (e & 1) * 4;
-            const float* xr = X + (int64_t)k * ldx;
-            if constexpr (XV) {
-                t[i] = *reinterpret_cast<const float4*>(xr + c0);
-            } else {
-                t[i].x = xr[min(c0, N - 1)];
-                t[i].y = xr[min(c0 + 1, N - 1)];
-                t[i].z = xr[min(c0 + 2, N - 1)];
-                t[i].w = xr[min(c0 + 3, N - 1)];
-            }
+            const int e = e0 + tid + NT * i;
+            const int c = (int)__umulhi((uint32_t)e, inv);
+            const int o = e - c * (kcw + 1);
+            k[i] = o < kcw ? c * kcw + o : K;  // K: a zero slot (or past the end)
+            t[i] = x[(int64_t)min(k[i], K - 1) * ldx];
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int e = e0 + tid + NT * i;
-            if (e < nq4) {
-                const int k = e >> 1, c0 = (e & 1) * 4;
-                float4 v = t[i];
-                if (k >= K) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (c0 >= N) v.x = 0.0f;
-                if (c0 + 1 >= N) v.y = 0.0f;
-                if (c0 + 2 >= N) v.z = 0.0f;
-                if (c0 + 3 >= N) v.w = 0.0f;
-                xs[e] = v;
-            }
+            if (e < n) xs[e] = k[i] < K ? t[i] : 0.0f;
         }
     }
-    __syncthreads();
+}
+
+// Fast N = 1 SpMV over the nnz-balanced copy (layout at pfr_csr::bal_meta):
+// every group holds about the same number of nonzeros however skewed the
+// row lengths are (fixed 16-row slabs of rows sorted by length measured
+// 1.45x slower on 4096 x 11008 at 30 % with lognormal rows, whose slab of
+// the 16 longest rows holds 3.7x the mean slab's nonzeros).  A workgroup
+// stages x once and takes H groups, W / H waves each (the copy holds about
+// two groups per CU).  Within a group, R (the group's row count) is a power
+// of two up to 64 and G = 64 / R: one wave instruction covers G consecutive
+// quad rows (64 consecutive records: coalesced 4-byte int8 or 16-byte float
+// values and 8-byte offset loads); lane (r, sub) takes row r of quad rows
+// sub, sub + G, ... .  Each lane loads U records per batch, two batches in
+// flight (quad rows clamped into the group, so every load is unconditional;
+// a clamped record is folded as value 0 at a zero slot of x, as its own x
+// may be inf or NaN), gathers their x values from LDS and accumulates with
+// fused multiply-adds into four partial sums, reduced across the lanes of a
+// row (shuffles) and then across the group's waves (LDS); an int8 row's sum
+// is scaled once at the end.  The sum is reassociated, so this kernel serves
+// the fast mode only.  Measured on the int8 decode shapes at 30 % (4096²,
+// 11008 x 4096, 4096 x 11008): 6.1 / 11.0 / 12.8 us with U = 2 and two
+// batches in flight, 6.7 / 11.8 / 13.3 us with U = 4 and one.
+template <bool I8, int W, int H, int U>
+__global__ __launch_bounds__(64 * W) void k_spmv_bal_fast(
+    int K, int ngroup, int nch, int kcw, const int4* __restrict__ meta, const int32_t* __restrict__ perm,
+    const void* __restrict__ vals, const uint16_t* __restrict__ cols, const float* __restrict__ rs,
+    const float* __restrict__ x, int ldx, float* __restrict__ y, int64_t ldy_r, const float* __restrict__ bias,
+    int64_t c_size, float beta, int act) {
+    static_assert(W % H == 0, "waves split evenly over the groups");
+    constexpr int WG = W / H;  // waves per group
+    extern __shared__ float4 dyn[];
+    float* const xs = reinterpret_cast<float*>(dyn);  // [nch * (kcw + 1)]
+    __shared__ float part[W][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gw = wave % WG;                                   // the wave's index within its group
+    const int grp = (int)blockIdx.x * H + wave / WG;            // uniform
+    const bool live = grp < ngroup;                             // the last workgroup's second group may not exist
+    const int4 m = meta[min(grp, ngroup - 1)];
+    const int lgR = __builtin_amdgcn_readfirstlane(m.x), p0 = __builtin_amdgcn_readfirstlane(m.y);
+    const int rec0 = __builtin_amdgcn_readfirstlane(m.z), nq = live ? __builtin_amdgcn_readfirstlane(m.w) : 0;
+    const int R = 1 << lgR, G = 64 >> lgR;
     using ValT = typename std::conditional<I8, uint32_t, float4>::type;
     const ValT* V = static_cast<const ValT*>(vals);
     const uint2* Cl = reinterpret_cast<const uint2*>(cols);
     const char* xb = reinterpret_cast<const char*>(xs);
-    const int r = lane % R, sub = lane / R;
-    for (int s = blockIdx.x; s < nslab; s += gridDim.x) {
-        const int qb = q0[s], nq = q0[s + 1] - qb;
-        float acc[8];
+    const int r = lane & (R - 1), sub = lane >> lgR;
+    ValT va[U], vb[U];
+    uint2 ca[U], cb[U];
+    auto load = [&](ValT* v, uint2* cc, int b) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
-        for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
-            const int g0 = b + sub;
-            ValT v[U];
-            uint2 cc[U];
+        for (int u = 0; u < U; ++u) {
+            const int64_t at = rec0 + (int64_t)min(b + sub + G * WG * u, nq - 1) * R + r;
+            v[u] = V[at];
+            cc[u] = Cl[at];
+        }
+    };
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // records past the group (clamped loads repeat its last one) are folded
+    // as value 0 at the chunk-0 zero slot, with selects rather than branches
+    const uint32_t z2 = (uint32_t)(4 * kcw) * 0x10001u;
+    auto fold = [&](const ValT* v, const uint2* cc, int b) {
+        const int g0 = b + sub;
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int64_t at = (int64_t)(qb + min(g0 + G * W * u, nq - 1)) * R + r;
-                v[u] = V[at];
-                cc[u] = Cl[at];
+        for (int u = 0; u < U; ++u) {
+            const bool in = g0 + G * WG * u < nq;
+            const uint32_t cx = in ? cc[u].x : z2, cy = in ? cc[u].y : z2;
+            const float x0 = *reinterpret_cast<const float*>(xb + (cx & 0xFFFF));
+            const float x1 = *reinterpret_cast<const float*>(xb + (cx >> 16));
+            const float x2 = *reinterpret_cast<const float*>(xb + (cy & 0xFFFF));
+            const float x3 = *reinterpret_cast<const float*>(xb + (cy >> 16));
+            float w0, w1, w2, w3;
+            if constexpr (I8) {
+                const uint32_t q = in ? v[u] : 0u;
+                w0 = (float)(int8_t)(q & 0xFF);
+                w1 = (float)(int8_t)((q >> 8) & 0xFF);
+                w2 = (float)(int8_t)((q >> 16) & 0xFF);
+                w3 = (float)(int8_t)(q >> 24);
+            } else {
+                w0 = in ? v[u].x : 0.0f; w1 = in ? v[u].y : 0.0f;
+                w2 = in ? v[u].z : 0.0f; w3 = in ? v[u].w : 0.0f;
+            }
+            a0 = __builtin_fmaf(w0, x0, a0);
+            a1 = __builtin_fmaf(w1, x1, a1);
+            a2 = __builtin_fmaf(w2, x2, a2);
+            a3 = __builtin_fmaf(w3, x3, a3);
+        }
+    };
+    const int step = G * WG * U;
+    const int b0 = G * gw;
+    const int nit = b0 < nq ? (nq - b0 + step - 1) / step : 0;  // the wave's batches (uniform)
+    if (nit > 0) load(va, ca, b0);
+    stage_x_chunks<64 * W>(xs, x, K, ldx, nch, kcw, tid);
+    __syncthreads();
+    // two batches in flight: batch i + 1's loads are issued before batch i is
+    // folded (past the last batch they are clamped repeats, never folded)
+    int i = 0;
+    for (; i + 2 <= nit; i += 2) {
+        load(vb, cb, b0 + (i + 1) * step);
+        fold(va, ca, b0 + i * step);
+        load(va, ca, b0 + (i + 2) * step);
+        fold(vb, cb, b0 + (i + 1) * step);
+    }
+    if (i < nit) fold(va, ca, b0 + i * step);
+    float acc = (a0 + a1) + (a2 + a3);
+    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane < R) part[wave][lane] = acc;
+    __syncthreads();
+    if (gw != 0 || lane >= R || !live) return;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WG; ++w) sum += part[wave + w][lane];
+    const int row = perm[p0 + lane];
+    if constexpr (I8) sum *= rs[row];
+    const int64_t f = (int64_t)row * ldy_r;
+    y[f] = bias_add(sum, f, bias, c_size, beta, act);
+}
+
+constexpr int kBalFastH = 2, kBalFastU = 2;  // groups per workgroup, records per lane and batch
+
+template <bool I8>
+void launch_bal_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, float* Y, int64_t ldy_r,
+                     const float* bias, int64_t c_size, float beta, int act) {
+    const size_t lds = (size_t)W->bal_nchunk * (W->bal_kcw + 1) * 4;  // at most 64 KiB (checked at upload)
+    const unsigned grid = (unsigned)((W->bal_ngroup + kBalFastH - 1) / kBalFastH);
+    hipLaunchKernelGGL((k_spmv_bal_fast<I8, 16, kBalFastH, kBalFastU>), dim3(grid), dim3(64 * 16), lds, ctx->stream,
+                       (int)W->K, W->bal_ngroup, W->bal_nchunk, W->bal_kcw, W->bal_meta, W->bal_perm, W->bal_val,
+                       W->bal_col, W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
+}
+
+// Fast 2 <= N <= 8 over the nnz-balanced copy: a persistent workgroup takes
+// groups b and b + gridDim.x (the copy holds at most two per CU), and walks
+// K chunk by chunk: the chunk's X rows are staged in LDS as rows of eight
+// floats (kcw + 1 rows with the zero row, 32 B each), then both groups'
+// records of that chunk are folded into per-lane sums, eight columns at a
+// time (two 16-byte LDS reads and eight FMAs per nonzero).  The sums of a
+// row's lanes meet by shuffles, then across the waves in LDS (waves 8..15
+// add theirs to waves 0..7 first, so the order is fixed).
+template <bool I8, int W, int U, bool XV>
+__global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
+    int K, int N, int ngroup, int nch, int kcw, const int4* __restrict__ meta, const int2* __restrict__ cmeta,
+    const int32_t* __restrict__ perm, const void* __restrict__ vals, const uint16_t* __restrict__ cols,
+    const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r,
+    int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    static_assert(W == 16, "the cross-wave sum pairs waves w and w + 8");
+    constexpr int NT = 64 * W;
+    extern __shared__ float4 xs[];  // [(kcw + 1) * 2]: row k at xs[2k], xs[2k + 1]
+    __shared__ float part[8][64][8];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const char* xb = reinterpret_cast<const char*>(xs);
+    int gs[2], lg[2];
+    gs[0] = blockIdx.x;
+    gs[1] = blockIdx.x + gridDim.x;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) lg[gi] = gs[gi] < ngroup ? meta[gs[gi]].x : 0;
+    float acc[2][8];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[gi][c] = 0.0f;
+    ValT v[U];
+    uint2 cc[U];
+    auto load = [&](int rec0, int nq, int R, int G, int r, int sub, int b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t at = rec0 + (int64_t)min(b + sub + G * W * u, nq - 1) * R + r;
+            v[u] = V[at];
+            cc[u] = Cl[at];
+        }
+    };
+    // the output rows and scales of both groups (thread t < 8R writes row
+    // t / 8, column t % 8), loaded now rather than as dependent loads at the
+    // end
+    int orow[2] = {0, 0};
+    float oscale[2] = {1.0f, 1.0f};
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        if (gs[gi] < ngroup && tid < (8 << lg[gi])) {
+            orow[gi] = perm[meta[gs[gi]].y + (tid >> 3)];
+            if constexpr (I8) oscale[gi] = rs[orow[gi]];
+        }
+    }
+    // the first group's first records of chunk 0 are requested before X is
+    // staged, so their latency and the staging's overlap
+    bool pre = false;
+    if (gs[0] < ngroup) {
+        const int lgR = __builtin_amdgcn_readfirstlane(lg[0]), R = 1 << lgR, G = 64 >> lgR;
+        const int2 cm = cmeta[gs[0] * nch];
+        const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
+        if (G * wave < nq) {
+            load(rec0, nq, R, G, lane & (R - 1), lane >> lgR, G * wave);
+            pre = true;
+        }
+    }
+    for (int ch = 0; ch < nch; ++ch) {
+        // stage the chunk's X rows: eight 16-byte (XV) or 4-byte loads per
+        // thread in flight, clamped; rows past the chunk or K are zero
+        const int k0 = ch * kcw, nq4 = (kcw + 1) * 2;  // float4 slots
+        const uint32_t cbase = (uint32_t)(ch * (kcw + 1) * 4);  // byte offset of the chunk's first float
+        for (int e0 = 0; e0 < nq4; e0 += 8 * NT) {
+            float4 t[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = min(e0 + tid + NT * i, nq4 - 1);
+                const int k = min(k0 + (e >> 1), K - 1), c0 = (e & 1) * 4;
+                const float* xr = X + (int64_t)k * ldx;
+                if constexpr (XV) {
+                    t[i] = *reinterpret_cast<const float4*>(xr + c0);
+                } else {
+                    t[i].x = xr[min(c0, N - 1)];
+                    t[i].y = xr[min(c0 + 1, N - 1)];
+                    t[i].z = xr[min(c0 + 2, N - 1)];
+                    t[i].w = xr[min(c0 + 3, N - 1)];
+                }
             }
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool in = g0 + G * W * u < nq;
-                float w[4];
-                if constexpr (I8) {
-                    w[0] = (float)(int8_t)(v[u] & 0xFF);
-                    w[1] = (float)(int8_t)((v[u] >> 8) & 0xFF);
-                    w[2] = (float)(int8_t)((v[u] >> 16) & 0xFF);
-                    w[3] = (float)(int8_t)(v[u] >> 24);
-                } else {
-                    w[0] = v[u].x; w[1] = v[u].y; w[2] = v[u].z; w[3] = v[u].w;
+            for (int i = 0; i < 8; ++i) {
+                const int e = e0 + tid + NT * i;
+                if (e < nq4) {
+                    const int kk = e >> 1, c0 = (e & 1) * 4;
+                    float4 v = t[i];
+                    if (kk >= kcw || k0 + kk >= K) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (c0 >= N) v.x = 0.0f;
+                    if (c0 + 1 >= N) v.y = 0.0f;
+                    if (c0 + 2 >= N) v.z = 0.0f;
+                    if (c0 + 3 >= N) v.w = 0.0f;
+                    xs[e] = v;
                 }
-                const uint32_t off[4] = {cc[u].x & 0xFFFF, cc[u].x >> 16, cc[u].y & 0xFFFF, cc[u].y >> 16};
+            }
+        }
+        __syncthreads();
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 lo = *reinterpret_cast<const float4*>(xb + (off[j] << 3));
-                    const float4 hi = *reinterpret_cast<const float4*>(xb + (off[j] << 3) + 16);
-                    if (in) {
-                        acc[0] = __builtin_fmaf(w[j], lo.x, acc[0]);
-                        acc[1] = __builtin_fmaf(w[j], lo.y, acc[1]);
-                        acc[2] = __builtin_fmaf(w[j], lo.z, acc[2]);
-                        acc[3] = __builtin_fmaf(w[j], lo.w, acc[3]);
-                        acc[4] = __builtin_fmaf(w[j], hi.x, acc[4]);
-                        acc[5] = __builtin_fmaf(w[j], hi.y, acc[5]);
-                        acc[6] = __builtin_fmaf(w[j], hi.z, acc[6]);
-                        acc[7] = __builtin_fmaf(w[j], hi.w, acc[7]);
+        for (int gi = 0; gi < 2; ++gi) {
+            if (gs[gi] >= ngroup) continue;
+            const int lgR = __builtin_amdgcn_readfirstlane(lg[gi]), R = 1 << lgR, G = 64 >> lgR;
+            const int2 cm = cmeta[gs[gi] * nch + ch];
+            const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
+            const int r = lane & (R - 1), sub = lane >> lgR;
+            for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
+                const int g0 = b + sub;
+                if (!(gi == 0 && pre)) load(rec0, nq, R, G, r, sub, b);
+                if (gi == 0) pre = false;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const bool in = g0 + G * W * u < nq;
+                    float w[4];
+                    if constexpr (I8) {
+                        w[0] = (float)(int8_t)(v[u] & 0xFF);
+                        w[1] = (float)(int8_t)((v[u] >> 8) & 0xFF);
+                        w[2] = (float)(int8_t)((v[u] >> 16) & 0xFF);
+                        w[3] = (float)(int8_t)(v[u] >> 24);
+                    } else {
+                        w[0] = v[u].x; w[1] = v[u].y; w[2] = v[u].z; w[3] = v[u].w;
+                    }
+                    // offsets count x's floats from the start of chunk 0
+                    // (with the zeros after earlier chunks); a staged X row
+                    // is 32 bytes, eight times a float
+                    const uint32_t off[4] = {(cc[u].x & 0xFFFF) - cbase, (cc[u].x >> 16) - cbase,
+                                             (cc[u].y & 0xFFFF) - cbase, (cc[u].y >> 16) - cbase};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float4 lo = *reinterpret_cast<const float4*>(xb + (off[j] << 3));
+                        const float4 hi = *reinterpret_cast<const float4*>(xb + (off[j] << 3) + 16);
+                        if (in) {
+                            acc[gi][0] = __builtin_fmaf(w[j], lo.x, acc[gi][0]);
+                            acc[gi][1] = __builtin_fmaf(w[j], lo.y, acc[gi][1]);
+                            acc[gi][2] = __builtin_fmaf(w[j], lo.z, acc[gi][2]);
+                            acc[gi][3] = __builtin_fmaf(w[j], lo.w, acc[gi][3]);
+                            acc[gi][4] = __builtin_fmaf(w[j], hi.x, acc[gi][4]);
+                            acc[gi][5] = __builtin_fmaf(w[j], hi.y, acc[gi][5]);
+                            acc[gi][6] = __builtin_fmaf(w[j], hi.z, acc[gi][6]);
+                            acc[gi][7] = __builtin_fmaf(w[j], hi.w, acc[gi][7]);
+                        }
                     }
                 }
             }
         }
+        __syncthreads();  // the next chunk overwrites X
+    }
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+    for (int gi = 0; gi < 2; ++gi) {
+        if (gs[gi] >= ngroup) continue;  // uniform
+        const int lgR = __builtin_amdgcn_readfirstlane(lg[gi]), R = 1 << lgR;
+        float* a = acc[gi];
 #pragma unroll
-            for (int o = R; o < 64; o <<= 1) acc[c] += __shfl_xor(acc[c], o, 64);
+        for (int c = 0; c < 8; ++c)
+            for (int o = R; o < 64; o <<= 1) a[c] += __shfl_xor(a[c], o, 64);
+        if (wave >= 8 && lane < R) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) part[wave - 8][lane][c] = a[c];
         }
-        if (lane < R) {
+        __syncthreads();
+        if (wave < 8 && lane < R) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) part[wave][lane][c] = acc[c];
+            for (int c = 0; c < 8; ++c) part[wave][lane][c] += a[c];
         }
         __syncthreads();
         if (tid < R * 8) {  // row tid / 8, column tid % 8
             const int rr = tid >> 3, c = tid & 7;
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < W; ++w) sum += part[w][rr][c];
-            const int row = perm[s * R + rr];
-            if (row >= 0 && c < N) {
-                if constexpr (I8) sum *= rs[row];
-                const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
+            for (int w = 0; w < 8; ++w) sum += part[w][rr][c];
+            if (c < N) {
+                if constexpr (I8) sum *= oscale[gi];
+                const int64_t f = (int64_t)orow[gi] * ldy_r + (int64_t)c * ldy_c;
                 Y[f] = bias_add(sum, f, bias, c_size, beta, act);
             }
         }
-        __syncthreads();  // part is rewritten for the next slab
+        __syncthreads();  // part is rewritten for the second group
     }
 }
 
-constexpr int kChainFast8W = 16, kChainFast8U = 2;
-
-// LDS bytes of k_spmm_chain_fast8's X rows, or 0 when they do not fit.
-size_t chain_fast8_lds(int64_t K) {
-    const size_t x = (size_t)(K + 1) * 32;
-    const size_t part = sizeof(float) * kChainFast8W * 16 * 9;
-    return x + part <= 160 * 1024 ? x : 0;
-}
+constexpr int kBalFast8U = 4;
 
 template <bool I8, bool XV>
-void launch_chain_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
-                        int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
-    auto kern = k_spmm_chain_fast8<I8, 16, kChainFast8W, kChainFast8U, XV>;
-    const size_t lds = chain_fast8_lds(W->K);
-    // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
-    static uint64_t allowed = 0;  // bit d: done on device d (< 64)
+void launch_bal_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
+                      int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
+    auto kern = k_spmm_bal_fast8<I8, 16, kBalFast8U, XV>;
+    const size_t lds = (size_t)(W->bal_kcw + 1) * 32;  // <= (4096 + 1) * 32 B, with part[8][64][8]: 144 KiB
+    static uint64_t allowed = 0;  // bit d: the dynamic LDS limit raised on device d (< 64)
     const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
     if (lds > 65536 && (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit))) {
         PFR_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)(160 * 1024 - sizeof(float) * kChainFast8W * 16 * 9)));
+                                    (int)((pfr::kBalChunk + 1) * 32)));
         if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
     }
-    const int grid = (int)std::min<int64_t>(W->chain_nslab, ctx->num_cu > 0 ? ctx->num_cu : 256);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kChainFast8W), lds, ctx->stream, (int)W->K, N,
-                       (int)W->chain_nslab, W->chain_q0, W->chain_perm, W->chain_val,
-                       static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, ldx, Y, ldy_r, ldy_c, bias,
-                       c_size, beta, act);
+    const int grid = (W->bal_ngroup + 1) / 2;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * 16), lds, ctx->stream, (int)W->K, N, W->bal_ngroup,
+                       W->bal_nchunk, W->bal_kcw, W->bal_meta, W->bal_cmeta, W->bal_perm, W->bal_val, W->bal_col,
+                       W->row_scale, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
 }
 
 // At[k, i] = RN(alpha * A[i, k]) for A rows x cols (At cols x rows).
@@ -1442,16 +1552,13 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     hipStream_t s = ctx->stream;
     const void* val = W->val;
     const float* rs = W->row_scale;
-    if (FAST && N == 1 && W->chain_q0 != nullptr && W->chain_xlds && ldx < INT32_MAX) {
-        if (W->chain_rows == 16) launch_chain_fast<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
-        else if (W->chain_rows == 32) launch_chain_fast<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
-        else launch_chain_fast<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
-    } else if (FAST && N >= 2 && N <= 8 && W->chain_q0 != nullptr && W->chain_xlds && W->chain_rows == 16 &&
-               chain_fast8_lds(W->K) > 0 && ldx < INT32_MAX) {
+    if (FAST && N == 1 && W->bal_meta != nullptr && ldx < INT32_MAX) {
+        launch_bal_fast<I8>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (FAST && N >= 2 && N <= 8 && W->bal_meta != nullptr) {
         if (N == 8 && ldx % 4 == 0 && aligned16(X))
-            launch_chain_fast8<I8, true>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+            launch_bal_fast8<I8, true>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else
-            launch_chain_fast8<I8, false>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+            launch_bal_fast8<I8, false>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else if (FAST && N <= 8) {
         const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
         const bool xv = N == 8 && ldx % 4 == 0 && aligned16(X);

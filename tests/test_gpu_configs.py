@@ -172,10 +172,10 @@ def test_workgroup_per_row_n1_long_k(ctx):
         W.free()
 
 
-def test_workgroup_per_row_gemm_epilogues(ctx):
+def test_balanced_gemm_epilogues(ctx):
     """The Gemm form y = act(A . B + bias) in fast mode with rows of op(B)^T
-    holding ~2,400 nonzeros and K = 6000 (too long for X rows in LDS): the
-    workgroup-per-row kernel with bias and Relu / Gelu fused; infinities in
+    holding ~2,400 nonzeros and K = 6000 (two K chunks of the nnz-balanced
+    copy), batch 1, 3 and 8, with bias and Relu / Gelu fused; infinities in
     A.  Normwise against the oracle's sparse product plus bias (and, for the
     finite rows, its dense cpu_gemm), and the fused activations
     bit-identical to the separate device kernels on the unfused result."""
@@ -195,7 +195,7 @@ def test_workgroup_per_row_gemm_epilogues(ctx):
         A[0, rng.integers(0, K, 3)] = np.inf
         dA = torch.from_numpy(A).cuda()
         dY = torch.empty((Mb, Nf), dtype=torch.float32, device="cuda")
-        say(f"workgroup per row Gemm Mb={Mb} fast, bias, inf in A")
+        say(f"balanced Gemm Mb={Mb} fast, bias, inf in A")
         ctx.gemm_csr_dev(dA.data_ptr(), Mb, K, BT, dY.data_ptr(), 1.0, 1.0, dC.data_ptr(), Nf, mode="fast")
         ctx.synchronize()
         plain = dY.cpu().numpy()

@@ -271,24 +271,30 @@ def test_column_slice_layout_cases(ctx):
     assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
 
 
-def test_fast_vector_row_chains(ctx):
-    """The fast N = 1 kernel over the row-chain copy (x staged in LDS): long
-    and short rows, int8 with row scales and fp32, empty rows (slabs with no
-    quad rows), a strided x, NaN and infinity in x, and the fused bias /
-    activation epilogue; then matrices with enough rows for 32- and 64-row
-    slabs, strict (bit-exact) and fast.  Fast results are normwise within
-    1e-5 of the strict oracle, with NaN exactly where the oracle has it."""
+def check_fast(Y, R):
+    """Fast-mode bar: NaN exactly where the oracle has it, infinities equal,
+    the finite entries normwise within 1e-5 of the oracle's largest."""
+    assert np.array_equal(np.isnan(Y), np.isnan(R))
+    fin = ~np.isnan(R)
+    assert np.array_equal(Y[np.isinf(R)], R[np.isinf(R)])
+    ok = fin & np.isfinite(R)
+    if ok.any():
+        scale = np.abs(R[ok]).max()
+        assert np.abs(Y[ok] - R[ok]).max() <= 1e-5 * scale
+
+
+def test_fast_vector_balanced(ctx):
+    """The fast N <= 8 kernels over the nnz-balanced copy (x staged in LDS):
+    long and short rows, int8 with row scales and fp32, empty rows (groups
+    with no quad rows), a strided x, NaN and infinity in x, and the fused
+    bias / activation epilogue; then matrices with enough rows for 32- and
+    64-row slabs of the row-chain copy, strict (bit-exact) and fast.  Fast
+    results are normwise within 1e-5 of the strict oracle, with NaN exactly
+    where the oracle has it."""
     import torch
 
     rng = np.random.default_rng(12)
-
-    def check(Y, R):
-        assert np.array_equal(np.isnan(Y), np.isnan(R))
-        fin = ~np.isnan(R)
-        scale = np.abs(R[fin & np.isfinite(R)]).max()
-        assert np.array_equal(Y[np.isinf(R)], R[np.isinf(R)])
-        ok = fin & np.isfinite(R)
-        assert np.abs(Y[ok] - R[ok]).max() <= 1e-5 * scale
+    check = check_fast
 
     cases = [("int8 long rows", 600, 6000, True), ("fp32 long rows", 700, 5000, False),
              ("int8 short rows", 3000, 2000, True)]
@@ -300,7 +306,7 @@ def test_fast_vector_row_chains(ctx):
         else:
             ip, ix, vals = workloads.csr_lognormal_rows(M, K, dens, 0.5, 0.02, seed=M)
         cnt = np.diff(ip)
-        cnt[-40:] = 0  # empty rows: sorted last, a slab of them holds no quad rows
+        cnt[-40:] = 0  # empty rows: sorted last, a group of them holds no quad rows
         mask = np.ones(len(ix), bool)
         for r in range(M - 40, M):
             mask[ip[r]:ip[r + 1]] = False
@@ -311,7 +317,7 @@ def test_fast_vector_row_chains(ctx):
         np.cumsum(cnt, out=ip[1:])
         W = ctx.csr_upload(M, K, ip, ix, q, row_scales=sc) if i8 else ctx.csr_upload(M, K, ip, ix, vals)
         x = rng.standard_normal(K).astype(np.float32)
-        say(f"fast row chains: {name} M={M} K={K}")
+        say(f"fast balanced: {name} M={M} K={K}")
         check(W.spmm(x, mode="fast"), O.orc_csr_spmv(M, K, ip, ix, vals, x))
         x2 = x.copy()
         x2[ix[0]] = np.nan
@@ -326,12 +332,12 @@ def test_fast_vector_row_chains(ctx):
         R = O.orc_csr_spmv(M, K, ip, ix, vals, x)
         check(dY[:, 0].cpu().numpy(), relu_ref(R))
         assert not dY[:, 1].cpu().numpy().any()
-        # 2 <= N <= 8 (X staged in LDS as rows of eight when K allows)
+        # 2 <= N <= 8 (X staged in LDS chunk by chunk as rows of eight)
         for N in (2, 5, 8):
             X = rng.standard_normal((K, N)).astype(np.float32)
             X[ix[1], N - 1] = np.nan
             X[ix[len(ix) // 3], 0] = -np.inf
-            say(f"fast row chains: {name} N={N}")
+            say(f"fast balanced: {name} N={N}")
             check(W.spmm(X, mode="fast"), O.orc_csr_spmm(M, K, ip, ix, vals, X))
         W.free()
     # 32- and 64-row slabs: more rows than 16-row (32-row) slabs give four
@@ -346,6 +352,57 @@ def test_fast_vector_row_chains(ctx):
         check(W.spmm(x, mode="fast"), R)
         assert bits_equal(W.spmm(x), R)
         W.free()
+
+
+def test_balanced_copy_edges(ctx):
+    """Shapes at the edges of the nnz-balanced copy, fast mode, N = 1..8
+    against the oracle: one row holding every column beside empty rows (the
+    budget search's largest single row), fewer rows than one group, a
+    single row, K at one chunk exactly (4096), one column past it (two
+    chunks, the second one column wide), the largest K whose staged x fits
+    64 KiB (16380: four chunks of 4095), and K one past that (no balanced
+    copy: the wave-per-row kernel), int8 and fp32, with a strided X."""
+    import torch
+
+    rng = np.random.default_rng(21)
+    cases = [("one full row", 300, 3000), ("few rows", 5, 9000), ("single row", 1, 4096),
+             ("one chunk", 700, 4096), ("ragged chunk", 700, 4097), ("largest K", 400, 16380),
+             ("past largest K", 400, 16381)]
+    for name, M, K in cases:
+        dens = 0.2
+        ip, ix, q, sc = workloads.csr_int8_lognormal(M, K, dens, 0.8, 0.02, seed=M + K)
+        if name == "one full row":
+            cnt = np.diff(ip)
+            rows = [np.arange(K) if r == 7 else (np.array([], np.int64) if r % 3 == 0 else ix[ip[r]:ip[r + 1]])
+                    for r in range(M)]
+            qs = [rng.integers(-127, 128, len(c)).astype(np.int8) for c in rows]
+            ip = np.zeros(M + 1, np.int64)
+            np.cumsum([len(c) for c in rows], out=ip[1:])
+            ix = np.concatenate(rows).astype(np.int64)
+            q = np.concatenate(qs)
+        vals = workloads.dequant_rows(ip, q, sc)
+        for tag, W in (("int8", ctx.csr_upload(M, K, ip, ix, q, row_scales=sc)),
+                       ("fp32", ctx.csr_upload(M, K, ip, ix, vals))):
+            for N in (1, 2, 3, 8):
+                X = rng.standard_normal((K, N)).astype(np.float32)
+                if len(ix):
+                    X[ix[len(ix) // 2], 0] = np.inf
+                say(f"balanced edges: {name} M={M} K={K} {tag} N={N}")
+                R = O.orc_csr_spmm(M, K, ip, ix, vals, X)
+                check_fast(W.spmm(X, mode="fast").reshape(M, N), R.reshape(M, N))
+                # X as the first N columns of a K x (2N + 1) device buffer
+                # (its other columns NaN), Y rows of stride N + 3
+                Xw = np.full((K, 2 * N + 1), np.nan, np.float32)
+                Xw[:, :N] = X
+                dX = torch.from_numpy(Xw).cuda()
+                dY = torch.zeros((M, N + 3), dtype=torch.float32, device="cuda")
+                torch.cuda.synchronize()
+                W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), ldx=2 * N + 1, ldy=N + 3, mode="fast")
+                ctx.synchronize()
+                Yw = dY.cpu().numpy()
+                check_fast(Yw[:, :N], R.reshape(M, N))
+                assert not Yw[:, N:].any()
+            W.free()
 
 
 def test_strict_vector_row_chains(ctx):
