@@ -15,7 +15,9 @@ import numpy as np
 
 from . import _lib
 
-RT_SO = os.path.join(_lib.LIB_DIR, "libpyflamert.so")
+# PFR_RUNTIME_LIB selects another build of the host runtime (the
+# AddressSanitizer/UBSan one, `make -C pyflamert_amd/csrc sanitize`).
+RT_SO = os.environ.get("PFR_RUNTIME_LIB") or os.path.join(_lib.LIB_DIR, "libpyflamert.so")
 
 _P = C.c_void_p
 _I64 = C.c_int64

@@ -138,10 +138,11 @@ def test_decode_device_pointers_strided(ctx, decode_layer):
             assert close_normwise(Y[:, :8], R), name
 
 
-def test_workgroup_per_row_n1_long_k(ctx):
-    """N = 1 fast with K >= 16384 (no LDS copy of x) and a mean row of about
-    3,000 nonzeros: the workgroup-per-row kernel over uint16 columns; fp32
-    and int8 values, NaN and inf in x, the Relu epilogue."""
+def test_workgroup_per_row_long_k(ctx):
+    """N <= 8 fast with K >= 16384 (no LDS copy of x or X) and a mean row of
+    about 3,000 nonzeros: the workgroup-per-row kernel over uint16 columns;
+    fp32 and int8 values, NaN and inf in x, the Relu epilogue, then N = 3
+    and 8 (the eight-wide float4 X reads) with infinities and NaN in X."""
     import torch
 
     M, K = 600, 20000
@@ -169,6 +170,12 @@ def test_workgroup_per_row_n1_long_k(ctx):
         ctx.synchronize()
         plain = dy.cpu().numpy()
         assert bits_equal(fused, np.where(plain > 0, plain, np.float32(0))), tag
+        for N in (3, 8):
+            X = rng.standard_normal((K, N)).astype(np.float32)
+            X[ix[10], 0] = np.inf
+            X[ix[len(ix) // 3], N - 1] = np.nan
+            say(f"workgroup per row N={N} K={K} {tag}")
+            assert close_normwise(W.spmm(X, mode="fast"), O.orc_csr_spmm(M, K, ip, ix, vals, X)), (tag, N)
         W.free()
 
 
