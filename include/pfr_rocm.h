@@ -119,6 +119,20 @@ int pfr_csr_upload_i32(pfr_ctx* ctx, int64_t M, int64_t K, int64_t nnz,
 int pfr_csr_from_dense(pfr_ctx* ctx, const float* dense, int64_t rows,
                        int64_t cols, int transpose, float threshold,
                        pfr_csr** out);
+/* pfr_csr_from_dense for a weight already on the device, with the pruning
+ * mask optionally applied on the way: the CSR of op(dense * mask), where
+ * dense * mask is apply_mask (sparse_tensor.cpp:616-631; mask may be NULL)
+ * and op transposes when transpose != 0, keeping |v| > threshold with
+ * columns ascending as to_sparse does (sparse_tensor.cpp:560-610).  dense
+ * and mask are rows x cols, row-major, device.  The nonzeros are found,
+ * compacted and laid out on the device; only per-row counts come back to
+ * the host (to plan the layouts), so the handle equals what
+ * pfr_csr_from_dense builds from the same weight, and every product gives
+ * bit-identical results with either.  Runs on the context's stream and
+ * returns when the handle is complete.  At most 2^24 rows of op(dense). */
+int pfr_csr_from_dense_dev(pfr_ctx* ctx, const float* dense, int64_t rows,
+                           int64_t cols, int transpose, float threshold,
+                           const float* mask, pfr_csr** out);
 int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz);
 int pfr_csr_free(pfr_csr* w);
 
@@ -197,6 +211,14 @@ int pfr_gemm_csr_act_noalloc_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64
 int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W,
                   pfr_dtype dtype, const float* w_scales, int64_t n_scales,
                   pfr_sp24** out);
+/* pfr_sp24_pack for a weight already on the device (W device, w_scales
+ * host): the same layout, written by device kernels, so the weight never
+ * crosses to the host; the 2:4 check runs on the device and reports the
+ * first offending group in the same words.  Returns when the handle is
+ * complete. */
+int pfr_sp24_pack_dev(pfr_ctx* ctx, int64_t M, int64_t K, const void* W,
+                      pfr_dtype dtype, const float* w_scales, int64_t n_scales,
+                      pfr_sp24** out);
 int pfr_sp24_info(const pfr_sp24* w, int64_t* M, int64_t* K, pfr_dtype* dtype);
 int pfr_sp24_free(pfr_sp24* w);
 
@@ -355,6 +377,12 @@ int pfr_magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float sparsi
  * 16.  Host pointers; _dev: device pointers. */
 int pfr_nm_mask(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask);
 int pfr_nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, float* mask);
+/* apply_mask (sparse_tensor.cpp:616-631): out[i] = w[i] * mask[i], one fp32
+ * multiply per element (NaN or inf facing a 0 mask gives NaN, as there).
+ * Host pointers; _dev: device pointers on the context's stream (out may be
+ * w). */
+int pfr_apply_mask(pfr_ctx* ctx, const float* w, const float* mask, int64_t n, float* out);
+int pfr_apply_mask_dev(pfr_ctx* ctx, const float* w, const float* mask, int64_t n, float* out);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,9 @@ SIGNATURES = {
     "pfr_nm_mask": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
     "pfr_nm_mask_dev": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
     "pfr_csr_from_dense": (_INT, [_P, _P, _I64, _I64, _INT, _F, _PP]),
+    "pfr_csr_from_dense_dev": (_INT, [_P, _P, _I64, _I64, _INT, _F, _P, _PP]),
+    "pfr_apply_mask": (_INT, [_P, _P, _P, _I64, _P]),
+    "pfr_apply_mask_dev": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_csr_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
     "pfr_csr_free": (_INT, [_P]),
     "pfr_spmm_csr": (_INT, [_P, _P, _P, _I64, _P, _INT]),
@@ -65,6 +68,7 @@ SIGNATURES = {
     "pfr_gemm_csr_act_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT, _INT]),
     "pfr_gemm_csr_act_noalloc_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _F, _F, _P, _I64, _P, _INT, _INT]),
     "pfr_sp24_pack": (_INT, [_P, _I64, _I64, _P, _INT, _P, _I64, _PP]),
+    "pfr_sp24_pack_dev": (_INT, [_P, _I64, _I64, _P, _INT, _P, _I64, _PP]),
     "pfr_sp24_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_INT)]),
     "pfr_sp24_free": (_INT, [_P]),
     "pfr_sp24_gemm_i8": (_INT, [_P, _P, _P, _I64, _F, _INT, _F, _I32, _P]),

@@ -188,6 +188,8 @@ constexpr int kBalChunk = 4096;    // most columns per chunk of the balanced cop
 namespace pfr {
 // Makes ctx's device current (cheap when it already is).
 void bind(pfr_ctx* ctx);
+// out[i] = w[i] * mask[i] on stream s (apply_mask); out may alias w.
+void apply_mask_dev(hipStream_t s, const float* w, const float* mask, int64_t n, float* out);
 // Records, once per device, the workspace address of the allocation-free
 // Gemm entry; `device` must be current.
 void init_noalloc_workspace(int device);

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstring>
+#include <memory>
 #include <numeric>
 #include <vector>
 
@@ -80,6 +81,75 @@ void sell_order(const std::vector<int32_t>& cnt, int64_t nch, int32_t* b, int64_
     sell_order(cnt, nch, b + h, n - h, depth + 1);
 }
 
+// ---- Derived copies ---------------------------------------------------------
+// Each derived copy is planned from per-row (per-chunk) nonzero counts alone:
+// row order, slab or group shapes and run offsets.  The upload path counts
+// on the host and fills on the host; the build from a dense device weight
+// counts on the device, plans on the host from the counts it copies back
+// (M x a few integers) and fills on the device, so the nonzeros never leave
+// the GPU and both paths give the same layout.
+
+// Chunking of the sliced-ELL copy: chunks of whole 16-row LDS loads (the
+// staging of a chunk never reaches the zero row that follows it).
+void sell_geom(int64_t K, int64_t* kc, int64_t* nch) {
+    *kc = std::min<int64_t>((K + 15) / 16 * 16, pfr::kSellMaxKC);
+    *nch = K > 0 ? (K + *kc - 1) / *kc : 0;
+}
+
+// The sliced-ELL copy exists for float32 weights whose count table stays
+// small (else the row kernels serve).
+bool sell_wanted(int64_t M, int64_t K, int64_t nnz) {
+    int64_t kc, nch;
+    sell_geom(K, &kc, &nch);
+    return M > 0 && K > 0 && nnz > 0 && M * nch <= (int64_t(1) << 26);
+}
+
+struct SellPlan {
+    int64_t kc = 0, nch = 0, nslab = 0, len = 0;
+    std::vector<int32_t> perm;  // [nslab * kSellRows] row of each slab lane, -1 none
+    std::vector<int64_t> off;   // [nslab * nch + 1] first int4 of each (slab, chunk) run
+};
+
+// cnt: [M * nch] nonzeros of row r in chunk c at r * nch + c.  False when
+// the copy would outgrow 32-bit offsets.
+bool plan_sell(int64_t M, int64_t K, const std::vector<int32_t>& cnt, SellPlan* p) {
+    sell_geom(K, &p->kc, &p->nch);
+    const int64_t nch = p->nch, R = pfr::kSellRows;
+    p->nslab = (M + R - 1) / R;
+    std::vector<int32_t> order((size_t)M);
+    std::iota(order.begin(), order.end(), 0);
+    sell_order(cnt, nch, order.data(), M, 0);
+    p->off.assign((size_t)(p->nslab * nch + 1), 0);
+    for (int64_t sl = 0; sl < p->nslab; ++sl)
+        for (int64_t c = 0; c < nch; ++c) {
+            int32_t mx = 0;
+            for (int64_t i = sl * R; i < std::min(M, sl * R + R); ++i)
+                mx = std::max(mx, cnt[(size_t)(order[(size_t)i] * nch + c)]);
+            const int64_t steps = (mx + pfr::kSellStepPad - 1) / pfr::kSellStepPad * pfr::kSellStepPad;
+            p->off[(size_t)(sl * nch + c + 1)] = p->off[(size_t)(sl * nch + c)] + steps / 8 * 64;
+        }
+    p->len = p->off.back();
+    if (p->len + pfr::kSellTail > INT32_MAX) return false;
+    p->perm.assign((size_t)(p->nslab * R), -1);
+    std::copy(order.begin(), order.end(), p->perm.begin());
+    return true;
+}
+
+// Uploads the plan's tables (sell_blk is set by the fill).
+void set_sell(pfr_csr* w, const SellPlan& p, hipStream_t s) {
+    std::vector<int32_t> soff((size_t)(p.nslab * (p.nch + 1)));
+    for (int64_t sl = 0; sl < p.nslab; ++sl)
+        for (int64_t c = 0; c <= p.nch; ++c)  // c == nch: end of the slab's last run
+            soff[(size_t)(sl * (p.nch + 1) + c)] = (int32_t)p.off[(size_t)(sl * p.nch + c)];
+    w->sell_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
+    w->sell_soff = dev_alloc_copy(soff.data(), (int64_t)soff.size(), s);
+    w->sell_nslab = (int32_t)p.nslab;
+    w->sell_nch = (int32_t)p.nch;
+    w->sell_kc = (int32_t)p.kc;
+    w->sell_len = p.len;
+    PFR_HIP(hipStreamSynchronize(s));  // soff goes out of scope
+}
+
 // Sliced-ELL copy (layout described at pfr_csr::sell_blk).  Each row keeps
 // its storage order inside a chunk and chunks are visited in order, so the
 // copy needs the chunk index to be non-decreasing along every row (always
@@ -88,188 +158,198 @@ void sell_order(const std::vector<int32_t>& cnt, int64_t nch, int32_t* b, int64_
 void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
                 const float* vals, hipStream_t s) {
     const int64_t M = w->M, K = w->K;
-    if (M == 0 || K == 0 || w->nnz == 0) return;
-    // chunks of whole 16-row LDS loads: the staging of a chunk never reaches
-    // the zero row that follows it
-    const int64_t kc = std::min<int64_t>((K + 15) / 16 * 16, pfr::kSellMaxKC);
-    const int64_t nch = (K + kc - 1) / kc;
-    if (M * nch > (int64_t(1) << 26)) return;  // count table too large: keep the row kernels
+    if (!sell_wanted(M, K, w->nnz)) return;
+    int64_t kc, nch;
+    sell_geom(K, &kc, &nch);
     for (int64_t r = 0; r < M; ++r)
         for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
             if (col[j] / kc < col[j - 1] / kc) return;
     std::vector<int32_t> cnt((size_t)(M * nch), 0);
     for (int64_t r = 0; r < M; ++r)
         for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cnt[(size_t)(r * nch + col[j] / kc)];
+    SellPlan p;
+    if (!plan_sell(M, K, cnt, &p)) return;
     const int64_t R = pfr::kSellRows;
-    const int64_t nslab = (M + R - 1) / R;
-    std::vector<int32_t> order((size_t)M);
-    std::iota(order.begin(), order.end(), 0);
-    sell_order(cnt, nch, order.data(), M, 0);
-    std::vector<int64_t> off((size_t)(nslab * nch + 1), 0);
-    for (int64_t sl = 0; sl < nslab; ++sl)
-        for (int64_t c = 0; c < nch; ++c) {
-            int32_t mx = 0;
-            for (int64_t i = sl * R; i < std::min(M, sl * R + R); ++i)
-                mx = std::max(mx, cnt[(size_t)(order[(size_t)i] * nch + c)]);
-            const int64_t steps = (mx + pfr::kSellStepPad - 1) / pfr::kSellStepPad * pfr::kSellStepPad;
-            off[(size_t)(sl * nch + c + 1)] = off[(size_t)(sl * nch + c)] + steps / 8 * 64;
-        }
-    const int64_t len = off.back();
-    if (len + pfr::kSellTail > INT32_MAX) return;
     const int32_t pad_off = (int32_t)(kc * 64);
-    std::vector<int4> blk((size_t)(len + pfr::kSellTail));
+    std::vector<int4> blk((size_t)(p.len + pfr::kSellTail));
     for (auto& b : blk) b = make_int4(pad_off, 0, pad_off, 0);
-    std::vector<int32_t> perm((size_t)(nslab * R), -1);
     std::vector<int32_t> t((size_t)nch);
     for (int64_t i = 0; i < M; ++i) {
-        const int32_t row = order[(size_t)i];
-        perm[(size_t)i] = row;
+        const int32_t row = p.perm[(size_t)i];
         const int64_t sl = i / R, r = i % R;
         std::fill(t.begin(), t.end(), 0);
         for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
             const int64_t c = col[j] / kc;
             const int32_t step = t[(size_t)c]++;
-            int4& b = blk[(size_t)(off[(size_t)(sl * nch + c)] + (step / 8) * 64 + 4 * r + (step % 8) / 2)];
+            int4& b = blk[(size_t)(p.off[(size_t)(sl * nch + c)] + (step / 8) * 64 + 4 * r + (step % 8) / 2)];
             int32_t bits;
             std::memcpy(&bits, &vals[j], 4);
             const int32_t o = (int32_t)((col[j] - c * kc) * 64);
             if (step % 2 == 0) { b.x = o; b.y = bits; } else { b.z = o; b.w = bits; }
         }
     }
-    std::vector<int32_t> soff((size_t)(nslab * (nch + 1)));
-    for (int64_t sl = 0; sl < nslab; ++sl)
-        for (int64_t c = 0; c <= nch; ++c)  // c == nch: end of the slab's last run
-            soff[(size_t)(sl * (nch + 1) + c)] = (int32_t)off[(size_t)(sl * nch + c)];
-    w->sell_perm = dev_alloc_copy(perm.data(), (int64_t)perm.size(), s);
-    w->sell_soff = dev_alloc_copy(soff.data(), (int64_t)soff.size(), s);
     w->sell_blk = dev_alloc_copy(blk.data(), (int64_t)blk.size(), s);
-    w->sell_nslab = (int32_t)nslab;
-    w->sell_nch = (int32_t)nch;
-    w->sell_kc = (int32_t)kc;
-    w->sell_len = len;
-    // the host copies must outlive the asynchronous uploads
+    set_sell(w, p, s);  // synchronizes: blk outlives the upload
+}
+
+// Rows sorted by count, longest first, ties by row index (the row order of
+// the row-chain and balanced copies).
+std::vector<int32_t> order_by_length(const std::vector<int32_t>& len) {
+    std::vector<int32_t> order(len.size());
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return len[a] > len[b]; });
+    return order;
+}
+
+struct ChainPlan {
+    int64_t R = 0, nslab = 0;
+    bool xlds = false, c16 = false;
+    std::vector<int32_t> perm, len;  // [nslab * R] row and count of each slab lane (-1 / 0: none)
+    std::vector<int32_t> q0;         // [nslab + 1] first quad row of each slab
+};
+
+// Row-chain plan from the row counts.  Slab height: the staged-x kernels'
+// per-CU traffic and producer work per step grow with the rows a workgroup
+// folds, so the slabs are as short as keeps about four workgroups per CU: 16
+// rows (which also lets the strict 2 <= N <= 8 kernel run), else 32, else
+// 64.  Measured on 4096 x 4096 at 10 %: strict N = 1 8.47 -> 7.52 us and
+// strict N = 2 / 8 69 / 57 -> 9.9 / 12.7 us against 64-row slabs (which this
+// rule used to keep for short rows while x was staged one load at a time).
+// The global-gather kernel takes 64.  False when the copy would outgrow
+// 32-bit offsets.
+bool plan_chain(const pfr_csr* w, const std::vector<int32_t>& len, ChainPlan* p) {
+    const int64_t M = w->M;
+    p->xlds = w->K < pfr::kChainXMax;
+    const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
+    p->R = !p->xlds ? pfr::kChainRows : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
+    const int64_t R = p->R;
+    const std::vector<int32_t> order = order_by_length(len);
+    p->nslab = (M + R - 1) / R;
+    p->q0.assign((size_t)p->nslab + 1, 0);
+    int64_t total = 0;
+    for (int64_t sl = 0; sl < p->nslab; ++sl) {
+        total += (len[(size_t)order[(size_t)(sl * R)]] + 3) / 4;  // the slab's longest row
+        if ((total + 1) * R * 4 > INT32_MAX) return false;
+        p->q0[(size_t)sl + 1] = (int32_t)total;
+    }
+    p->c16 = p->xlds || w->K <= 65536;
+    p->perm.assign((size_t)(p->nslab * R), -1);
+    p->len.assign((size_t)(p->nslab * R), 0);
+    for (int64_t i = 0; i < M; ++i) {
+        p->perm[(size_t)i] = order[(size_t)i];
+        p->len[(size_t)i] = len[(size_t)order[(size_t)i]];
+    }
+    return true;
+}
+
+// Uploads the plan's tables (chain_val / chain_col are set by the fill).
+void set_chain(pfr_csr* w, const ChainPlan& p, hipStream_t s) {
+    w->chain_len = dev_alloc_copy(p.len.data(), (int64_t)p.len.size(), s);
+    w->chain_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
+    w->chain_q0 = dev_alloc_copy(p.q0.data(), (int64_t)p.q0.size(), s);
+    w->chain_rows = (int32_t)p.R;
+    w->chain_nslab = (int32_t)p.nslab;
+    w->chain_xlds = p.xlds;
+    w->chain_c16 = p.c16;
     PFR_HIP(hipStreamSynchronize(s));
 }
 
-// Row-chain copy (layout described at pfr_csr::chain_q0).  Rows are sorted
-// by count, longest first (ties by row index), so each slab's rows have
-// similar lengths and the padding to the slab maximum stays small.
+// Row-chain copy (layout described at pfr_csr::chain_q0), filled on the host.
 template <class V, class C>
 void fill_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
-                const std::vector<int32_t>& order, const std::vector<int32_t>& q0, hipStream_t s) {
-    const int64_t R = w->chain_rows, nslab = w->chain_nslab, nrec = (int64_t)q0.back() * R;
+                const ChainPlan& p, hipStream_t s) {
+    const int64_t R = p.R, nrec = (int64_t)p.q0.back() * R;
     // staged-x form: byte offsets into the LDS copy of x, padding at its zero
-    // slot K; otherwise column indices, padding at column 0
-    // one spare quad row of padding after the last slab: the kernels' clamped
-    // loads may touch it
-    const int64_t mul = w->chain_xlds ? 4 : 1;
+    // slot K; otherwise column indices, padding at column 0.  One spare quad
+    // row of padding after the last slab: the kernels' clamped loads may
+    // touch it.
+    const int64_t mul = p.xlds ? 4 : 1;
     std::vector<V> v((size_t)((nrec + R) * 4), V(0));
-    std::vector<C> c((size_t)((nrec + R) * 4), C(w->chain_xlds ? w->K * 4 : 0));
-    std::vector<int32_t> len((size_t)(nslab * R), 0), perm((size_t)(nslab * R), -1);
-    for (int64_t i = 0; i < (int64_t)order.size(); ++i) {
-        const int32_t row = order[(size_t)i];
+    std::vector<C> c((size_t)((nrec + R) * 4), C(p.xlds ? w->K * 4 : 0));
+    for (int64_t i = 0; i < w->M; ++i) {
+        const int32_t row = p.perm[(size_t)i];
         const int64_t sl = i / R, lane = i % R;
-        perm[(size_t)i] = row;
-        len[(size_t)i] = rowptr[row + 1] - rowptr[row];
         for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
             const int64_t step = j - rowptr[row];
-            const size_t at = (size_t)((((int64_t)q0[(size_t)sl] + step / 4) * R + lane) * 4 + step % 4);
+            const size_t at = (size_t)((((int64_t)p.q0[(size_t)sl] + step / 4) * R + lane) * 4 + step % 4);
             v[at] = vals[j];
             c[at] = (C)(col[j] * mul);
         }
     }
     w->chain_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
     w->chain_col = dev_alloc_copy(c.data(), (int64_t)c.size(), s);
-    w->chain_len = dev_alloc_copy(len.data(), (int64_t)len.size(), s);
-    w->chain_perm = dev_alloc_copy(perm.data(), (int64_t)perm.size(), s);
-    w->chain_q0 = dev_alloc_copy(q0.data(), (int64_t)q0.size(), s);
-    PFR_HIP(hipStreamSynchronize(s));  // the host vectors go out of scope here
+    set_chain(w, p, s);  // synchronizes: v and c outlive the uploads
 }
 
 void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
                  const void* vals, hipStream_t s) {
     const int64_t M = w->M;
     if (M == 0 || w->nnz == 0) return;
-    // Slab height: the staged-x kernels' per-CU traffic and producer work per
-    // step grow with the rows a workgroup folds, so the slabs are as short as
-    // keeps about four workgroups per CU: 16 rows (which also lets the strict
-    // 2 <= N <= 8 kernel run), else 32, else 64.  Measured on 4096 x 4096 at
-    // 10 %: strict N = 1 8.47 -> 7.52 us and strict N = 2 / 8 69 / 57 ->
-    // 9.9 / 12.7 us against 64-row slabs (which this rule used to keep for
-    // short rows while x was staged one load at a time).  The global-gather
-    // kernel takes 64.
-    w->chain_xlds = w->K < pfr::kChainXMax;
-    const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
-    const int64_t R = !w->chain_xlds ? pfr::kChainRows : (M < 16 * 4 * cu ? 16 : (M < 32 * 4 * cu ? 32 : 64));
-    w->chain_rows = (int32_t)R;
-    std::vector<int32_t> order((size_t)M);
-    std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
-        return rowptr[a + 1] - rowptr[a] > rowptr[b + 1] - rowptr[b];
-    });
-    const int64_t nslab = (M + R - 1) / R;
-    std::vector<int32_t> q0((size_t)nslab + 1, 0);
-    int64_t total = 0;
-    for (int64_t sl = 0; sl < nslab; ++sl) {
-        const int32_t first = order[(size_t)(sl * R)];  // the slab's longest row
-        total += (rowptr[first + 1] - rowptr[first] + 3) / 4;
-        if ((total + 1) * R * 4 > INT32_MAX) return;  // keep the block kernels
-        q0[(size_t)sl + 1] = (int32_t)total;
-    }
-    w->chain_nslab = (int32_t)nslab;
-    w->chain_c16 = w->chain_xlds || w->K <= 65536;
+    std::vector<int32_t> len((size_t)M);
+    for (int64_t r = 0; r < M; ++r) len[(size_t)r] = rowptr[r + 1] - rowptr[r];
+    ChainPlan p;
+    if (!plan_chain(w, len, &p)) return;  // keep the block kernels
     if (w->vdt == PFR_F32) {
-        if (w->chain_c16) fill_chain<float, uint16_t>(w, rowptr, col, static_cast<const float*>(vals), order, q0, s);
-        else fill_chain<float, int32_t>(w, rowptr, col, static_cast<const float*>(vals), order, q0, s);
+        if (p.c16) fill_chain<float, uint16_t>(w, rowptr, col, static_cast<const float*>(vals), p, s);
+        else fill_chain<float, int32_t>(w, rowptr, col, static_cast<const float*>(vals), p, s);
     } else {
-        if (w->chain_c16) fill_chain<int8_t, uint16_t>(w, rowptr, col, static_cast<const int8_t*>(vals), order, q0, s);
-        else fill_chain<int8_t, int32_t>(w, rowptr, col, static_cast<const int8_t*>(vals), order, q0, s);
+        if (p.c16) fill_chain<int8_t, uint16_t>(w, rowptr, col, static_cast<const int8_t*>(vals), p, s);
+        else fill_chain<int8_t, int32_t>(w, rowptr, col, static_cast<const int8_t*>(vals), p, s);
     }
 }
 
-// nnz-balanced copy (layout described at pfr_csr::bal_meta).  Rows are taken
-// longest first; each group takes as many rows as the largest power of two
-// (at most 64 and at most the rows left) whose padded records -- R times the
-// sum over chunks of its longest row there -- fit the budget, so a row
-// longer than the budget makes a group of its own.  The budget is the
-// smallest that keeps the group count at most two per CU.  Only for K whose
-// chunks, each with its zero slot, fit 64 KiB of staged x (the N = 1
+// Chunking of the balanced copy: C chunks of kcw columns; false when the
+// chunks, each with its zero slot, exceed 64 KiB of staged x (the N = 1
 // kernel stages all of x at once).
-template <class V>
-void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
-               hipStream_t s) {
-    const int64_t M = w->M, K = w->K;
-    if (M == 0 || w->nnz == 0 || K == 0) return;
-    const int64_t C = (K + pfr::kBalChunk - 1) / pfr::kBalChunk, kcw = (K + C - 1) / C;
-    if (C * (kcw + 1) * 4 > 65536) return;
-    std::vector<int32_t> order((size_t)M);
-    std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
-        return rowptr[a + 1] - rowptr[a] > rowptr[b + 1] - rowptr[b];
-    });
+bool bal_geom(int64_t K, int64_t* C, int64_t* kcw) {
+    if (K <= 0) return false;
+    *C = (K + pfr::kBalChunk - 1) / pfr::kBalChunk;
+    *kcw = (K + *C - 1) / *C;
+    return *C * (*kcw + 1) * 4 <= 65536;
+}
+
+struct BalPlan {
+    int64_t C = 0, kcw = 0, G = 0, nrec = 0;
+    std::vector<int4> meta;    // [G] {log2 R, first perm entry, first record, quad rows}
+    std::vector<int2> cmeta;   // [G * C] {first record, quad rows} of each (group, chunk)
+    std::vector<int32_t> perm; // [M] row of each sorted position
+    std::vector<int32_t> gpos; // [M] group of each sorted position
+};
+
+// nnz-balanced plan (layout described at pfr_csr::bal_meta) from the row
+// counts and the per-chunk counts cntc[r * C + c].  Rows are taken longest
+// first; each group takes as many rows as the largest power of two (at most
+// 64 and at most the rows left) whose padded records -- R times the sum over
+// chunks of its longest row there -- fit the budget, so a row longer than
+// the budget makes a group of its own.  The budget is the smallest that
+// keeps the group count at most two per CU.  False when the copy would
+// outgrow 32-bit offsets.
+bool plan_bal(const pfr_csr* w, const std::vector<int32_t>& len, const std::vector<int32_t>& cntc, BalPlan* p) {
+    const int64_t M = w->M;
+    if (!bal_geom(w->K, &p->C, &p->kcw)) return false;
+    const int64_t C = p->C;
+    const std::vector<int32_t> order = order_by_length(len);
     // quad rows per (sorted position, chunk)
-    std::vector<int32_t> qz((size_t)(M * C), 0);
-    for (int64_t i = 0; i < M; ++i) {
-        const int32_t r = order[(size_t)i];
-        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++qz[(size_t)(i * C + col[j] / kcw)];
-        for (int64_t c = 0; c < C; ++c) qz[(size_t)(i * C + c)] = (qz[(size_t)(i * C + c)] + 3) / 4;
-    }
-    auto recs = [&](int64_t i, int64_t p) {  // padded records of rows i .. i+p-1 as one group
+    std::vector<int32_t> qz((size_t)(M * C));
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t c = 0; c < C; ++c)
+            qz[(size_t)(i * C + c)] = (cntc[(size_t)(order[(size_t)i] * C + c)] + 3) / 4;
+    auto recs = [&](int64_t i, int64_t n) {  // padded records of rows i .. i+n-1 as one group
         int64_t t = 0;
         for (int64_t c = 0; c < C; ++c) {
             int32_t mx = 0;
-            for (int64_t j = i; j < i + p; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
+            for (int64_t j = i; j < i + n; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
             t += mx;
         }
-        return p * t;
+        return n * t;
     };
     auto cut = [&](int64_t budget, std::vector<int>* out) {
         int64_t n = 0;
         for (int64_t i = 0; i < M;) {
-            int p = 64;
-            while (p > 1 && (p > M - i || recs(i, p) > budget)) p >>= 1;
-            if (out) out->push_back(p);
-            i += p;
+            int q = 64;
+            while (q > 1 && (q > M - i || recs(i, q) > budget)) q >>= 1;
+            if (out) out->push_back(q);
+            i += q;
             ++n;
         }
         return n;
@@ -286,62 +366,85 @@ void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector
     std::vector<int> groups;
     cut(lo, &groups);
     const int64_t G = (int64_t)groups.size();
-    std::vector<int4> meta((size_t)G);
-    std::vector<int2> cmeta((size_t)(G * C));
-    int64_t nrec = 0;
-    {
-        int64_t i = 0;
-        for (int64_t g = 0; g < G; ++g) {
-            const int R = groups[(size_t)g];
-            for (int64_t c = 0; c < C; ++c) {
-                int32_t mx = 0;
-                for (int64_t j = i; j < i + R; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
-                cmeta[(size_t)(g * C + c)] = make_int2((int)nrec, mx);
-                nrec += (int64_t)R * mx;
-            }
-            i += R;
-        }
-    }
-    if ((nrec + 64) * 4 > INT32_MAX || G > INT32_MAX) return;
-    std::vector<int32_t> perm((size_t)M, -1);
-    // one spare record per lane after the last group
-    std::vector<V> v((size_t)((nrec + 64) * 4), V(0));
-    std::vector<uint16_t> cidx((size_t)((nrec + 64) * 4), (uint16_t)(4 * kcw));  // chunk 0's zero
-    std::vector<int32_t> k_in((size_t)C);
-    int64_t i = 0;
+    p->G = G;
+    p->meta.resize((size_t)G);
+    p->cmeta.resize((size_t)(G * C));
+    p->perm.assign(order.begin(), order.end());
+    p->gpos.resize((size_t)M);
+    int64_t nrec = 0, i = 0;
     for (int64_t g = 0; g < G; ++g) {
         const int R = groups[(size_t)g];
         int lg = 0;
         while ((1 << lg) < R) ++lg;
-        int nq = 0;
+        int64_t nq = 0;
         for (int64_t c = 0; c < C; ++c) {
-            const int2 cm = cmeta[(size_t)(g * C + c)];
-            nq += cm.y;
-            for (int64_t e = (int64_t)cm.x * 4; e < ((int64_t)cm.x + (int64_t)R * cm.y) * 4; ++e)
+            int32_t mx = 0;
+            for (int64_t j = i; j < i + R; ++j) mx = std::max(mx, qz[(size_t)(j * C + c)]);
+            if (nrec > INT32_MAX) return false;
+            p->cmeta[(size_t)(g * C + c)] = make_int2((int)nrec, mx);
+            nrec += (int64_t)R * mx;
+            nq += mx;
+        }
+        p->meta[(size_t)g] = make_int4(lg, (int)i, p->cmeta[(size_t)(g * C)].x, (int)std::min<int64_t>(nq, INT32_MAX));
+        for (int64_t j = i; j < i + R; ++j) p->gpos[(size_t)j] = (int32_t)g;
+        i += R;
+    }
+    p->nrec = nrec;
+    return (nrec + 64) * 4 <= INT32_MAX && G <= INT32_MAX;
+}
+
+// Uploads the plan's tables (bal_val / bal_col are set by the fill).
+void set_bal(pfr_csr* w, const BalPlan& p, hipStream_t s) {
+    w->bal_meta = dev_alloc_copy(p.meta.data(), p.G, s);
+    w->bal_cmeta = dev_alloc_copy(p.cmeta.data(), p.G * p.C, s);
+    w->bal_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
+    w->bal_ngroup = (int32_t)p.G;
+    w->bal_nchunk = (int32_t)p.C;
+    w->bal_kcw = (int32_t)p.kcw;
+    PFR_HIP(hipStreamSynchronize(s));
+}
+
+// nnz-balanced copy, filled on the host.
+template <class V>
+void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
+               hipStream_t s) {
+    const int64_t M = w->M;
+    int64_t C, kcw;
+    if (M == 0 || w->nnz == 0 || !bal_geom(w->K, &C, &kcw)) return;
+    std::vector<int32_t> len((size_t)M), cntc((size_t)(M * C), 0);
+    for (int64_t r = 0; r < M; ++r) {
+        len[(size_t)r] = rowptr[r + 1] - rowptr[r];
+        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cntc[(size_t)(r * C + col[j] / kcw)];
+    }
+    BalPlan p;
+    if (!plan_bal(w, len, cntc, &p)) return;
+    // one spare record per lane after the last group
+    std::vector<V> v((size_t)((p.nrec + 64) * 4), V(0));
+    std::vector<uint16_t> cidx((size_t)((p.nrec + 64) * 4), (uint16_t)(4 * kcw));  // chunk 0's zero
+    for (int64_t g = 0; g < p.G; ++g) {
+        const int64_t R = int64_t(1) << p.meta[(size_t)g].x;
+        for (int64_t c = 0; c < C; ++c) {
+            const int2 cm = p.cmeta[(size_t)(g * C + c)];
+            for (int64_t e = (int64_t)cm.x * 4; e < ((int64_t)cm.x + R * cm.y) * 4; ++e)
                 cidx[(size_t)e] = (uint16_t)(4 * (c * (kcw + 1) + kcw));  // padding: this chunk's zero
         }
-        meta[(size_t)g] = make_int4(lg, (int)i, cmeta[(size_t)(g * C)].x, nq);
-        for (int lane = 0; lane < R; ++lane, ++i) {
-            const int32_t row = order[(size_t)i];
-            perm[(size_t)i] = row;
-            std::fill(k_in.begin(), k_in.end(), 0);
-            for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
-                const int64_t c = col[j] / kcw, k = k_in[(size_t)c]++;
-                const size_t at = (size_t)(((cmeta[(size_t)(g * C + c)].x + (k / 4) * R + lane) * 4) + k % 4);
-                v[at] = vals[j];
-                cidx[at] = (uint16_t)(4 * (c * (kcw + 1) + col[j] - c * kcw));
-            }
+    }
+    std::vector<int32_t> k_in((size_t)C);
+    for (int64_t i = 0; i < M; ++i) {
+        const int64_t g = p.gpos[(size_t)i];
+        const int64_t R = int64_t(1) << p.meta[(size_t)g].x, lane = i - p.meta[(size_t)g].y;
+        const int32_t row = p.perm[(size_t)i];
+        std::fill(k_in.begin(), k_in.end(), 0);
+        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
+            const int64_t c = col[j] / kcw, k = k_in[(size_t)c]++;
+            const size_t at = (size_t)(((p.cmeta[(size_t)(g * C + c)].x + (k / 4) * R + lane) * 4) + k % 4);
+            v[at] = vals[j];
+            cidx[at] = (uint16_t)(4 * (c * (kcw + 1) + col[j] - c * kcw));
         }
     }
-    w->bal_meta = dev_alloc_copy(meta.data(), G, s);
-    w->bal_cmeta = dev_alloc_copy(cmeta.data(), G * C, s);
-    w->bal_perm = dev_alloc_copy(perm.data(), M, s);
     w->bal_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
     w->bal_col = dev_alloc_copy(cidx.data(), (int64_t)cidx.size(), s);
-    w->bal_ngroup = (int32_t)G;
-    w->bal_nchunk = (int32_t)C;
-    w->bal_kcw = (int32_t)kcw;
-    PFR_HIP(hipStreamSynchronize(s));  // the host vectors go out of scope here
+    set_bal(w, p, s);  // synchronizes: v and cidx outlive the uploads
 }
 
 pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
@@ -385,6 +488,356 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {
+        free_csr(w);
+        throw;
+    }
+}
+
+
+// ---- Build from a dense device weight ----------------------------------------
+
+// Device memory freed when it goes out of scope (temporaries of a build).
+struct DevTmp {
+    void* p = nullptr;
+    explicit DevTmp(size_t bytes) { PFR_HIP(hipMalloc(&p, bytes > 0 ? bytes : 4)); }
+    ~DevTmp() { if (p) (void)hipFree(p); }
+    DevTmp(const DevTmp&) = delete;
+    DevTmp& operator=(const DevTmp&) = delete;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+constexpr int kMaxCountChunks = 4096;  // sliced-ELL chunks counted in LDS (K <= 4M)
+
+template <class T>
+__global__ __launch_bounds__(256) void k_fill(T* __restrict__ p, int64_t n, T v) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+template <class T>
+void fill_dev(T* p, int64_t n, T v, hipStream_t s) {
+    if (n <= 0) return;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+    PFR_HIP(hipGetLastError());
+}
+
+// D[c, r] = A[r, c] (* mask[r, c]) for A rows x cols: the op(W) a CSR of
+// W^T is built from, through 32 x 33 LDS tiles (coalesced both ways).
+template <bool MASK>
+__global__ __launch_bounds__(256) void k_transpose_mask(const float* __restrict__ A, const float* __restrict__ mask,
+                                                        int64_t rows, int64_t cols, float* __restrict__ D) {
+    __shared__ float t[32][33];
+    const int64_t ntc = (cols + 31) / 32;  // one workgroup per 32 x 32 tile
+    const int64_t r0 = (int64_t)blockIdx.x / ntc * 32, c0 = (int64_t)blockIdx.x % ntc * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) {
+            float v = A[r * cols + c];
+            if constexpr (MASK) v = v * mask[r * cols + c];
+            t[i][tx] = v;
+        }
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) D[c * rows + r] = t[tx][i];
+    }
+}
+
+// Adds the kept entries of one wave's 64 consecutive columns [kw, kw + 64)
+// (bit l of m: column kw + l) to the counts of their chunks of width w.  The
+// 64 columns meet at most two chunks: w >= 64 whenever there are two.
+__device__ __forceinline__ void count_chunks(int32_t* s, uint64_t m, int64_t kw, int64_t w) {
+    const int64_t c = kw / w, b = (c + 1) * w - kw;  // lanes below b are in chunk c
+    if (b >= 64) {
+        atomicAdd(&s[c], (int)__popcll(m));
+    } else {
+        const uint64_t lo = m & ((uint64_t(1) << b) - 1), hi = m >> b;
+        if (lo) atomicAdd(&s[c], (int)__popcll(lo));
+        if (hi) atomicAdd(&s[c + 1], (int)__popcll(hi));
+    }
+}
+
+// One workgroup per row of D (M x K, row-major): the row's count of
+// |v| > thr (the test of to_sparse, sparse_tensor.cpp:578; NaN fails it),
+// then its counts per sliced-ELL chunk (nchs of width kc) and per balanced
+// chunk (nchb of width kcw): cnt[r * (1 + nchs + nchb) + ...].
+__global__ __launch_bounds__(256) void k_dense_count(const float* __restrict__ D, int64_t K, float thr, int kc,
+                                                     int nchs, int kcw, int nchb, int32_t* __restrict__ cnt) {
+    extern __shared__ int32_t sc[];  // [1 + nchs + nchb]
+    const int n = 1 + nchs + nchb;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < n; i += 256) sc[i] = 0;
+    __syncthreads();
+    const float* row = D + (int64_t)blockIdx.x * K;
+    int tot = 0;
+    for (int64_t k0 = 0; k0 < K; k0 += 256) {
+        const int64_t k = k0 + tid;
+        const bool f = k < K && fabsf(row[k]) > thr;
+        const uint64_t m = __ballot(f);
+        if (lane == 0 && m) {
+            const int64_t kw = k0 + 64 * wave;
+            tot += (int)__popcll(m);
+            if (nchs) count_chunks(sc + 1, m, kw, kc);
+            if (nchb) count_chunks(sc + 1 + nchs, m, kw, kcw);
+        }
+    }
+    if (lane == 0 && tot) atomicAdd(&sc[0], tot);
+    __syncthreads();
+    for (int i = tid; i < n; i += 256) cnt[(int64_t)blockIdx.x * n + i] = sc[i];
+}
+
+// One workgroup per row of D: the kept entries in ascending column order at
+// rowptr[r] onward (the order to_sparse emits), as int32 (and, when col16 is
+// given, uint16) columns and float values.
+__global__ __launch_bounds__(256) void k_dense_compact(const float* __restrict__ D, int64_t K, float thr,
+                                                       const int32_t* __restrict__ rowptr, int32_t* __restrict__ col,
+                                                       uint16_t* __restrict__ col16, float* __restrict__ val) {
+    __shared__ int wsum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* row = D + (int64_t)blockIdx.x * K;
+    int base = rowptr[blockIdx.x];
+    for (int64_t k0 = 0; k0 < K; k0 += 256) {
+        const int64_t k = k0 + tid;
+        const float v = k < K ? row[k] : 0.0f;
+        const bool f = k < K && fabsf(v) > thr;
+        const uint64_t m = __ballot(f);
+        if (lane == 0) wsum[wave] = (int)__popcll(m);
+        __syncthreads();
+        int off = base, total = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            off += w < wave ? wsum[w] : 0;
+            total += wsum[w];
+        }
+        if (f) {
+            const int j = off + (int)__popcll(m & ((uint64_t(1) << lane) - 1));
+            col[j] = (int32_t)k;
+            val[j] = v;
+            if (col16) col16[j] = (uint16_t)k;
+        }
+        base += total;
+        __syncthreads();
+    }
+}
+
+// First index in [lo, hi) of the ascending columns col[] that is >= t.
+__device__ __forceinline__ int32_t first_at_least(const int32_t* __restrict__ col, int32_t lo, int32_t hi, int32_t t) {
+    while (lo < hi) {
+        const int32_t mid = lo + (hi - lo) / 2;
+        if (col[mid] < t) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Sliced-ELL fill, one wave per sorted position i (row perm[i], slab i / 16,
+// lane i % 16): entry j of chunk c is that chunk's step j - (the row's first
+// entry in c), as build_sell places it.  blk holds the padding pattern.
+__global__ __launch_bounds__(256) void k_sell_fill(int64_t M, const int32_t* __restrict__ perm,
+                                                   const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+                                                   const float* __restrict__ val, const int64_t* __restrict__ off,
+                                                   int nch, int kc, int4* __restrict__ blk) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= M) return;
+    const int lane = threadIdx.x & 63;
+    const int32_t row = perm[i], b = rowptr[row], e = rowptr[row + 1];
+    const int64_t sl = i / pfr::kSellRows, r = i % pfr::kSellRows;
+    for (int32_t j = b + lane; j < e; j += 64) {
+        const int32_t k = col[j], c = k / kc;
+        const int32_t step = j - first_at_least(col, b, j, c * kc);
+        int32_t* q = reinterpret_cast<int32_t*>(blk + off[sl * nch + c] + (step / 8) * 64 + 4 * r + (step % 8) / 2) +
+                     (step % 2) * 2;
+        q[0] = (k - c * kc) * 64;
+        q[1] = __float_as_int(val[j]);
+    }
+}
+
+// Row-chain fill, one wave per sorted position i (row perm[i], slab i / R,
+// lane i % R), as fill_chain places the entries; v and c hold the padding.
+template <class C>
+__global__ __launch_bounds__(256) void k_chain_fill(int64_t M, int R, const int32_t* __restrict__ perm,
+                                                    const int32_t* __restrict__ q0, const int32_t* __restrict__ rowptr,
+                                                    const int32_t* __restrict__ col, const float* __restrict__ val,
+                                                    int mul, float* __restrict__ v, C* __restrict__ c) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= M) return;
+    const int lane = threadIdx.x & 63;
+    const int32_t row = perm[i], b = rowptr[row], e = rowptr[row + 1];
+    const int64_t sl = i / R, ln = i % R, q = q0[sl];
+    for (int32_t j = b + lane; j < e; j += 64) {
+        const int64_t step = j - b;
+        const int64_t at = ((q + step / 4) * R + ln) * 4 + step % 4;
+        v[at] = val[j];
+        c[at] = (C)(col[j] * mul);
+    }
+}
+
+// Balanced copy: padding of each (group, chunk) region at that chunk's zero.
+__global__ __launch_bounds__(256) void k_bal_pad(int C, int kcw, const int4* __restrict__ meta,
+                                                 const int2* __restrict__ cmeta, uint16_t* __restrict__ cidx) {
+    const int64_t g = blockIdx.x;
+    const int64_t R = int64_t(1) << meta[g].x;
+    for (int c = 0; c < C; ++c) {
+        const int2 cm = cmeta[g * C + c];
+        const uint16_t z = (uint16_t)(4 * (c * (kcw + 1) + kcw));
+        for (int64_t e = (int64_t)cm.x * 4 + threadIdx.x; e < ((int64_t)cm.x + R * cm.y) * 4; e += 256) cidx[e] = z;
+    }
+}
+
+// Balanced fill, one wave per sorted position i (group gpos[i], lane i minus
+// the group's first position): entry j is entry k of its row in chunk c, k
+// counted from the row's first entry in c, placed as build_bal places it.
+__global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, const int4* __restrict__ meta,
+                                                  const int2* __restrict__ cmeta, const int32_t* __restrict__ perm,
+                                                  const int32_t* __restrict__ gpos, const int32_t* __restrict__ rowptr,
+                                                  const int32_t* __restrict__ col, const float* __restrict__ val,
+                                                  float* __restrict__ v, uint16_t* __restrict__ cidx) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= M) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t g = gpos[i];
+    const int4 m = meta[g];
+    const int64_t R = int64_t(1) << m.x, ln = i - m.y;
+    const int32_t row = perm[i], b = rowptr[row], e = rowptr[row + 1];
+    for (int32_t j = b + lane; j < e; j += 64) {
+        const int32_t kk = col[j], c = kk / kcw;
+        const int64_t k = j - first_at_least(col, b, j, c * kcw);
+        const int64_t at = ((cmeta[g * C + c].x + (k / 4) * R + ln) * 4) + k % 4;
+        v[at] = val[j];
+        cidx[at] = (uint16_t)(4 * (c * (kcw + 1) + kk - c * kcw));
+    }
+}
+
+template <class T>
+T* dev_alloc(int64_t count) {
+    void* p = nullptr;
+    PFR_HIP(hipMalloc(&p, sizeof(T) * (size_t)(count > 0 ? count : 1)));
+    return static_cast<T*>(p);
+}
+
+unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
+
+// The CSR handle of D (M x K, row-major, device), with every derived copy
+// the upload path would build, from counts copied back to the host and
+// fills on the device.
+pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, float thr) {
+    hipStream_t s = ctx->stream;
+    int64_t kc, nchs;
+    sell_geom(K, &kc, &nchs);
+    if (!sell_wanted(M, K, 1) || nchs > kMaxCountChunks) nchs = 0;
+    int64_t nchb = 0, kcw = 1;
+    if (!bal_geom(K, &nchb, &kcw)) nchb = 0, kcw = 1;
+    const int64_t stride = 1 + nchs + nchb;
+    std::vector<int32_t> cnt((size_t)(M * stride));
+    {
+        DevTmp dcnt(sizeof(int32_t) * (size_t)(M * stride));
+        hipLaunchKernelGGL(k_dense_count, dim3((unsigned)M), dim3(256), (size_t)stride * 4, s, D, K, thr, (int)kc,
+                           (int)nchs, (int)kcw, (int)nchb, dcnt.as<int32_t>());
+        PFR_HIP(hipGetLastError());
+        PFR_HIP(hipMemcpyAsync(cnt.data(), dcnt.p, cnt.size() * 4, hipMemcpyDeviceToHost, s));
+        PFR_HIP(hipStreamSynchronize(s));
+    }
+    std::vector<int32_t> rowptr((size_t)M + 1, 0), len((size_t)M);
+    for (int64_t r = 0; r < M; ++r) {
+        len[(size_t)r] = cnt[(size_t)(r * stride)];
+        pfr::require((int64_t)rowptr[(size_t)r] + len[(size_t)r] < INT32_MAX, "nnz exceeds 32-bit indices");
+        rowptr[(size_t)r + 1] = rowptr[(size_t)r] + len[(size_t)r];
+    }
+    auto* w = new pfr_csr();
+    try {
+        w->ctx = ctx;
+        w->M = M;
+        w->K = K;
+        w->nnz = rowptr[(size_t)M];
+        w->vdt = PFR_F32;
+        w->max_row_nnz = M ? *std::max_element(len.begin(), len.end()) : 0;
+        w->cols_sorted = true;
+        w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
+        w->col = dev_alloc<int32_t>(w->nnz);
+        float* val = dev_alloc<float>(w->nnz);
+        w->val = val;
+        if (K <= 65536 && w->nnz > 0) w->col16 = dev_alloc<uint16_t>(w->nnz);
+        hipLaunchKernelGGL(k_dense_compact, dim3((unsigned)M), dim3(256), 0, s, D, K, thr, w->rowptr, w->col,
+                           w->col16, val);
+        PFR_HIP(hipGetLastError());
+        std::vector<int32_t> blocks = spmv_blocks(rowptr, M);
+        w->n_spmv_blocks = (int64_t)blocks.size() - 1;
+        w->spmv_blocks = dev_alloc_copy(blocks.data(), (int64_t)blocks.size(), s);
+        PFR_HIP(hipStreamSynchronize(s));  // blocks goes out of scope
+        if (w->nnz == 0) return w;
+        if (nchs > 0 && sell_wanted(M, K, w->nnz)) {
+            std::vector<int32_t> cs((size_t)(M * nchs));
+            for (int64_t r = 0; r < M; ++r)
+                std::copy(cnt.begin() + r * stride + 1, cnt.begin() + r * stride + 1 + nchs, cs.begin() + r * nchs);
+            SellPlan p;
+            if (plan_sell(M, K, cs, &p)) {
+                w->sell_blk = dev_alloc<int4>(p.len + pfr::kSellTail);
+                const int32_t pad = (int32_t)(p.kc * 64);
+                fill_dev(w->sell_blk, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
+                set_sell(w, p, s);
+                int64_t* off = dev_alloc_copy(p.off.data(), (int64_t)p.off.size(), s);
+                hipLaunchKernelGGL(k_sell_fill, dim3(waves_grid(M)), dim3(256), 0, s, M, w->sell_perm, w->rowptr,
+                                   w->col, val, off, (int)p.nch, (int)p.kc, w->sell_blk);
+                hipError_t e = hipGetLastError();
+                (void)hipStreamSynchronize(s);
+                (void)hipFree(off);
+                if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_sell_fill: ") + hipGetErrorString(e));
+            }
+        }
+        ChainPlan cp;
+        if (plan_chain(w, len, &cp)) {
+            const int64_t n = ((int64_t)cp.q0.back() * cp.R + cp.R) * 4;
+            float* v = dev_alloc<float>(n);
+            w->chain_val = v;
+            fill_dev(v, n, 0.0f, s);
+            set_chain(w, cp, s);
+            const int mul = cp.xlds ? 4 : 1;
+            if (cp.c16) {
+                auto* c = dev_alloc<uint16_t>(n);
+                w->chain_col = c;
+                fill_dev(c, n, (uint16_t)(cp.xlds ? K * 4 : 0), s);
+                hipLaunchKernelGGL(k_chain_fill<uint16_t>, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)cp.R,
+                                   w->chain_perm, w->chain_q0, w->rowptr, w->col, val, mul, v, c);
+            } else {
+                auto* c = dev_alloc<int32_t>(n);
+                w->chain_col = c;
+                fill_dev(c, n, (int32_t)(cp.xlds ? K * 4 : 0), s);
+                hipLaunchKernelGGL(k_chain_fill<int32_t>, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)cp.R,
+                                   w->chain_perm, w->chain_q0, w->rowptr, w->col, val, mul, v, c);
+            }
+            PFR_HIP(hipGetLastError());
+        }
+        if (nchb > 0) {
+            std::vector<int32_t> cb((size_t)(M * nchb));
+            for (int64_t r = 0; r < M; ++r)
+                std::copy(cnt.begin() + r * stride + 1 + nchs, cnt.begin() + (r + 1) * stride, cb.begin() + r * nchb);
+            BalPlan bp;
+            if (plan_bal(w, len, cb, &bp)) {
+                const int64_t n = (bp.nrec + 64) * 4;
+                float* v = dev_alloc<float>(n);
+                w->bal_val = v;
+                w->bal_col = dev_alloc<uint16_t>(n);
+                fill_dev(v, n, 0.0f, s);
+                fill_dev(w->bal_col, n, (uint16_t)(4 * bp.kcw), s);  // chunk 0's zero
+                set_bal(w, bp, s);
+                int32_t* gpos = dev_alloc_copy(bp.gpos.data(), (int64_t)bp.gpos.size(), s);
+                hipLaunchKernelGGL(k_bal_pad, dim3((unsigned)bp.G), dim3(256), 0, s, (int)bp.C, (int)bp.kcw,
+                                   w->bal_meta, w->bal_cmeta, w->bal_col);
+                hipLaunchKernelGGL(k_bal_fill, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)bp.C, (int)bp.kcw,
+                                   w->bal_meta, w->bal_cmeta, w->bal_perm, gpos, w->rowptr, w->col, val, v,
+                                   w->bal_col);
+                hipError_t e = hipGetLastError();
+                (void)hipStreamSynchronize(s);
+                (void)hipFree(gpos);
+                if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_fill: ") + hipGetErrorString(e));
+            }
+        }
+        PFR_HIP(hipStreamSynchronize(s));
+        return w;
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
         free_csr(w);
         throw;
     }
@@ -483,6 +936,47 @@ int pfr_csr_from_dense(pfr_ctx* ctx, const float* dense, int64_t rows, int64_t c
             }
         }
         *out = build(ctx, M, K, rp, cl, vv.data(), PFR_F32, nullptr);
+    });
+}
+
+int pfr_csr_from_dense_dev(pfr_ctx* ctx, const float* dense, int64_t rows, int64_t cols, int transpose,
+                           float threshold, const float* mask, pfr_csr** out) {
+    return pfr::guarded([&] {
+        pfr::require(out != nullptr, "null output handle");
+        *out = nullptr;
+        pfr::bind(ctx);
+        pfr::require(rows >= 0 && cols >= 0, "negative dimension");
+        pfr::require(rows < INT32_MAX && cols < INT32_MAX, "dimension exceeds 32-bit indices");
+        pfr::require(dense != nullptr || rows * cols == 0, "null dense weight");
+        const int64_t M = transpose ? cols : rows, K = transpose ? rows : cols;
+        // one 256-thread workgroup per row; one per 32 x 32 tile for the transpose
+        pfr::require(M <= (int64_t(1) << 24) && (rows + 31) / 32 * ((cols + 31) / 32) < (int64_t(1) << 31),
+                     "weight too large for the device build");
+        if (M == 0 || K == 0) {
+            *out = build(ctx, M, K, std::vector<int32_t>((size_t)M + 1, 0), {}, nullptr, PFR_F32, nullptr);
+            return;
+        }
+        hipStream_t s = ctx->stream;
+        const float* D = dense;
+        std::unique_ptr<DevTmp> tmp;
+        if (transpose || mask) {  // op(dense * mask), row-major
+            tmp.reset(new DevTmp(sizeof(float) * (size_t)(M * K)));
+            if (transpose) {
+                const unsigned tiles = (unsigned)((rows + 31) / 32 * ((cols + 31) / 32));
+                if (mask)
+                    hipLaunchKernelGGL(k_transpose_mask<true>, dim3(tiles), dim3(256), 0, s, dense, mask, rows, cols,
+                                       tmp->as<float>());
+                else
+                    hipLaunchKernelGGL(k_transpose_mask<false>, dim3(tiles), dim3(256), 0, s, dense, mask, rows,
+                                       cols, tmp->as<float>());
+                PFR_HIP(hipGetLastError());
+            } else {
+                pfr::apply_mask_dev(s, dense, mask, M * K, tmp->as<float>());
+            }
+            D = tmp->as<float>();
+        }
+        *out = build_dense_dev(ctx, D, M, K, threshold);
+        PFR_HIP(hipStreamSynchronize(s));  // tmp is freed on return
     });
 }
 

@@ -472,6 +472,26 @@ void nm_mask_dev(pfr_ctx* ctx, const float* w, int64_t total, int n, int m, floa
     PFR_HIP(hipGetLastError());
 }
 
+// apply_mask (sparse_tensor.cpp:616-631): out[i] = w[i] * mask[i], one fp32
+// multiply per element (so NaN or inf against a 0 mask gives NaN, and -w * 0
+// gives -0, as there).  16-byte loads and stores when all three pointers
+// allow them.
+template <bool V4>
+__global__ __launch_bounds__(256) void k_apply_mask(const float* w, const float* __restrict__ m, int64_t n,
+                                                    float* out) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if constexpr (V4) {
+        const int64_t n4 = n / 4;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+            const float4 a = reinterpret_cast<const float4*>(w)[i], b = reinterpret_cast<const float4*>(m)[i];
+            reinterpret_cast<float4*>(out)[i] = make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+        }
+        for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) out[i] = w[i] * m[i];
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) out[i] = w[i] * m[i];
+    }
+}
+
 // Host-pointer form: stage, run, copy back, synchronise.
 template <class F>
 void host_mask_call(pfr_ctx* ctx, const float* w, int64_t n, float* mask, F&& f) {
@@ -487,7 +507,46 @@ void host_mask_call(pfr_ctx* ctx, const float* w, int64_t n, float* mask, F&& f)
 
 }  // namespace
 
+namespace pfr {
+void apply_mask_dev(hipStream_t s, const float* w, const float* mask, int64_t n, float* out) {
+    if (n == 0) return;
+    require(w && mask && out, "null weight, mask or output");
+    const int64_t blocks = std::min<int64_t>((n / 4 + 255) / 256 + 1, 8192);
+    const auto a = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (a(w) && a(mask) && a(out))
+        hipLaunchKernelGGL(k_apply_mask<true>, dim3((unsigned)blocks), dim3(256), 0, s, w, mask, n, out);
+    else
+        hipLaunchKernelGGL(k_apply_mask<false>, dim3((unsigned)blocks), dim3(256), 0, s, w, mask, n, out);
+    PFR_HIP(hipGetLastError());
+}
+}  // namespace pfr
+
 extern "C" {
+
+int pfr_apply_mask_dev(pfr_ctx* ctx, const float* w, const float* mask, int64_t n, float* out) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        pfr::apply_mask_dev(ctx->stream, w, mask, n, out);
+    });
+}
+
+int pfr_apply_mask(pfr_ctx* ctx, const float* w, const float* mask, int64_t n, float* out) {
+    return pfr::guarded([&] {
+        pfr::bind(ctx);
+        pfr::require(n >= 0, "negative element count");
+        if (n == 0) return;
+        pfr::require(w && mask && out, "null weight, mask or output");
+        float* dw = static_cast<float*>(ctx->scratch[0].ensure((size_t)n * 4));
+        float* dm = static_cast<float*>(ctx->scratch[1].ensure((size_t)n * 4));
+        float* dy = static_cast<float*>(ctx->scratch[2].ensure((size_t)n * 4));
+        PFR_HIP(hipMemcpyAsync(dw, w, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+        PFR_HIP(hipMemcpyAsync(dm, mask, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+        pfr::apply_mask_dev(ctx->stream, dw, dm, n, dy);
+        PFR_HIP(hipMemcpyAsync(out, dy, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+        PFR_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
 
 int pfr_magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask) {
     return pfr::guarded([&] {

@@ -695,6 +695,210 @@ pfr_sp24* pack_bf16(pfr_ctx* ctx, int64_t M, int64_t K, const uint16_t* W) {
     }
 }
 
+// ---- Packing a weight already on the device -------------------------------
+// The same layouts as pack_i8 / pack_bf16, written by one thread per
+// (16-row tile, k tile, lane) from a device weight; the 2:4 check reports
+// the first offending group (row-major order) through an atomic minimum.
+
+template <class T>
+__device__ __forceinline__ bool sp24_nz(T v) {
+    if constexpr (sizeof(T) == 1) return v != 0;
+    else return (v & 0x7FFF) != 0;  // bf16: +0 and -0 are zeros
+}
+
+// The two kept positions of a 4-group (ascending), as pick2 chooses them.
+__device__ __forceinline__ void pick2_dev(unsigned nzmask, int* p0, int* p1) {
+    const int n = __popc(nzmask);
+    if (n >= 2) {
+        *p0 = __ffs(nzmask) - 1;
+        *p1 = __ffs(nzmask & (nzmask - 1)) - 1;
+    } else if (n == 1) {
+        const int p = __ffs(nzmask) - 1;
+        *p0 = 0;
+        *p1 = p == 0 ? 1 : p;
+    } else {
+        *p0 = 0;
+        *p1 = 1;
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T sp24_at(const T* __restrict__ W, int64_t M, int64_t K, int64_t r, int64_t k) {
+    return (r < M && k < K) ? W[r * K + k] : T(0);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void k_sp24_check(const T* __restrict__ W, int64_t M, int64_t K, int64_t ng,
+                                                    unsigned long long* __restrict__ first_bad) {
+    const int64_t n = M * ng;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / ng, k = (i % ng) * 4;
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c += sp24_nz(sp24_at(W, M, K, r, k + t)) ? 1 : 0;
+        if (c > 2) atomicMin(first_bad, (unsigned long long)i);
+    }
+}
+
+// int8: thread (mt, kt, l) writes the 16 kept bytes and the index word of
+// lane l's fragment: groups g = 0..7 at k = kt * 128 + 32 * (l >> 4) + 4 g of
+// row mt * 16 + (l & 15).
+__global__ __launch_bounds__(256) void k_sp24_pack_i8(const int8_t* __restrict__ W, int64_t M, int64_t K,
+                                                      int64_t nmt, int64_t nkt, int4* __restrict__ a,
+                                                      uint32_t* __restrict__ ix) {
+    const int64_t n = nmt * nkt * 64;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int l = (int)(i & 63);
+        const int64_t kt = (i >> 6) % nkt, mt = (i >> 6) / nkt;
+        const int64_t r = mt * 16 + (l & 15);
+        uint32_t word = 0, b[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int64_t ks = kt * 128 + 32 * (l >> 4) + 4 * g;
+            int8_t v[4];
+            unsigned nz = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] = sp24_at(W, M, K, r, ks + t);
+                nz |= (v[t] != 0 ? 1u : 0u) << t;
+            }
+            int p0, p1;
+            pick2_dev(nz, &p0, &p1);
+            const uint32_t pair = (uint32_t)(uint8_t)v[p0] | ((uint32_t)(uint8_t)v[p1] << 8);
+            b[g / 2] |= pair << (16 * (g % 2));
+            word |= (uint32_t)(p0 | (p1 << 2)) << (4 * g);
+        }
+        a[i] = make_int4((int)b[0], (int)b[1], (int)b[2], (int)b[3]);
+        ix[i] = word;
+    }
+}
+
+// bf16: thread (mt, kp, l) writes lane l's two fragments of k tiles 2 kp and
+// 2 kp + 1 (8 kept values each) and their shared index word (low half: the
+// even tile).
+__global__ __launch_bounds__(256) void k_sp24_pack_bf16(const uint16_t* __restrict__ W, int64_t M, int64_t K,
+                                                        int64_t nmt, int64_t nkp, int4* __restrict__ a,
+                                                        uint32_t* __restrict__ ix) {
+    const int64_t n = nmt * nkp * 64, nkt = 2 * nkp;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int l = (int)(i & 63);
+        const int64_t kp = (i >> 6) % nkp, mt = (i >> 6) / nkp;
+        const int64_t r = mt * 16 + (l & 15);
+        uint32_t word = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t kt = 2 * kp + h;
+            uint32_t b[4] = {0, 0, 0, 0}, half = 0;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t ks = kt * 64 + 16 * (l >> 4) + 4 * g;
+                uint16_t v[4];
+                unsigned nz = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    v[t] = sp24_at(W, M, K, r, ks + t);
+                    nz |= (sp24_nz(v[t]) ? 1u : 0u) << t;
+                }
+                int p0, p1;
+                pick2_dev(nz, &p0, &p1);
+                b[g] = (uint32_t)v[p0] | ((uint32_t)v[p1] << 16);
+                half |= (uint32_t)(p0 | (p1 << 2)) << (4 * g);
+            }
+            a[(mt * nkt + kt) * 64 + l] = make_int4((int)b[0], (int)b[1], (int)b[2], (int)b[3]);
+            word |= half << (16 * h);
+        }
+        ix[i] = word;
+    }
+}
+
+// Row sums of an int8 weight (the zero-point correction), one workgroup per
+// row.
+__global__ __launch_bounds__(256) void k_sp24_row_sum(const int8_t* __restrict__ W, int64_t K,
+                                                      int32_t* __restrict__ rs) {
+    __shared__ int part[4];
+    const int64_t r = blockIdx.x;
+    int sum = 0;
+    for (int64_t k = threadIdx.x; k < K; k += 256) sum += W[r * K + k];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) rs[r] = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 8192); }
+
+pfr_sp24* pack_dev(pfr_ctx* ctx, int64_t M, int64_t K, const void* Wv, pfr_dtype dtype) {
+    hipStream_t s = ctx->stream;
+    const bool i8 = dtype == PFR_I8;
+    const int64_t Mp = round_up(M, kPadM), Kp = i8 ? round_up(K, 512) : round_up(K, 128);
+    // the 2:4 check over every 4-group of the padded rows (the padding is zero)
+    {
+        unsigned long long* bad = nullptr;
+        PFR_HIP(hipMalloc(&bad, sizeof(unsigned long long)));
+        const unsigned long long none = ~0ull;
+        unsigned long long first = none;
+        hipError_t e = hipMemcpyAsync(bad, &none, sizeof(none), hipMemcpyHostToDevice, s);
+        const int64_t ng = Kp / 4;
+        if (e == hipSuccess && M > 0) {
+            if (i8)
+                hipLaunchKernelGGL(k_sp24_check<int8_t>, dim3(grid_for(M * ng)), dim3(256), 0, s,
+                                   static_cast<const int8_t*>(Wv), M, K, ng, bad);
+            else
+                hipLaunchKernelGGL(k_sp24_check<uint16_t>, dim3(grid_for(M * ng)), dim3(256), 0, s,
+                                   static_cast<const uint16_t*>(Wv), M, K, ng, bad);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipMemcpyAsync(&first, bad, sizeof(first), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        (void)hipFree(bad);
+        if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("2:4 check: ") + hipGetErrorString(e));
+        if (first != none) {
+            const int64_t r = (int64_t)(first / (unsigned long long)ng), k = (int64_t)(first % (unsigned long long)ng) * 4;
+            throw pfr::Error(PFR_ERR_INVALID_ARG, "weight is not 2:4 sparse: row " + std::to_string(r) + ", k " +
+                                                      std::to_string(k) + ".." + std::to_string(k + 3) +
+                                                      " has more than two nonzeros");
+        }
+    }
+    auto* w = new pfr_sp24();
+    try {
+        w->ctx = ctx;
+        w->M = M;
+        w->K = K;
+        w->Mp = Mp;
+        w->Kp = Kp;
+        w->dtype = dtype;
+        const int64_t nmt = Mp / 16;
+        if (i8) {
+            const int64_t nkt = Kp / 128;
+            PFR_HIP(hipMalloc(&w->a, (size_t)(nmt * nkt * 64 * 16)));
+            PFR_HIP(hipMalloc(&w->idx, (size_t)(nmt * nkt * 64 * 4)));
+            PFR_HIP(hipMalloc(&w->row_sum, (size_t)Mp * 4));
+            hipLaunchKernelGGL(k_sp24_pack_i8, dim3(grid_for(nmt * nkt * 64)), dim3(256), 0, s,
+                               static_cast<const int8_t*>(Wv), M, K, nmt, nkt, static_cast<int4*>(w->a), w->idx);
+            PFR_HIP(hipMemcpyAsync(w->row_sum, std::vector<int32_t>((size_t)Mp, 0).data(), (size_t)Mp * 4,
+                                   hipMemcpyHostToDevice, s));
+            PFR_HIP(hipStreamSynchronize(s));  // the zero vector is a temporary
+            if (M > 0 && K > 0)
+                hipLaunchKernelGGL(k_sp24_row_sum, dim3((unsigned)M), dim3(256), 0, s,
+                                   static_cast<const int8_t*>(Wv), K, w->row_sum);
+        } else {
+            const int64_t nkp = Kp / 128;
+            PFR_HIP(hipMalloc(&w->a, (size_t)(nmt * 2 * nkp * 64 * 16)));
+            PFR_HIP(hipMalloc(&w->idx, (size_t)(nmt * nkp * 64 * 4)));
+            hipLaunchKernelGGL(k_sp24_pack_bf16, dim3(grid_for(nmt * nkp * 64)), dim3(256), 0, s,
+                               static_cast<const uint16_t*>(Wv), M, K, nmt, nkp, static_cast<int4*>(w->a), w->idx);
+        }
+        PFR_HIP(hipGetLastError());
+        PFR_HIP(hipStreamSynchronize(s));
+        return w;
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
+        free_sp24(w);
+        throw;
+    }
+}
+
 void check_i8(const pfr_sp24* W) {
     pfr::require(W != nullptr, "null 2:4 weight handle");
     if (W->dtype != PFR_I8) throw pfr::Error(PFR_ERR_UNSUPPORTED, "weight is not int8");
@@ -873,10 +1077,12 @@ void gemm_bf16_dev(pfr_ctx* ctx, const pfr_sp24* W, const uint16_t* X, int64_t N
 
 }  // namespace
 
-extern "C" {
-
-int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype dtype, const float* w_scales,
-                  int64_t n_scales, pfr_sp24** out) {
+namespace {
+// Shared by both pack entry points: argument checks, the packing itself
+// (host or device weight) and the per-row scales.
+template <class Pack>
+int sp24_pack_any(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype dtype, const float* w_scales,
+                  int64_t n_scales, pfr_sp24** out, Pack&& pack) {
     return pfr::guarded([&] {
         pfr::require(out != nullptr, "null output handle");
         *out = nullptr;
@@ -894,8 +1100,7 @@ int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype d
                 scales[(size_t)m] = s;
             }
         }
-        pfr_sp24* w = dtype == PFR_I8 ? pack_i8(ctx, M, K, static_cast<const int8_t*>(W))
-                                      : pack_bf16(ctx, M, K, static_cast<const uint16_t*>(W));
+        pfr_sp24* w = pack();
         for (float v : scales) w->w_scale_max = std::max(w->w_scale_max, v);
         try {
             PFR_HIP(hipMalloc(&w->w_scale, sizeof(float) * (size_t)(M > 0 ? M : 1)));
@@ -906,6 +1111,23 @@ int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype d
         }
         *out = w;
     });
+}
+}  // namespace
+
+extern "C" {
+
+int pfr_sp24_pack(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype dtype, const float* w_scales,
+                  int64_t n_scales, pfr_sp24** out) {
+    return sp24_pack_any(ctx, M, K, W, dtype, w_scales, n_scales, out, [&] {
+        return dtype == PFR_I8 ? pack_i8(ctx, M, K, static_cast<const int8_t*>(W))
+                               : pack_bf16(ctx, M, K, static_cast<const uint16_t*>(W));
+    });
+}
+
+int pfr_sp24_pack_dev(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype dtype, const float* w_scales,
+                      int64_t n_scales, pfr_sp24** out) {
+    return sp24_pack_any(ctx, M, K, W, dtype, w_scales, n_scales, out,
+                         [&] { return pack_dev(ctx, M, K, W, dtype); });
 }
 
 int pfr_sp24_info(const pfr_sp24* w, int64_t* M, int64_t* K, pfr_dtype* dtype) {

@@ -87,6 +87,40 @@ class Context:
                                            threshold, C.byref(h)))
         return CsrWeight(self, h)
 
+    def csr_from_dense_dev(self, dense_ptr, rows, cols, transpose=False, threshold=0.0, mask_ptr=None):
+        """CSR of op(dense * mask) built on the device from device pointers
+        (pfr_csr_from_dense_dev); mask_ptr None: no mask."""
+        h = C.c_void_p()
+        check(self._lib.pfr_csr_from_dense_dev(self.handle, dense_ptr, rows, cols, int(bool(transpose)),
+                                               threshold, mask_ptr, C.byref(h)))
+        return CsrWeight(self, h)
+
+    def sp24_pack_dev(self, W_ptr, M, K, dtype, w_scales=None):
+        """2:4 weight [M, K] on the device: dtype "i8" (with 1 or M host
+        scales) or "bf16" (pfr_sp24_pack_dev)."""
+        h = C.c_void_p()
+        if dtype == "i8":
+            sc = np.ascontiguousarray(np.atleast_1d(w_scales), np.float32)
+            check(self._lib.pfr_sp24_pack_dev(self.handle, M, K, W_ptr, PFR_I8, _ptr(sc), sc.size, C.byref(h)))
+        elif dtype == "bf16":
+            check(self._lib.pfr_sp24_pack_dev(self.handle, M, K, W_ptr, PFR_BF16, None, 0, C.byref(h)))
+        else:
+            raise TypeError("2:4 weights are int8 or bf16")
+        return Sp24Weight(self, h)
+
+    def apply_mask(self, w, mask):
+        """apply_mask on the GPU: w * mask elementwise (float32)."""
+        w = np.ascontiguousarray(w, np.float32)
+        mask = np.ascontiguousarray(mask, np.float32)
+        if w.size != mask.size:
+            raise ValueError("Tensor and mask must have same number of elements")
+        out = np.empty_like(w)
+        check(self._lib.pfr_apply_mask(self.handle, _ptr(w), _ptr(mask), w.size, _ptr(out)))
+        return out
+
+    def apply_mask_dev(self, w_ptr, mask_ptr, n, out_ptr):
+        check(self._lib.pfr_apply_mask_dev(self.handle, w_ptr, mask_ptr, n, out_ptr))
+
     def sp24_pack(self, W, w_scales=None):
         """2:4 weight [M, K]: int8 (with 1 or M symmetric scales) or bf16 bits
         (uint16)."""
