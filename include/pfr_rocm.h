@@ -133,6 +133,18 @@ int pfr_csr_from_dense(pfr_ctx* ctx, const float* dense, int64_t rows,
 int pfr_csr_from_dense_dev(pfr_ctx* ctx, const float* dense, int64_t rows,
                            int64_t cols, int transpose, float threshold,
                            const float* mask, pfr_csr** out);
+/* Give the handle the dense kernels' treatment of non-finite activations
+ * (cpu_matmul / cpu_gemm, math.cpp:268-438, on the zero-filled weight), for
+ * a CSR that stands in for a dense initializer: those kernels multiply every
+ * activation by every weight, so an inf or NaN activation meets the zeros
+ * the CSR does not store (inf * 0 = NaN), which sparse_matmul
+ * (sparse_tensor.cpp:473-519) skips.  Builds a bitmap of the stored entries
+ * (M x ceil(K / 64) words); from then on every product through the handle
+ * is followed by a fix-up pass over the activations that writes NaN (through
+ * the bias and activation epilogue) where an inf activation meets an
+ * unstored weight or a NaN activation meets any weight of an output.  For
+ * finite activations results are unchanged.  Idempotent. */
+int pfr_csr_dense_semantics(pfr_csr* w);
 int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz);
 int pfr_csr_free(pfr_csr* w);
 
@@ -196,6 +208,21 @@ int pfr_gemm_csr_act_noalloc_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64
                                  int transA, const pfr_csr* BT, float alpha, float beta,
                                  const float* C, int64_t c_size, float* Y, int mode,
                                  int act);
+
+/* ---- Dense products (weights above the sparse path's density gate) -------- */
+
+/* cpu_gemm / cpu_matmul (math.cpp:268-438) on dense float32 operands:
+ *   Y[i, j] = act(sum_k (alpha * op(A)[i, k]) * B[k, j] + beta * C[(i*N + j) % c_size])
+ * op(A) = A (M x K) or, with transA, A^T (A is K x M); B is K x N with row
+ * stride ldb; Y rows are ldy floats apart; C may be NULL.  Each output sums
+ * its terms in ascending k from +0 with separate multiply and add, as the
+ * reference loops do, so results are bit-identical to cpu_gemm (and, with
+ * alpha = 1 and no C, to cpu_matmul), non-finite values included.  act as
+ * in pfr_spmm_csr_act_dev.  Device pointers, the context's stream. */
+int pfr_gemm_dense_dev(pfr_ctx* ctx, const float* A, int64_t M, int64_t K,
+                       int transA, const float* B, int64_t N, int64_t ldb,
+                       float alpha, float beta, const float* C, int64_t c_size,
+                       float* Y, int64_t ldy, int act);
 
 /* ---- 2:4 structured weights (sparse MFMA, gfx950 smfmac) ------------------- */
 

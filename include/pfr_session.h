@@ -62,6 +62,12 @@ int pfr_session_supported_ops(pfr_session* s, char* buf, int64_t cap);
  * nodes, a Relu that is a product's only consumer fused into the product),
  * with *steps its kernel launches; 0 and 0 when it runs node by node. */
 int pfr_session_device_plan(pfr_session* s, int* device_resident, int* steps);
+/* After a run: how many Gemm / MatMul / QuantizedMatMul weights went to the
+ * device as CSR (float32 initializers with at most half their entries
+ * nonzero, and CSR records), as dense matrices (denser float32
+ * initializers), and as 2:4 int8.  No reference counterpart (the CPU
+ * backend keeps every weight as it is). */
+int pfr_session_weight_forms(pfr_session* s, int* csr, int* dense, int* sp24);
 
 /* Host-side model utilities (no device needed).  pfr_model_describe loads
  * and validates a .pfm with this runtime's loader and writes a JSON summary

@@ -56,6 +56,8 @@ SIGNATURES = {
     "pfr_nm_mask_dev": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
     "pfr_csr_from_dense": (_INT, [_P, _P, _I64, _I64, _INT, _F, _PP]),
     "pfr_csr_from_dense_dev": (_INT, [_P, _P, _I64, _I64, _INT, _F, _P, _PP]),
+    "pfr_csr_dense_semantics": (_INT, [_P]),
+    "pfr_gemm_dense_dev": (_INT, [_P, _P, _I64, _I64, _INT, _P, _I64, _I64, _F, _F, _P, _I64, _P, _I64, _INT]),
     "pfr_apply_mask": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_apply_mask_dev": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_csr_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),

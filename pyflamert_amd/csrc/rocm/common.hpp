@@ -66,6 +66,20 @@ __device__ __forceinline__ float gelu(float v) {
     return 0.5f * v * (1.0f + tanhf(inner));
 }
 
+// Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size],
+// then optionally a fused Relu (activation.cpp:45-60: std::max(0.0f, v), which
+// is (0 < v) ? v : +0, so -0 and NaN give +0) or Gelu (activation.cpp:239-259).
+__device__ __forceinline__ float bias_add(float v, int64_t f, const float* __restrict__ bias,
+                                          int64_t c_size, float beta, int act) {
+    if (bias != nullptr) {
+        const float t = beta * bias[f % c_size];
+        v = v + t;
+    }
+    if (act == PFR_ACT_RELU) v = (0.0f < v) ? v : 0.0f;
+    else if (act == PFR_ACT_GELU) v = pfr::gelu(v);
+    return v;
+}
+
 // Grow-only device buffer owned by a context.
 struct DevBuf {
     void* p = nullptr;
@@ -172,6 +186,13 @@ struct pfr_csr {
     void* bal_val = nullptr;
     uint16_t* bal_col = nullptr;
     int32_t bal_ngroup = 0, bal_nchunk = 0, bal_kcw = 0;
+    // Stored-entry bitmap (set by pfr_csr_dense_semantics): bit k % 64 of
+    // pattern[r * pattern_nw + k / 64] is set when row r stores column k.
+    // While it is set, every product through the handle is followed by the
+    // non-finite fix-up, which gives the dense kernels' results where an inf
+    // or NaN activation meets a weight the CSR does not store (a zero).
+    uint64_t* pattern = nullptr;
+    int64_t pattern_nw = 0;
 };
 
 namespace pfr {

@@ -36,7 +36,7 @@ void free_csr(pfr_csr* w) {
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
                     (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0, (void*)w->col16,
                     (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col, (void*)w->bal_meta,
-                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col})
+                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col, (void*)w->pattern})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -722,6 +722,18 @@ unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
 // The CSR handle of D (M x K, row-major, device), with every derived copy
 // the upload path would build, from counts copied back to the host and
 // fills on the device.
+// Stored-entry bitmap: one wave per row sets the bit of every stored column.
+__global__ __launch_bounds__(256) void k_pattern(int64_t M, const int32_t* __restrict__ rowptr,
+                                                 const int32_t* __restrict__ col, int64_t nw,
+                                                 unsigned long long* __restrict__ bm) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= M) return;
+    for (int32_t j = rowptr[r] + (int32_t)(threadIdx.x & 63); j < rowptr[r + 1]; j += 64) {
+        const int32_t k = col[j];
+        atomicOr(&bm[r * nw + k / 64], 1ull << (k % 64));
+    }
+}
+
 pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, float thr) {
     hipStream_t s = ctx->stream;
     int64_t kc, nchs;
@@ -977,6 +989,32 @@ int pfr_csr_from_dense_dev(pfr_ctx* ctx, const float* dense, int64_t rows, int64
         }
         *out = build_dense_dev(ctx, D, M, K, threshold);
         PFR_HIP(hipStreamSynchronize(s));  // tmp is freed on return
+    });
+}
+
+int pfr_csr_dense_semantics(pfr_csr* w) {
+    return pfr::guarded([&] {
+        pfr::require(w != nullptr, "null CSR handle");
+        pfr::bind(w->ctx);
+        if (w->pattern != nullptr || w->M == 0 || w->K == 0) return;
+        const int64_t nw = (w->K + 63) / 64;
+        hipStream_t s = w->ctx->stream;
+        auto* bm = dev_alloc<unsigned long long>(w->M * nw);
+        try {
+            fill_dev(bm, w->M * nw, 0ull, s);
+            if (w->nnz > 0) {
+                hipLaunchKernelGGL(k_pattern, dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, w->rowptr, w->col, nw,
+                                   bm);
+                PFR_HIP(hipGetLastError());
+            }
+            PFR_HIP(hipStreamSynchronize(s));
+        } catch (...) {
+            (void)hipStreamSynchronize(s);
+            (void)hipFree(bm);
+            throw;
+        }
+        w->pattern = reinterpret_cast<uint64_t*>(bm);
+        w->pattern_nw = nw;
     });
 }
 

@@ -26,6 +26,8 @@ static __device__ __align__(256) float scratch[kNoAllocFloats];
 
 namespace {
 
+using pfr::bias_add;
+
 constexpr int kWaves = 4;  // waves per 256-thread workgroup
 constexpr int kSpmvThreads = 512;  // threads of the vector kernel's workgroup
 constexpr int kSpmvCap = 4096;     // products staged per workgroup chunk (16 KB)
@@ -53,19 +55,6 @@ __device__ __forceinline__ float wval(const void* __restrict__ val, const float*
     }
 }
 
-// Bias epilogue of cpu_gemm (math.cpp:431-433): out[f] += beta * c[f % c_size],
-// then optionally a fused Relu (activation.cpp:45-60: std::max(0.0f, v), which
-// is (0 < v) ? v : +0, so -0 and NaN give +0) or Gelu (activation.cpp:239-259).
-__device__ __forceinline__ float bias_add(float v, int64_t f, const float* __restrict__ bias,
-                                          int64_t c_size, float beta, int act) {
-    if (bias != nullptr) {
-        const float t = beta * bias[f % c_size];
-        v = v + t;
-    }
-    if (act == PFR_ACT_RELU) v = (0.0f < v) ? v : 0.0f;
-    else if (act == PFR_ACT_GELU) v = pfr::gelu(v);
-    return v;
-}
 
 // One wave per CSR row, lanes across the N columns (4 per lane when VEC).
 // Output element (row, c) goes to Y[row * ldy_r + c * ldy_c].
@@ -1642,6 +1631,46 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     }
 }
 
+// Non-finite fix-up for a handle with the stored-entry bitmap: the dense
+// kernels (math.cpp:268-438) multiply every activation by every weight, so
+// x[k, c] = NaN makes output column c NaN in every row, and x[k, c] = +-inf
+// makes (row, c) NaN wherever row does not store k (inf * 0); the sparse
+// kernels skip those terms.  One workgroup per 64 x 64 tile of X (k x c),
+// read coalesced into LDS; a wave per column reduces its 64 k to a NaN flag
+// and an inf mask (ballots), and only a column with either walks the rows,
+// writing the epilogue of NaN (bias and activation as the product kernels
+// apply them) where the rule says so.  Columns without non-finite values --
+// the normal case -- cost one read of X.
+__global__ __launch_bounds__(256) void k_nonfinite_fix(const float* __restrict__ X, int64_t ldx, int64_t K,
+                                                       int64_t N, int64_t M, const uint64_t* __restrict__ bm,
+                                                       int64_t nw, float* __restrict__ Y, int64_t ldy_r,
+                                                       int64_t ldy_c, const float* __restrict__ bias,
+                                                       int64_t c_size, float beta, int act) {
+    __shared__ float t[64][65];  // t[c][k]
+    const int64_t kt = blockIdx.x, k0 = kt * 64, c0 = (int64_t)blockIdx.y * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+        const int cc = e % 64, kk = e / 64;
+        const int64_t k = k0 + kk, c = c0 + cc;
+        t[cc][kk] = (k < K && c < N) ? X[k * ldx + c] : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float qnan = __builtin_nanf("");
+    for (int cc = wave; cc < 64 && c0 + cc < N; cc += 4) {
+        const float v = t[cc][lane];
+        const bool nan = __ballot(v != v) != 0;
+        const uint64_t inf = __ballot(__builtin_isinf(v));
+        if (!nan && inf == 0) continue;
+        const int64_t c = c0 + cc;
+        for (int64_t r = lane; r < M; r += 64) {
+            if (nan || (inf & ~bm[r * nw + kt]) != 0) {
+                const int64_t f = r * ldy_r + c * ldy_c;
+                Y[f] = bias_add(qnan, f, bias, c_size, beta, act);
+            }
+        }
+    }
+}
+
 // Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
 void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
                  int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
@@ -1658,6 +1687,13 @@ void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int6
         else launch_csr_kernels<false, false>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     }
     PFR_HIP(hipGetLastError());
+    if (W->pattern != nullptr && W->K > 0) {
+        pfr::require((N + 63) / 64 < 65536, "too many columns for the non-finite fix-up's grid");
+        const dim3 grid((unsigned)((W->K + 63) / 64), (unsigned)((N + 63) / 64));
+        hipLaunchKernelGGL(k_nonfinite_fix, grid, dim3(256), 0, ctx->stream, X, ldx, W->K, N, W->M, W->pattern,
+                           W->pattern_nw, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        PFR_HIP(hipGetLastError());
+    }
 }
 
 void check_csr(const pfr_csr* W) {

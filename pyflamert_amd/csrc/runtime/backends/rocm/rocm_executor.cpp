@@ -119,6 +119,7 @@ void RocmExecutor::release_weights() {
     for (auto& kv : weights_) {
         if (kv.second.csr) pfr_csr_free(kv.second.csr);
         if (kv.second.sp24) pfr_sp24_free(kv.second.sp24);
+        if (kv.second.dense) pfr_dev_free(ctx_, kv.second.dense);
     }
     weights_.clear();
     for (auto& kv : constants_) pfr_dev_free(ctx_, kv.second.p);
@@ -157,7 +158,7 @@ const Tensor& RocmExecutor::initializer_value(const Graph& graph, const std::str
 void RocmExecutor::prepare_sparse_views(const Graph& graph) {
     for (const auto& kv : weights_) {
         const Node* n = kv.first;
-        const int slot = kv.second.kind == DeviceWeight::CsrB || kv.second.kind == DeviceWeight::Sp24B ? 1 : 0;
+        const int slot = kv.second.second() ? 1 : 0;
         const std::string& nm = n->inputs()[(size_t)slot];
         const SparseInitializer* s = graph.get_sparse_initializer(nm);
         if (s && !sparse_views_.count(nm))
@@ -267,6 +268,77 @@ std::vector<float> weight_scales_b(const Node& n, int64_t cols) {
 }
 }  // namespace
 
+// The device form of a float32 initializer weight W (rows x cols) of a
+// Gemm / MatMul: the product's second operand B (op(B) = W, or W^T with
+// transB), or its first operand A.  The density gate picks the form:
+// - at most kSparseDensityGate nonzero: a CSR (of op(B)^T, or of A) that
+//   drops the zeros, with the dense kernels' non-finite rules switched on
+//   (pfr_csr_dense_semantics) and NaN weights kept as stored entries, so
+//   every result equals cpu_gemm / cpu_matmul on W;
+// - denser: W itself for the dense product (op(B) made K x N row-major).
+RocmExecutor::DeviceWeight RocmExecutor::dense_initializer_weight(const Tensor& W, bool second, bool transB) {
+    const int64_t rows = W.shape()[0], cols = W.shape()[1];
+    const float* d = W.data_ptr<float>();
+    int64_t nnz = 0;
+    bool nan = false;
+    for (int64_t i = 0; i < rows * cols; ++i) {
+        nnz += d[i] != 0.0f || d[i] != d[i];
+        nan = nan || d[i] != d[i];
+    }
+    DeviceWeight w;
+    const bool sparse = rows * cols == 0 || (double)nnz <= kSparseDensityGate * (double)(rows * cols);
+    if (sparse) {
+        // CSR rows: output features (op(B)^T) for B, rows of A for A
+        const bool tr = second && !transB;  // B given K x N: its CSR is of W^T
+        const int64_t M = tr ? cols : rows, K = tr ? rows : cols;
+        auto at = [&](int64_t r, int64_t c) { return tr ? d[c * cols + r] : d[r * cols + c]; };
+        if (!nan) {
+            pfr_check(pfr_csr_from_dense(ctx_, d, rows, cols, tr ? 1 : 0, 0.0f, &w.csr));
+        } else {  // to_sparse drops NaN (|NaN| > 0 fails); the dense kernels multiply it
+            std::vector<int64_t> ip((size_t)M + 1, 0), ix;
+            std::vector<float> v;
+            ix.reserve((size_t)nnz);
+            v.reserve((size_t)nnz);
+            for (int64_t r = 0; r < M; ++r) {
+                for (int64_t c = 0; c < K; ++c) {
+                    const float x = at(r, c);
+                    if (x != 0.0f || x != x) {
+                        ix.push_back(c);
+                        v.push_back(x);
+                    }
+                }
+                ip[(size_t)r + 1] = (int64_t)ix.size();
+            }
+            pfr_check(pfr_csr_upload(ctx_, M, K, (int64_t)v.size(), ip.data(), ix.data(), v.data(), PFR_F32, nullptr,
+                                     &w.csr));
+        }
+        w.kind = second ? DeviceWeight::CsrB : DeviceWeight::CsrA;
+        pfr_check(pfr_csr_dense_semantics(w.csr));
+        return w;
+    }
+    // dense: B as op(B) (K x N), A as is (M x K)
+    std::vector<float> t;
+    const float* src = d;
+    if (second && transB) {  // B is N x K
+        t.resize((size_t)(rows * cols));
+        for (int64_t n = 0; n < rows; ++n)
+            for (int64_t k = 0; k < cols; ++k) t[(size_t)(k * rows + n)] = d[n * cols + k];
+        src = t.data();
+    }
+    void* p = nullptr;
+    pfr_check(pfr_dev_alloc(ctx_, rows * cols * 4, &p));
+    w.dense = static_cast<float*>(p);
+    w.kind = second ? DeviceWeight::DenseB : DeviceWeight::DenseA;
+    try {
+        pfr_check(pfr_copy_to_device(ctx_, p, src, rows * cols * 4));
+        pfr_check(pfr_synchronize(ctx_));
+    } catch (...) {
+        pfr_dev_free(ctx_, p);
+        throw;
+    }
+    return w;
+}
+
 void RocmExecutor::prepare(const Graph& graph) {
     if (prepared_for_ == &graph) return;
     release_weights();
@@ -283,17 +355,22 @@ void RocmExecutor::prepare(const Graph& graph) {
         auto csr_rec = [&](size_t i) { return sparse(i) && sparse(i)->format == SparseInitializer::Csr; };
         DeviceWeight w;
         try {
+            // A CSR record stands for the zero-filled weight it was written
+            // from, so its products keep the dense kernels' non-finite rules.
             if (n->op_type() == "Gemm" && csr_rec(1)) {
                 // B stored K x N (transB 0) or N x K: the device weight is op(B)^T
                 const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
                 w.csr = upload_sparse_csr(ctx_, *sparse(1), !tb);
                 w.kind = DeviceWeight::CsrB;
+                pfr_check(pfr_csr_dense_semantics(w.csr));
             } else if (n->op_type() == "MatMul" && csr_rec(1)) {
                 w.csr = upload_sparse_csr(ctx_, *sparse(1), true);
                 w.kind = DeviceWeight::CsrB;
+                pfr_check(pfr_csr_dense_semantics(w.csr));
             } else if (n->op_type() == "MatMul" && csr_rec(0) && !init(1) && !sparse(1)) {
                 w.csr = upload_sparse_csr(ctx_, *sparse(0), false);
                 w.kind = DeviceWeight::CsrA;
+                pfr_check(pfr_csr_dense_semantics(w.csr));
             } else if (n->op_type() == "QuantizedMatMul" && sparse(0) &&
                        sparse(0)->format == SparseInitializer::Nm24 && n->get_attr<int64_t>("a_zero_point", 0) == 0) {
                 // expanded for the packer only; the record is 2:4 by construction
@@ -303,19 +380,11 @@ void RocmExecutor::prepare(const Graph& graph) {
                                         (int64_t)sc.size(), &w.sp24));
                 w.kind = DeviceWeight::Sp24A;
             } else if (n->op_type() == "Gemm" && init(1) && is_f32_matrix(*init(1))) {
-                const Tensor& B = *init(1);
-                const bool tb = n->get_attr<int64_t>("transB", 0) != 0;
-                pfr_check(pfr_csr_from_dense(ctx_, B.data_ptr<float>(), B.shape()[0], B.shape()[1], tb ? 0 : 1, 0.0f,
-                                             &w.csr));
-                w.kind = DeviceWeight::CsrB;
+                w = dense_initializer_weight(*init(1), true, n->get_attr<int64_t>("transB", 0) != 0);
             } else if (n->op_type() == "MatMul" && init(1) && is_f32_matrix(*init(1))) {
-                const Tensor& B = *init(1);
-                pfr_check(pfr_csr_from_dense(ctx_, B.data_ptr<float>(), B.shape()[0], B.shape()[1], 1, 0.0f, &w.csr));
-                w.kind = DeviceWeight::CsrB;
+                w = dense_initializer_weight(*init(1), true, false);
             } else if (n->op_type() == "MatMul" && init(0) && !init(1) && is_f32_matrix(*init(0))) {
-                const Tensor& A = *init(0);
-                pfr_check(pfr_csr_from_dense(ctx_, A.data_ptr<float>(), A.shape()[0], A.shape()[1], 0, 0.0f, &w.csr));
-                w.kind = DeviceWeight::CsrA;
+                w = dense_initializer_weight(*init(0), false, false);
             } else if (n->op_type() == "QuantizedMatMul" && !init(0) && !sparse(0) &&
                        ((sparse(1) && sparse(1)->format == SparseInitializer::Nm24) ||
                         (init(1) && init(1)->ndim() == 2 &&
@@ -380,11 +449,11 @@ void RocmExecutor::build_plan(const Graph& graph) {
         if (!dynq && n->outputs().size() != 1) return;
         const DeviceWeight* w = weight(n);
         PlanStep st{PlanStep::Relu, n, PFR_ACT_NONE, n->outputs()[0]};
-        if (op == "Gemm" && w && w->kind == DeviceWeight::CsrB)
+        if (op == "Gemm" && w && (w->kind == DeviceWeight::CsrB || w->kind == DeviceWeight::DenseB))
             st.op = PlanStep::Gemm;
-        else if (op == "MatMul" && w && w->kind == DeviceWeight::CsrB)
+        else if (op == "MatMul" && w && (w->kind == DeviceWeight::CsrB || w->kind == DeviceWeight::DenseB))
             st.op = PlanStep::MatMulB;
-        else if (op == "MatMul" && w && w->kind == DeviceWeight::CsrA)
+        else if (op == "MatMul" && w && (w->kind == DeviceWeight::CsrA || w->kind == DeviceWeight::DenseA))
             st.op = PlanStep::MatMulA;
         else if (op == "QuantizedMatMul" && w && w->kind == DeviceWeight::Sp24A)
             st.op = PlanStep::QMatMul;
@@ -526,9 +595,14 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                 }
                 out.shape = {M, N};
                 out.p = device_buffer(st.out, M * N * 4);
-                pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), M, Ka, (int)ta,
-                                               weight(n)->csr, alpha, beta, c, c_size, static_cast<float*>(out.p),
-                                               math_mode_, act));
+                const DeviceWeight* w = weight(n);
+                if (w->kind == DeviceWeight::DenseB)
+                    pfr_check(pfr_gemm_dense_dev(ctx_, static_cast<const float*>(A.p), M, Ka, (int)ta, w->dense, N, N,
+                                                 alpha, beta, c, c_size, static_cast<float*>(out.p), N, act));
+                else
+                    pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), M, Ka, (int)ta, w->csr,
+                                                   alpha, beta, c, c_size, static_cast<float*>(out.p), math_mode_,
+                                                   act));
                 break;
             }
             case PlanStep::MatMulB:
@@ -552,9 +626,14 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                     const int64_t rows = numel(out.shape);
                     out.shape.push_back(N);
                     out.p = device_buffer(st.out, rows * N * 4);
-                    pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), rows, Ka, 0, weight(n)->csr,
-                                                   1.0f, 1.0f, nullptr, 0, static_cast<float*>(out.p), math_mode_,
-                                                   act));
+                    const DeviceWeight* w = weight(n);
+                    if (w->kind == DeviceWeight::DenseB)
+                        pfr_check(pfr_gemm_dense_dev(ctx_, static_cast<const float*>(A.p), rows, Ka, 0, w->dense, N, N,
+                                                     1.0f, 1.0f, nullptr, 0, static_cast<float*>(out.p), N, act));
+                    else
+                        pfr_check(pfr_gemm_csr_act_dev(ctx_, static_cast<const float*>(A.p), rows, Ka, 0, w->csr,
+                                                       1.0f, 1.0f, nullptr, 0, static_cast<float*>(out.p), math_mode_,
+                                                       act));
                 } else {
                     const DevTensor& B = act_in(1);
                     need_f32(B.dtype, "MatMul input B");
@@ -563,8 +642,13 @@ std::vector<Tensor> RocmExecutor::execute_plan(const Graph& graph,
                     const int64_t M = as[0], N = bs[1];
                     out.shape = {M, N};
                     out.p = device_buffer(st.out, M * N * 4);
-                    pfr_check(pfr_spmm_csr_act_dev(ctx_, weight(n)->csr, static_cast<const float*>(B.p), N, N,
-                                                   static_cast<float*>(out.p), N, math_mode_, act));
+                    const DeviceWeight* w = weight(n);
+                    if (w->kind == DeviceWeight::DenseA)
+                        pfr_check(pfr_gemm_dense_dev(ctx_, w->dense, M, Ka, 0, static_cast<const float*>(B.p), N, N,
+                                                     1.0f, 1.0f, nullptr, 0, static_cast<float*>(out.p), N, act));
+                    else
+                        pfr_check(pfr_spmm_csr_act_dev(ctx_, w->csr, static_cast<const float*>(B.p), N, N,
+                                                       static_cast<float*>(out.p), N, math_mode_, act));
                 }
                 break;
             }
@@ -883,7 +967,7 @@ std::vector<Tensor> RocmExecutor::execute(const Graph& graph, const std::unorder
         std::vector<const Tensor*> ins;
         ins.reserve(node->inputs().size());
         const DeviceWeight* w = weight(node.get());
-        const int wslot = !w ? -1 : (w->kind == DeviceWeight::CsrB || w->kind == DeviceWeight::Sp24B ? 1 : 0);
+        const int wslot = !w ? -1 : (w->second() ? 1 : 0);
         for (size_t i = 0; i < node->inputs().size(); ++i) {
             const std::string& nm = node->inputs()[i];
             auto it = view.find(nm);

@@ -58,10 +58,16 @@ LayerNormExtent layernorm_extent(const std::vector<int64_t>& x_shape, int64_t sc
 class RocmExecutor : public Backend {
 public:
     struct DeviceWeight {
-        enum Kind { None, CsrB, CsrA, Sp24A, Sp24B } kind = None;
+        enum Kind { None, CsrB, CsrA, Sp24A, Sp24B, DenseB, DenseA } kind = None;
         pfr_csr* csr = nullptr;    // CsrB: CSR of op(B)^T; CsrA: CSR of A
         pfr_sp24* sp24 = nullptr;  // Sp24A: 2:4-compressed int8 A; Sp24B: B^T (N x K), 2:4 along K
+        float* dense = nullptr;    // DenseB: op(B), K x N row-major; DenseA: A, M x K row-major
+        // the weight is the product's second operand (B)
+        bool second() const { return kind == CsrB || kind == Sp24B || kind == DenseB; }
     };
+    // A float32 initializer weight takes the sparse (CSR) path when at most
+    // this fraction of its entries is nonzero, else the dense product.
+    static constexpr double kSparseDensityGate = 0.5;
 
     // opt: None runs node by node through the OpFuncs; Basic adds the
     // device-resident plan; Extended and All also fuse Relu into products.
@@ -84,8 +90,19 @@ public:
     bool device_plan() const { return last_on_device_; }
     // Kernel launches of the plan (a fused pair counts once).
     size_t device_plan_steps() const { return plan_.size(); }
+    // Prepared weights by device form: CSR, dense (above the density gate), 2:4.
+    void weight_forms(int* csr, int* dense, int* sp24) const {
+        *csr = *dense = *sp24 = 0;
+        for (const auto& kv : weights_) {
+            const auto k = kv.second.kind;
+            if (k == DeviceWeight::CsrA || k == DeviceWeight::CsrB) ++*csr;
+            else if (k == DeviceWeight::DenseA || k == DeviceWeight::DenseB) ++*dense;
+            else if (k == DeviceWeight::Sp24A || k == DeviceWeight::Sp24B) ++*sp24;
+        }
+    }
 
 private:
+    DeviceWeight dense_initializer_weight(const Tensor& W, bool second, bool transB);
     // One kernel launch of the device plan.
     struct PlanStep {
         enum Op { Gemm, MatMulB, MatMulA, QMatMul, QMatMulT, Relu, Softmax, DynQuant, Gelu, Add, LayerNorm, Quant, Dequant } op;

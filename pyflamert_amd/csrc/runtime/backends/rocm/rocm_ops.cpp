@@ -6,6 +6,7 @@
 // 77-167 and :251-278, activation.cpp:45-60, :157-237 and :239-259,
 // nn.cpp:419-478; per-tensor Quantize / Dequantize / QuantizeLinear /
 // DequantizeLinear, quantized_ops.cpp:35-70 and :284-347).
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -32,6 +33,32 @@ void need_f32(const Tensor& t, const char* what) {
         throw std::invalid_argument(std::string(what) + " must be float32, got " + dtype_name(t.dtype()));
 }
 
+// Device memory for one call's staged host operands.
+struct DevScratch {
+    pfr_ctx* ctx;
+    void* p = nullptr;
+    DevScratch(pfr_ctx* c, int64_t bytes) : ctx(c) { pfr_check(pfr_dev_alloc(c, std::max<int64_t>(bytes, 4), &p)); }
+    ~DevScratch() {
+        if (p) pfr_dev_free(ctx, p);
+    }
+    DevScratch(const DevScratch&) = delete;
+    DevScratch& operator=(const DevScratch&) = delete;
+    float* f() const { return static_cast<float*>(p); }
+};
+
+// The dense product (a weight above the density gate) on host operands:
+// Y[M, N] = alpha * op(A) . B + beta * C with one of A, B the device weight.
+void dense_host(pfr_ctx* ctx, const float* A, bool a_dev, int64_t M, int64_t K, int ta, const float* B, bool b_dev,
+                int64_t N, float alpha, float beta, const float* C, int64_t c_size, float* Y) {
+    DevScratch da(ctx, a_dev ? 0 : M * K * 4), db(ctx, b_dev ? 0 : K * N * 4), dc(ctx, c_size * 4), dy(ctx, M * N * 4);
+    if (!a_dev) pfr_check(pfr_copy_to_device(ctx, da.p, A, M * K * 4));
+    if (!b_dev) pfr_check(pfr_copy_to_device(ctx, db.p, B, K * N * 4));
+    if (C && c_size) pfr_check(pfr_copy_to_device(ctx, dc.p, C, c_size * 4));
+    pfr_check(pfr_gemm_dense_dev(ctx, a_dev ? A : da.f(), M, K, ta, b_dev ? B : db.f(), N, N, alpha, beta,
+                                 C && c_size ? dc.f() : nullptr, c_size, dy.f(), N, PFR_ACT_NONE));
+    pfr_check(pfr_copy_to_host(ctx, Y, dy.p, M * N * 4));
+}
+
 // MatMul with one pruned, initializer operand (math.cpp:268-374 semantics).
 std::vector<Tensor> rocm_matmul(const std::vector<const Tensor*>& in, const OpContext& ctx) {
     need_inputs(in, 2, "MatMul");
@@ -44,7 +71,8 @@ std::vector<Tensor> rocm_matmul(const std::vector<const Tensor*>& in, const OpCo
     if (Ka != Kb)
         throw std::invalid_argument("MatMul: incompatible dimensions - A has inner dim " + std::to_string(Ka) +
                                     ", B has inner dim " + std::to_string(Kb));
-    if (w && w->kind == RocmExecutor::DeviceWeight::CsrB) {
+    using DW = RocmExecutor::DeviceWeight;
+    if (w && (w->kind == DW::CsrB || w->kind == DW::DenseB)) {
         // A [..., M, K] (broadcast over the batch dims) x W [K, N]: rows flatten.
         need_f32(a, "MatMul input A");
         const int64_t N = b.shape()[1];
@@ -52,16 +80,24 @@ std::vector<Tensor> rocm_matmul(const std::vector<const Tensor*>& in, const OpCo
         os.push_back(N);
         Tensor out(os, DType::Float32);
         const int64_t rows = a.num_elements() / Ka;
-        pfr_check(pfr_gemm_csr(ex.ctx(), a.data_ptr<float>(), rows, Ka, 0, w->csr, 1.0f, 1.0f, nullptr, 0,
-                               out.data_ptr<float>(), ex.math_mode()));
+        if (w->kind == DW::DenseB)
+            dense_host(ex.ctx(), a.data_ptr<float>(), false, rows, Ka, 0, w->dense, true, N, 1.0f, 1.0f, nullptr, 0,
+                       out.data_ptr<float>());
+        else
+            pfr_check(pfr_gemm_csr(ex.ctx(), a.data_ptr<float>(), rows, Ka, 0, w->csr, 1.0f, 1.0f, nullptr, 0,
+                                   out.data_ptr<float>(), ex.math_mode()));
         return {std::move(out)};
     }
-    if (w && w->kind == RocmExecutor::DeviceWeight::CsrA) {
+    if (w && (w->kind == DW::CsrA || w->kind == DW::DenseA)) {
         need_f32(b, "MatMul input B");
         if (b.ndim() != 2) throw std::invalid_argument("MatMul: a pruned first operand needs a 2-D second operand");
         const int64_t M = a.shape()[0], N = b.shape()[1];
         Tensor out({M, N}, DType::Float32);
-        pfr_check(pfr_spmm_csr(ex.ctx(), w->csr, b.data_ptr<float>(), N, out.data_ptr<float>(), ex.math_mode()));
+        if (w->kind == DW::DenseA)
+            dense_host(ex.ctx(), w->dense, true, M, Ka, 0, b.data_ptr<float>(), false, N, 1.0f, 1.0f, nullptr, 0,
+                       out.data_ptr<float>());
+        else
+            pfr_check(pfr_spmm_csr(ex.ctx(), w->csr, b.data_ptr<float>(), N, out.data_ptr<float>(), ex.math_mode()));
         return {std::move(out)};
     }
     throw std::runtime_error("MatMul: neither operand is a float32 2-D initializer; the rocm backend runs "
@@ -77,7 +113,7 @@ std::vector<Tensor> rocm_gemm(const std::vector<const Tensor*>& in, const OpCont
     const Tensor& B = *in[1];
     const Tensor* C = in.size() > 2 ? in[2] : nullptr;
     if (A.ndim() < 2 || B.ndim() < 2) throw std::invalid_argument("Gemm input A/B must have at least 2 dimensions");
-    if (!w || w->kind != RocmExecutor::DeviceWeight::CsrB)
+    if (!w || (w->kind != RocmExecutor::DeviceWeight::CsrB && w->kind != RocmExecutor::DeviceWeight::DenseB))
         throw std::runtime_error("Gemm: B is not a float32 2-D initializer; the rocm backend runs pruned-weight "
                                  "products only");
     need_f32(A, "Gemm input A");
@@ -100,8 +136,12 @@ std::vector<Tensor> rocm_gemm(const std::vector<const Tensor*>& in, const OpCont
         c = C->data_ptr<float>();
         c_size = C->num_elements();
     }
-    pfr_check(pfr_gemm_csr(ex.ctx(), A.data_ptr<float>(), M, Ka, (int)ta, w->csr, alpha, beta, c, c_size,
-                           out.data_ptr<float>(), ex.math_mode()));
+    if (w->kind == RocmExecutor::DeviceWeight::DenseB)
+        dense_host(ex.ctx(), A.data_ptr<float>(), false, M, Ka, (int)ta, w->dense, true, N, alpha, beta, c, c_size,
+                   out.data_ptr<float>());
+    else
+        pfr_check(pfr_gemm_csr(ex.ctx(), A.data_ptr<float>(), M, Ka, (int)ta, w->csr, alpha, beta, c, c_size,
+                               out.data_ptr<float>(), ex.math_mode()));
     return {std::move(out)};
 }
 

@@ -314,4 +314,13 @@ int pfr_session_device_plan(pfr_session* s, int* device_resident, int* steps) {
     });
 }
 
+int pfr_session_weight_forms(pfr_session* s, int* csr, int* dense, int* sp24) {
+    return guard([&] {
+        if (!s || !csr || !dense || !sp24) throw PyFlameRTError("null argument");
+        auto* ex = dynamic_cast<RocmExecutor*>(&s->sess->backend());
+        if (ex) ex->weight_forms(csr, dense, sp24);
+        else *csr = *dense = *sp24 = 0;
+    });
+}
+
 }  // extern "C"

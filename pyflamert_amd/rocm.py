@@ -121,6 +121,13 @@ class Context:
     def apply_mask_dev(self, w_ptr, mask_ptr, n, out_ptr):
         check(self._lib.pfr_apply_mask_dev(self.handle, w_ptr, mask_ptr, n, out_ptr))
 
+    def gemm_dense_dev(self, A_ptr, M, K, B_ptr, N, Y_ptr, transA=False, alpha=1.0, beta=1.0, C_ptr=None,
+                       c_size=0, ldb=None, ldy=None, relu=False, gelu=False):
+        """Dense strict product (pfr_gemm_dense_dev), device pointers."""
+        act = _lib.ACT_GELU if gelu else (_lib.ACT_RELU if relu else 0)
+        check(self._lib.pfr_gemm_dense_dev(self.handle, A_ptr, M, K, int(bool(transA)), B_ptr, N, ldb or N,
+                                           alpha, beta, C_ptr, c_size, Y_ptr, ldy or N, act))
+
     def sp24_pack(self, W, w_scales=None):
         """2:4 weight [M, K]: int8 (with 1 or M symmetric scales) or bf16 bits
         (uint16)."""
@@ -277,6 +284,12 @@ class CsrWeight:
         M, K, nnz = C.c_int64(), C.c_int64(), C.c_int64()
         check(ctx._lib.pfr_csr_info(handle, C.byref(M), C.byref(K), C.byref(nnz)))
         self.M, self.K, self.nnz = M.value, K.value, nnz.value
+
+    def dense_semantics(self):
+        """pfr_csr_dense_semantics: products then propagate non-finite
+        activations as the dense kernels do."""
+        check(self.ctx._lib.pfr_csr_dense_semantics(self.handle))
+        return self
 
     def free(self):
         if self.handle:

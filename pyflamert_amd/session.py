@@ -32,6 +32,7 @@ _SIGS = {
     "pfr_session_result": (_INT, [_P, _INT, C.POINTER(_INT), _P, C.POINTER(_INT), C.POINTER(_P)]),
     "pfr_session_supported_ops": (_INT, [_P, C.c_char_p, _I64]),
     "pfr_session_device_plan": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT)]),
+    "pfr_session_weight_forms": (_INT, [_P, C.POINTER(_INT), C.POINTER(_INT), C.POINTER(_INT)]),
     "pfr_model_describe": (_INT, [C.c_char_p, C.c_char_p, _I64, C.POINTER(_I64)]),
     "pfr_model_resave": (_INT, [C.c_char_p, C.c_char_p]),
     "pfr_model_quantize": (_INT, [C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(_INT)]),
@@ -188,6 +189,14 @@ class InferenceSession:
         _check(self._L.pfr_session_supported_ops(self._h, buf, len(buf)))
         lines = buf.value.decode().split("\n")
         return lines[0], lines[1:]
+
+    def weight_forms(self):
+        """{"csr": n, "dense": n, "sp24": n}: the device form of each prepared
+        weight (float32 initializers at most half nonzero and CSR records go
+        to CSR, denser ones to the dense product)."""
+        a, b, c = C.c_int(), C.c_int(), C.c_int()
+        _check(self._L.pfr_session_weight_forms(self._h, C.byref(a), C.byref(b), C.byref(c)))
+        return {"csr": a.value, "dense": b.value, "sp24": c.value}
 
     def device_plan(self):
         """(device_resident, kernel_steps) of the last run: whether the graph
