@@ -392,8 +392,10 @@ int pfr_dynamic_quantize_linear_dev(pfr_ctx* ctx, const float* x, int64_t n, uin
  * are restored (set to 1) in flat order while more than (size_t)((float)n *
  * s) zeros remain.  s <= 0 gives all ones, s >= 1 all zeros; n == 0 with
  * 0 < s < 1 is PFR_ERR_INVALID_ARG ("Cannot prune empty weight tensor").
- * Bit-identical to the reference for finite weights (NaN magnitudes order
- * above +inf here; the reference's std::sort leaves them unspecified).
+ * Bit-identical to the reference for NaN-free weights.  A NaN weight gets
+ * mask 0 and counts among the zeros, as the reference's comparisons make
+ * it; its place in the sort, which the reference's std::sort leaves
+ * unspecified, is taken above +inf.
  * Host pointers; _dev: device pointers on the context's stream. */
 int pfr_magnitude_mask(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask);
 int pfr_magnitude_mask_dev(pfr_ctx* ctx, const float* w, int64_t n, float sparsity, float* mask);

@@ -131,8 +131,14 @@ void orc_apply_mask(const float* t, const float* mask, int64_t n, float* out) {
 /* mask producers                                                            */
 /* ------------------------------------------------------------------------ */
 
+/* Ascending, NaN after everything (+inf included).  std::sort's order of
+ * NaN importances is unspecified (they break its strict weak ordering);
+ * this fixes it to the end, as the GPU's radix select on |w| bit patterns
+ * does.  For NaN-free input it is the plain ascending order. */
 static int cmp_float_asc(const void* pa, const void* pb) {
     float a = *(const float*)pa, b = *(const float*)pb;
+    const int na = a != a, nb = b != b;
+    if (na || nb) return na - nb;
     return (a < b) ? -1 : (a > b) ? 1 : 0;
 }
 

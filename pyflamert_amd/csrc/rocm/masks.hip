@@ -8,7 +8,8 @@
 //   order (:91-99).  Here the order statistic is a radix select over the
 //   |w| bit patterns (non-negative floats order as their uint32 bits; NaN,
 //   whose position the reference's std::sort leaves unspecified, sorts above
-//   +inf), four 8-bit passes, each a histogram kernel and a one-block bucket
+//   +inf, and, as in the reference's comparisons, is never kept and counts
+//   among the zeros), four 8-bit passes, each a histogram kernel and a one-block bucket
 //   choice, all on the stream; the tie restore is a flat-order rank of the
 //   elements equal to the threshold (per-block counts, a one-block scan,
 //   then per-element ranks).
@@ -277,8 +278,17 @@ __global__ __launch_bounds__(1024) void k_mag_pick(MagState* st, const uint32_t*
     }
 }
 
+// The reference's float comparisons on |w| keys: a NaN key (bits above
+// +inf's) is never greater than or equal to the threshold, and nothing is
+// greater than or equal to a NaN threshold; for other keys the uint32 order
+// is the float order.
+__device__ __forceinline__ bool key_nan(uint32_t k) { return k > 0x7F800000u; }
+__device__ __forceinline__ bool key_gt(uint32_t k, uint32_t thr) { return !key_nan(k) && !key_nan(thr) && k > thr; }
+__device__ __forceinline__ bool key_eq(uint32_t k, uint32_t thr) { return !key_nan(k) && k == thr; }
+
 // Per block: keys equal to the threshold (in the block's flat range) and,
-// across blocks, keys at or below it.
+// across blocks, keys not above it (the mask's zeros before the restore,
+// NaN keys included, as the reference counts them).
 template <bool VEC>
 __global__ __launch_bounds__(kMaskThreads) void k_mag_count(const float* __restrict__ w, int64_t n,
                                                              const MagState* __restrict__ st,
@@ -293,8 +303,8 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_count(const float* __restr
     uint32_t tie = 0, le = 0;
 #pragma unroll
     for (int i = 0; i < kMaskPerThread; ++i) {
-        tie += i < valid && keys[i] == thr;
-        le += i < valid && keys[i] <= thr;
+        tie += i < valid && key_eq(keys[i], thr);
+        le += i < valid && !key_gt(keys[i], thr);
     }
     // one LDS atomic per wave, not per thread
 #pragma unroll
@@ -366,7 +376,7 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restr
     const int valid = load_keys16<VEC>(w, n, start, keys);
     uint32_t mine = 0;
 #pragma unroll
-    for (int i = 0; i < kMaskPerThread; ++i) mine += i < valid && keys[i] == thr;
+    for (int i = 0; i < kMaskPerThread; ++i) mine += i < valid && key_eq(keys[i], thr);
     scan[t] = mine;
     __syncthreads();
     for (int off = 1; off < kMaskThreads; off <<= 1) {
@@ -379,8 +389,8 @@ __global__ __launch_bounds__(kMaskThreads) void k_mag_write(const float* __restr
     float v[kMaskPerThread];
 #pragma unroll
     for (int i = 0; i < kMaskPerThread; ++i) {
-        v[i] = keys[i] > thr ? 1.0f : 0.0f;
-        if (keys[i] == thr && i < valid) {
+        v[i] = key_gt(keys[i], thr) ? 1.0f : 0.0f;
+        if (key_eq(keys[i], thr) && i < valid) {
             if (rank < restore) v[i] = 1.0f;
             ++rank;
         }

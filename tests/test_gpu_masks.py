@@ -83,6 +83,21 @@ def test_nm_ratios_and_partial_groups(ctx, total):
         assert same(ctx.nm_mask(w, n, m), O.orc_nm_mask(w, n, m)), (total, n, m)
 
 
+@pytest.mark.parametrize("frac,s", [(0.01, 0.5), (0.01, 0.995), (0.2, 0.9), (0.3, 0.05)])
+def test_magnitude_nan_weights(ctx, frac, s):
+    """A NaN weight is never kept and counts among the zeros (the
+    reference's comparisons); the threshold may fall on finite values or on
+    a NaN.  Bit-identical to the oracle."""
+    rng = np.random.default_rng(int(frac * 1000) + int(s * 1000))
+    for n in (1000, 4096 * 3 + 5):
+        w = tie_heavy(rng, n)
+        w[rng.random(n) < frac] = np.nan
+        say(f"magnitude mask with NaN n={n} frac={frac} s={s}")
+        got = ctx.magnitude_mask(w, s)
+        assert same(got, O.orc_magnitude_mask(w, s)), (n, frac, s)
+        assert not got[np.isnan(w)].any()
+
+
 def test_full_size_and_compiled_reference(ctx):
     """A 2:4 and a 70 % magnitude mask of a 4096 x 4096 N(0, 1) weight, and
     an 11008 x 4096 2:4 mask, against the oracle and (where it is built)

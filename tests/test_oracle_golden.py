@@ -243,6 +243,42 @@ def test_nm_mask_invariants():
     assert np.array_equal(m, ref)
 
 
+def magnitude_mask_textbook(w, s):
+    """magnitude_pruning.cpp:22-102 written from its definition with numpy:
+    threshold = the sorted |w| at min(floor(n s), n - 1) (np.sort puts NaN
+    last), keep |w| > threshold, then restore threshold ties in flat order
+    while more than (size_t)((float)n * s) are pruned."""
+    imp = np.abs(w.astype(np.float32))
+    n = imp.size
+    idx = min(int(np.floor(np.float64(n) * np.float64(np.float32(s)))), n - 1)
+    thr = np.sort(imp)[idx]
+    m = (imp > thr).astype(np.float32)
+    target = int(np.float32(n) * np.float32(s))
+    extra = int((m == 0).sum()) - target
+    for i in np.nonzero((m == 0) & (imp == thr))[0]:
+        if extra <= 0:
+            break
+        m[i] = 1.0
+        extra -= 1
+    return m
+
+
+def test_magnitude_mask_nan_weights():
+    """NaN weights: never kept (NaN > t is false), counted among the zeros,
+    never restored (NaN == t is false); their place in the sort is taken
+    after +inf.  The oracle against the definition above, with the
+    threshold among the finite values, at a NaN, and with ties."""
+    rng = np.random.default_rng(4)
+    for n, frac, s in ((1000, 0.01, 0.5), (1000, 0.01, 0.995), (257, 0.2, 0.9), (64, 0.0, 0.3)):
+        w = rng.standard_normal(n).astype(np.float32)
+        w[rng.integers(0, n, n // 10)] = np.float32(0.5)  # ties
+        w[rng.random(n) < frac] = np.nan
+        w[3] = -np.inf
+        got = O.orc_magnitude_mask(w, s)
+        assert np.array_equal(got, magnitude_mask_textbook(w, s)), (n, frac, s)
+        assert not got[np.isnan(w)].any()
+
+
 def test_bf16_rne_on_positive_finite_values():
     """For positive finite values the reference conversion is plain RNE."""
     import torch
