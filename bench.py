@@ -33,6 +33,7 @@ FP32_VALU_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (packed FMA)
 STRICT_VALU_CEILING_TFLOPS = 39.3  # one non-packed fp32 op per lane per clock, 256 CUs x 64 lanes x 2.4 GHz
 FMA_VALU_CEILING_TFLOPS = 78.6     # one non-packed fp32 FMA (2 flops) per lane per clock
 INT8_DENSE_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (the 2:4 instruction doubles K per issue)
+BF16_SPARSE_PEAK_TFLOPS = 5000.0  # MI355X bf16 MFMA with 2:4 sparsity, dense-equivalent (2.5 dense)
 M = K = 4096
 DENSITY = 0.1
 N_MAIN = 256
@@ -478,6 +479,61 @@ def calibrate_copy(mib):
                       "launches": 10}), flush=True)
 
 
+def bench_sp24_bf16(ctx, args):
+    """2:4 bf16 GEMM: W 11008 x 4096 (top-2-of-4 of N(0,1), bf16), X 4096 x 512
+    bf16, fp32 accumulate and output.  One launch includes the activation
+    transpose the kernel reads B from; 16 weight sets rotate (16 x 51 MB of
+    operands and outputs, beyond the 256 MB cache)."""
+    import numpy as np
+    import torch
+
+    from pyflamert_amd import workloads
+
+    M, K, N = 11008, 4096, 512
+    w = workloads.keep_top2_of_4(np.random.default_rng(3).standard_normal((M, K), dtype=np.float32))
+    wb = workloads.bf16_bits_rne(w)
+    xb = workloads.bf16_bits_rne(workloads.dense_normal((K, N), 1.0, seed=4))
+    sets = []
+    for _ in range(16):
+        W = ctx.sp24_pack(wb)
+        dX = torch.from_numpy(xb.view(np.int16)).cuda()
+        dY = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        sets.append((W, dX, dY))
+    torch.cuda.synchronize()
+
+    def launch(i):
+        W, dX, dY = sets[i % len(sets)]
+        W.gemm_bf16_dev(dX.data_ptr(), N, dY.data_ptr())
+
+    for i in range(20):
+        launch(i)
+    torch.cuda.synchronize()
+    steps = max(50, args.steps // 10)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        launch(i)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    useful = M * N * K  # 2 flops x the M*N*K/2 kept products
+    byts = M * K + M * K // 16 + 2 * K * N + 4 * M * N  # kept bf16 values, 2-bit positions, X, fp32 Y
+    res = {
+        "ms_per_launch": round(ms, 5),
+        "useful_tflops": round(useful / (ms * 1e-3) / 1e12, 1),
+        "dense_equiv_tflops": round(2 * useful / (ms * 1e-3) / 1e12, 1),
+        "frac_of_sparse_bf16_peak": round(2 * useful / (ms * 1e-3) / 1e12 / BF16_SPARSE_PEAK_TFLOPS, 4),
+        "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm": round(byts / (ms * 1e-3) / 1e9 / 8000.0, 4),
+        "shape": [M, K, N],
+    }
+    log(f"sp24 bf16: {res}")
+    for W, _, _ in sets:
+        W.free()
+    return res
+
+
 def bench_sp24(ctx, args):
     """2:4 int8 GEMM: W 11008 x 4096 (top-2-of-4, per-row int8), X 4096 x 512
     int8 (scale 0.05), int32 accumulate, requantised int8 output.  One launch
@@ -642,6 +698,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="time only the N=256 SpMM (profiler runs)")
     ap.add_argument("--only-sp24", action="store_true", help="time only the 2:4 int8 GEMM (profiler runs)")
+    ap.add_argument("--only-sp24-bf16", action="store_true", help="time only the 2:4 bf16 GEMM (profiler runs)")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
                     help="run a copy-like kernel of MIB MiB for counter calibration and exit")
     args = ap.parse_args()
@@ -666,6 +723,10 @@ def main():
         print(json.dumps({"sp24_i8": bench_sp24(ctx, args)}), flush=True)
         ctx.close()
         return
+    if args.only_sp24_bf16:
+        print(json.dumps({"sp24_bf16": bench_sp24_bf16(ctx, args)}), flush=True)
+        ctx.close()
+        return
 
     log("generating W 4096x4096 at 10% density ...")
     ip, ix, v = workloads.csr_uniform(M, K, DENSITY, 0.02, seed=1234)
@@ -677,6 +738,7 @@ def main():
         # the other workloads first: the headline is timed on a GPU that has
         # been busy (clocks up), with its own warm-up on top
         extra["sp24_i8"] = bench_sp24(ctx, args)
+        extra["sp24_bf16"] = bench_sp24_bf16(ctx, args)
         extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
         extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
         extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)

@@ -34,7 +34,7 @@ typedef __bf16 v16bf __attribute__((ext_vector_type(16)));
 struct pfr_sp24 {
     pfr_ctx* ctx = nullptr;
     int64_t M = 0, K = 0;
-    int64_t Mp = 0, Kp = 0;  // padded: Mp % 128 == 0, Kp % 128 == 0
+    int64_t Mp = 0, Kp = 0;  // padded: Mp % 256 == 0; Kp % 512 == 0 (int8) or % 256 (bf16), at least one tile
     pfr_dtype dtype = PFR_I8;
     void* a = nullptr;        // compressed values, [Mp/16][Kp/KT][64][16 B]
     uint32_t* idx = nullptr;  // [Mp/16][Kp/KT (int8) | Kp/128 (bf16)][64]
@@ -45,8 +45,6 @@ struct pfr_sp24 {
 
 namespace {
 
-constexpr int kTileM = 128;  // bf16 kernel: rows per workgroup (4 waves x 32)
-constexpr int kTileN = 64;   // bf16 kernel: columns per workgroup
 constexpr int kPadM = 256;   // packed weights pad M to this (the int8 tile height)
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -89,22 +87,38 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // ---- kernels ----------------------------------------------------------------
 
-// XT[n][k] (Np x Kp, zero padded) = X[k][n] (K x N, row stride ldx).
-template <class T>
-__global__ __launch_bounds__(256) void k_transpose_pad(const T* __restrict__ X, int64_t K, int64_t N,
-                                                       int64_t ldx, T* __restrict__ XT, int64_t Kp) {
-    __shared__ T tile[64][65];
+// XT[n][k] (Np x Kp) = X[k][n] for 16-bit elements (bf16 bits), zero
+// outside K x N: a 64 x 64 block per workgroup, read as 8-byte runs of four
+// columns along X rows and written as 8-byte runs of four k along XT rows
+// (the element-wise form spent 10.5 us on 4096 x 512, about 4x this).
+__global__ __launch_bounds__(256) void k_transpose_b16(const uint16_t* __restrict__ X, int64_t K, int64_t N,
+                                                       int64_t ldx, int vec, uint16_t* __restrict__ XT, int64_t Kp) {
+    __shared__ uint16_t tile[64][68];  // tile[k][n], rows 136 B apart (8-byte aligned)
     const int t = threadIdx.x;
     const int64_t k0 = (int64_t)blockIdx.x * 64, n0 = (int64_t)blockIdx.y * 64;
-    for (int i = 0; i < 16; ++i) {
-        const int kk = (t >> 6) + 4 * i, nn = t & 63;
-        const int64_t k = k0 + kk, n = n0 + nn;
-        tile[kk][nn] = (k < K && n < N) ? X[k * ldx + n] : T(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // X row k0 + kk, columns n0 + 4q .. +3
+        const int e = t + 256 * i, kk = e >> 4, q = e & 15;
+        const int64_t k = k0 + kk, n = n0 + 4 * q;
+        uint16_t v[4] = {0, 0, 0, 0};
+        if (k < K) {
+            if (vec && n + 4 <= N) {
+                const uint2 u = *reinterpret_cast<const uint2*>(X + k * ldx + n);
+                v[0] = (uint16_t)u.x; v[1] = (uint16_t)(u.x >> 16); v[2] = (uint16_t)u.y; v[3] = (uint16_t)(u.y >> 16);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = n + j < N ? X[k * ldx + n + j] : (uint16_t)0;
+            }
+        }
+        *reinterpret_cast<uint2*>(&tile[kk][4 * q]) = make_uint2(v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16));
     }
     __syncthreads();
-    for (int i = 0; i < 16; ++i) {
-        const int nn = (t >> 6) + 4 * i, kk = t & 63;
-        XT[(n0 + nn) * Kp + k0 + kk] = tile[kk][nn];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // XT row n0 + nn, k0 + 4q .. +3
+        const int e = t + 256 * i, nn = e >> 4, q = e & 15;
+        const uint32_t lo = tile[4 * q][nn] | ((uint32_t)tile[4 * q + 1][nn] << 16);
+        const uint32_t hi = tile[4 * q + 2][nn] | ((uint32_t)tile[4 * q + 3][nn] << 16);
+        *reinterpret_cast<uint2*>(XT + (n0 + nn) * Kp + k0 + 4 * q) = make_uint2(lo, hi);
     }
 }
 
@@ -513,62 +527,200 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
                           xs_dev, zp_dev, row_sum);
 }
 
-// bf16: 16x16x64 tiles, index words hold two k-tiles (abid 0 / 1).
-__global__ __launch_bounds__(256) void k_sp24_bf16(
-    int nkt, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
-    const uint16_t* __restrict__ XT, int64_t Kp, int M, int N, float* __restrict__ Y, int64_t ldy) {
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int mt0 = (int)blockIdx.x * (kTileM / 16) + 2 * w;
-    const int nt0 = (int)blockIdx.y * (kTileN / 16);
+// bf16 2:4 GEMM with the int8 kernel's pipeline: 256 x 128 outputs per
+// workgroup of four waves (one per SIMD, 64 rows x 128 columns each: 4 x 8
+// tiles of 16 x 16, 128 fp32 accumulators), a k step of 64 (one
+// v_smfmac_f32_16x16x64_bf16 per tile), operands in four 36 KiB LDS stages
+// filled by direct-to-LDS loads four steps ahead:
+//   A values  [16 row blocks][64 lanes][16 B]  (8 kept bf16 per lane)
+//   A indices [16 row blocks][64 lanes] u32    (the word of the step's k
+//             pair; the step uses half abid = step % 2)
+//   B         [128 columns][128 B]: the 64 bf16 of one XT row, 16-byte chunk
+//             c stored at c ^ ((column >> 1) & 7) (16 distinct bank groups
+//             per ds_read_b128)
+// The per-lane B fragment of the bf16 instruction (k 8 kb + e, then 32 +
+// 8 kb + e) occupies the same bytes of the 128-byte row as the int8 one (k
+// 16 kb + b, then 64 + 16 kb + b), so the B reads are the int8 kernel's.
+// Per step a workgroup loads 36 KiB for 4 x 32 smfmac (16 clocks each per
+// SIMD: 512), the int8 kernel's balance, so it is bound the same way: by
+// the operand loads.  nkt (steps) is a multiple of 4 (K padded to 256).
+// XROW = true reads the row-major activation X itself (K % 256 == 0, N %
+// 128 == 0, rows 16-byte aligned) instead of a transposed copy: LDS then
+// holds the step's 64 X rows (256 B each; 16-byte piece q of row k at q ^
+// 2 bf16_swizzle(k), pairs kept together) and the B fragments come from
+// ds_read_b64_tr_b16, which (measured on the device) gives lane t of each
+// 16-lane group element t % 4 of the 8-byte reads of source lanes t / 4 +
+// 4i, i = 0..3; so source lane s pointing at row k0 + s / 4, columns
+// 4 (s % 4) .. + 3 of a 16-column chunk gives lane t the four k values k0 ..
+// k0 + 3 of column chunk + t.
+__device__ __forceinline__ int bf16_swizzle(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
+template <bool XROW>
+__global__ __launch_bounds__(kI8Threads, 1) void k_sp24_bf16p(int nkt, const v4i* __restrict__ A,
+                                                              const uint32_t* __restrict__ I,
+                                                              const uint16_t* __restrict__ XT, int64_t ldb_bytes,
+                                                              int M, int N, float* __restrict__ Y, int64_t ldy,
+                                                              int ntn) {
+    __shared__ __attribute__((aligned(1024))) char st0[kStage];
+    __shared__ __attribute__((aligned(1024))) char st1[kStage];
+    __shared__ __attribute__((aligned(1024))) char st2[kStage];
+    __shared__ __attribute__((aligned(1024))) char st3[kStage];
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const int kb = l >> 4, c = l & 15;
-    v4f acc[2][4];
+    int mt, nt;
+    {  // consecutive tiles of the m-major order go to one XCD
+        const int G = (int)gridDim.x, L = (int)blockIdx.x, xcd = L & 7, slot = L >> 3;
+        const int q = G >> 3, rem = G & 7;
+        const int T = xcd * q + min(xcd, rem) + slot;
+        mt = T / ntn;
+        nt = T % ntn;
+    }
+    const int64_t mb0 = (int64_t)mt * (kI8TileM / 16);
+    const int64_t n0 = (int64_t)nt * kI8TileN;
+    constexpr int kLoads = 12;
+    const int nkp = nkt / 2;
+    const v4i* asrc = A + ((mb0 + w) * nkt) * 64 + l;
+    const uint32_t* isrc = I + ((mb0 + w) * nkp) * 64 + l;
+    const int64_t arb4 = (int64_t)4 * nkt * 64, irb4 = (int64_t)4 * nkp * 64;
+    // B: per k step, XT form: 128 XT rows (columns n0 ..) of 128 B, 8 per
+    // wave instruction; X-row form: 64 X rows (k) of 256 B, 4 per instruction
+    const v4i* bsrc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    const int nkp = nkt / 2;  // index words per row tile
-    const v4i* a0p = A + ((int64_t)mt0 * nkt) * 64 + l;
-    const v4i* a1p = A + ((int64_t)(mt0 + 1) * nkt) * 64 + l;
-    const uint32_t* i0p = I + ((int64_t)mt0 * nkp) * 64 + l;
-    const uint32_t* i1p = I + ((int64_t)(mt0 + 1) * nkp) * 64 + l;
-    const uint16_t* xb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xb[j] = XT + (int64_t)((nt0 + j) * 16 + c) * Kp + 8 * kb;
-    for (int kp = 0; kp < nkp; ++kp) {
-        const int ix0 = (int)i0p[(int64_t)kp * 64], ix1 = (int)i1p[(int64_t)kp * 64];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int kt = 2 * kp + h;
-            const v8bf a0 = __builtin_bit_cast(v8bf, a0p[(int64_t)kt * 64]);
-            const v8bf a1 = __builtin_bit_cast(v8bf, a1p[(int64_t)kt * 64]);
-            v16bf b[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const v4i lo = *reinterpret_cast<const v4i*>(xb[j] + (int64_t)kt * 64);
-                const v4i hi = *reinterpret_cast<const v4i*>(xb[j] + (int64_t)kt * 64 + 32);
-                b[j] = __builtin_bit_cast(v16bf, v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (h == 0) {
-                    acc[0][j] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(a0, b[j], acc[0][j], ix0, 0, 0);
-                    acc[1][j] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(a1, b[j], acc[1][j], ix1, 0, 0);
-                } else {
-                    acc[0][j] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(a0, b[j], acc[0][j], ix0, 0, 1);
-                    acc[1][j] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(a1, b[j], acc[1][j], ix1, 0, 1);
-                }
-            }
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (XROW) {
+            const int k = 4 * (w + 4 * i) + (l >> 4);
+            const int piece = (l & 15) ^ (2 * bf16_swizzle(k));
+            bsrc[i] = reinterpret_cast<const v4i*>(reinterpret_cast<const char*>(XT) + k * ldb_bytes + 2 * n0 +
+                                                   16 * piece);
+        } else {
+            const int n = 8 * (w + 4 * i) + (l >> 3);
+            const int chunk = (l & 7) ^ ((n >> 1) & 7);
+            bsrc[i] = reinterpret_cast<const v4i*>(reinterpret_cast<const char*>(XT) + (n0 + n) * ldb_bytes +
+                                                   16 * chunk);
         }
     }
+    const int64_t b_step = XROW ? 64 * ldb_bytes / 16 : 8;  // v4i per k step
+    auto issue = [&](char* st, int s) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(asrc + i * arb4 + (int64_t)s * 64, PFR_LDS(st + (w + 4 * i) * 1024), 16,
+                                             0, 0);
+            __builtin_amdgcn_global_load_lds(isrc + i * irb4 + (int64_t)(s >> 1) * 64,
+                                             PFR_LDS(st + kLdsA + (w + 4 * i) * 256), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)s * b_step,
+                                             PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 4 * i) * 128), 16, 0, 0);
+        }
+    };
+    auto issue_tail = [&](char* st) {  // same instructions, every lane reading A[0]
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = (nt0 + j) * 16 + c;
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + (w + 4 * i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + (w + 4 * i) * 256), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(A, PFR_LDS(st + kLdsA + kLdsI + 8 * (w + 4 * i) * 128), 16, 0, 0);
+        }
+    };
+    const int xsw = (c >> 1) & 7;
+    const int bxt = kLdsA + kLdsI + c * 128;
+    // X-row form: read r (k0 = 8 kb + 4 (r & 1) + 32 (r >> 1)) of this lane
+    // starts at row k0 + c / 4, bytes 8 ((c % 4) & 1) of logical piece 2j +
+    // (c % 4) / 2; bf16_swizzle of that row is the same for all four reads
+    const int trg = 2 * ((c >> 2) | ((kb & 1) << 2));
+    const int trb = kLdsA + kLdsI + (8 * kb + (c >> 2)) * 256 + 8 * (c & 1);
+    v4f acc[4][8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = (mt0 + i) * 16 + 4 * kb + r;
-                if (m < M && n < N) Y[(int64_t)m * ldy + n] = acc[i][j][r];
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    struct Frag {
+        v4i a[4];
+        int ix[4];
+        v8i b[8];
+    };
+    auto fetch = [&](Frag& f, const char* st) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (XROW) {
+                typedef short v4s __attribute__((ext_vector_type(4)));
+                v2i q[4];
+                const char* bp = st + trb + 16 * ((2 * j + ((c >> 1) & 1)) ^ trg);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    q[r] = __builtin_bit_cast(
+                        v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                 (__attribute__((address_space(3))) v4s*)(bp + 1024 * (r & 1) + 8192 * (r >> 1))));
+                f.b[j] = v8i{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
+            } else {
+                const char* bp = st + bxt + j * 16 * 128;
+                const v4i lo = *reinterpret_cast<const v4i*>(bp + 16 * (kb ^ xsw));
+                const v4i hi = *reinterpret_cast<const v4i*>(bp + 16 * ((4 + kb) ^ xsw));
+                f.b[j] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f.a[i] = *reinterpret_cast<const v4i*>(st + ((w * 4 + i) * 64 + l) * 16);
+            f.ix[i] = *reinterpret_cast<const int*>(st + kLdsA + ((w * 4 + i) * 64 + l) * 4);
+        }
+    };
+    auto mma = [&](const Frag& f, auto abid) {
+        constexpr int H = decltype(abid)::value;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(__builtin_bit_cast(v8bf, f.a[i]),
+                                                                      __builtin_bit_cast(v16bf, f.b[j]), acc[i][j],
+                                                                      f.ix[i], 0, H);
+    };
+    auto vm_wait = [](int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (0 << 8); };
+    Frag fa, fb;
+    auto step = [&](Frag& cur, Frag& nxt, char* st_cur, char* st_next, int s, auto abid) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * kLoads));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s >= 0) issue(st_cur, s + 4);
+        else issue_tail(st_cur);
+        fetch(nxt, st_next);
+        mma(cur, abid);
+        static_for<0, 32>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, g < 8 ? 2 : 1, 0);   // DS read
+            if constexpr ((g + 1) * 12 / 32 > g * 12 / 32)
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);           // VMEM read (stage load)
+        });
+    };
+    const std::integral_constant<int, 0> h0{};
+    const std::integral_constant<int, 1> h1{};
+    issue(st0, 0);
+    issue(st1, 1);
+    issue(st2, 2);
+    issue(st3, 3);
+    __builtin_amdgcn_s_waitcnt(vm_wait(3 * kLoads) | (0xF << 8));
+    __builtin_amdgcn_s_barrier();
+    fetch(fa, st0);
+    for (int s = 0; s < nkt - 4; s += 4) {
+        step(fa, fb, st0, st1, s, h0);
+        step(fb, fa, st1, st2, s + 1, h1);
+        step(fa, fb, st2, st3, s + 2, h0);
+        step(fb, fa, st3, st0, s + 3, h1);
+    }
+    step(fa, fb, st0, st1, -1, h0);
+    step(fb, fa, st1, st2, -1, h1);
+    step(fa, fb, st2, st3, -1, h0);
+    step(fb, fa, st3, st0, -1, h1);
+    __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = (mb0 + 4 * w + i) * 16 + 4 * kb + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t n = n0 + 16 * j + c;
+                if (n < N) Y[m * ldy + n] = acc[i][j][r];
             }
         }
 }
@@ -584,7 +736,7 @@ __global__ __launch_bounds__(256) void k_flip_sign(const uint8_t* __restrict__ X
 // ---- host -----------------------------------------------------------------
 
 pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
-    const int64_t Mp = round_up(M, kPadM), Kp = round_up(K, 512), nkt = Kp / 128;
+    const int64_t Mp = round_up(M, kPadM), Kp = round_up(std::max<int64_t>(K, 1), 512), nkt = Kp / 128;
     std::vector<int8_t> a((size_t)(Mp / 16 * nkt * 64 * 16), 0);
     std::vector<uint32_t> ix((size_t)(Mp / 16 * nkt * 64), 0);
     auto wat = [&](int64_t r, int64_t k) -> int8_t { return (r < M && k < K) ? W[r * K + k] : 0; };
@@ -646,7 +798,7 @@ pfr_sp24* pack_i8(pfr_ctx* ctx, int64_t M, int64_t K, const int8_t* W) {
 bool bf16_nz(uint16_t b) { return (b & 0x7FFF) != 0; }
 
 pfr_sp24* pack_bf16(pfr_ctx* ctx, int64_t M, int64_t K, const uint16_t* W) {
-    const int64_t Mp = round_up(M, kPadM), Kp = round_up(K, 128), nkt = Kp / 64, nkp = nkt / 2;
+    const int64_t Mp = round_up(M, kPadM), Kp = round_up(std::max<int64_t>(K, 1), 256), nkt = Kp / 64, nkp = nkt / 2;
     std::vector<uint16_t> a((size_t)(Mp / 16 * nkt * 64 * 8), 0);
     std::vector<uint32_t> ix((size_t)(Mp / 16 * nkp * 64), 0);
     auto wat = [&](int64_t r, int64_t k) -> uint16_t { return (r < M && k < K) ? W[r * K + k] : 0; };
@@ -831,7 +983,7 @@ unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 25
 pfr_sp24* pack_dev(pfr_ctx* ctx, int64_t M, int64_t K, const void* Wv, pfr_dtype dtype) {
     hipStream_t s = ctx->stream;
     const bool i8 = dtype == PFR_I8;
-    const int64_t Mp = round_up(M, kPadM), Kp = i8 ? round_up(K, 512) : round_up(K, 128);
+    const int64_t Mp = round_up(M, kPadM), Kp = round_up(std::max<int64_t>(K, 1), i8 ? 512 : 256);
     // the 2:4 check over every 4-group of the padded rows (the padding is zero)
     {
         unsigned long long* bad = nullptr;
@@ -905,15 +1057,6 @@ void check_i8(const pfr_sp24* W) {
 }
 
 // XT for the activation: int8 or bf16 bits, Np x Kp.
-template <class T>
-T* stage_xt(pfr_ctx* ctx, const T* X, int64_t K, int64_t N, int64_t ldx, int64_t Kp, int64_t Np) {
-    T* xt = static_cast<T*>(ctx->scratch[3].ensure(sizeof(T) * (size_t)(Np * Kp)));
-    dim3 grid((unsigned)(Kp / 64), (unsigned)(Np / 64));
-    hipLaunchKernelGGL(k_transpose_pad<T>, grid, dim3(256), 0, ctx->stream, X, K, N, ldx, xt, Kp);
-    PFR_HIP(hipGetLastError());
-    return xt;
-}
-
 // x_u8: X holds uint8 values.  x_zp: the activation zero point, or
 // (zp_dev set) a device uint8 holding it; x_scale likewise with xs_dev.
 void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, int64_t ldx, float x_scale,
@@ -1067,11 +1210,26 @@ void gemm_bf16_dev(pfr_ctx* ctx, const pfr_sp24* W, const uint16_t* X, int64_t N
     pfr::require(ldx >= N && ldy >= N, "leading dimension smaller than N");
     if (W->M == 0 || N == 0) return;
     pfr::require(X != nullptr && Y != nullptr, "null X/Y");
-    const int64_t Np = round_up(N, kTileN);
-    const uint16_t* xt = stage_xt(ctx, X, W->K, N, ldx, W->Kp, Np);
-    dim3 grid((unsigned)(W->Mp / kTileM), (unsigned)(Np / kTileN));
-    hipLaunchKernelGGL(k_sp24_bf16, grid, dim3(256), 0, ctx->stream, (int)(W->Kp / 64),
-                       static_cast<const v4i*>(W->a), W->idx, xt, W->Kp, (int)W->M, (int)N, Y, ldy);
+    // The kernel reads whole 128-column, 64-row B tiles.  X itself serves
+    // when those stay inside it and its rows are 16-byte aligned; otherwise
+    // it is transposed into a zero-padded XT (Np x Kp) first.
+    const bool xrow = W->K == W->Kp && N % kI8TileN == 0 && ldx % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    const int64_t Np = round_up(N, kI8TileN);
+    const int ntn = (int)(Np / kI8TileN);
+    const dim3 grid((unsigned)(W->Mp / kI8TileM * ntn));
+    if (xrow) {
+        hipLaunchKernelGGL(k_sp24_bf16p<true>, grid, dim3(kI8Threads), 0, ctx->stream, (int)(W->Kp / 64),
+                           static_cast<const v4i*>(W->a), W->idx, X, ldx * 2, (int)W->M, (int)N, Y, ldy, ntn);
+    } else {
+        uint16_t* xt = static_cast<uint16_t*>(ctx->scratch[3].ensure(sizeof(uint16_t) * (size_t)(Np * W->Kp)));
+        const int vec = (ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0) ? 1 : 0;
+        hipLaunchKernelGGL(k_transpose_b16, dim3((unsigned)(W->Kp / 64), (unsigned)(Np / 64)), dim3(256), 0,
+                           ctx->stream, X, W->K, N, ldx, vec, xt, W->Kp);
+        PFR_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_sp24_bf16p<false>, grid, dim3(kI8Threads), 0, ctx->stream, (int)(W->Kp / 64),
+                           static_cast<const v4i*>(W->a), W->idx, xt, W->Kp * 2, (int)W->M, (int)N, Y, ldy, ntn);
+    }
     PFR_HIP(hipGetLastError());
 }
 

@@ -63,6 +63,14 @@ def round_half_away(x):
     return (np.sign(x) * np.floor(np.abs(x) + np.float32(0.5))).astype(np.float32)
 
 
+def bf16_bits_rne(x):
+    """bf16 bit patterns of finite float32 values, rounded to nearest even
+    (synthetic bf16 operands; the reference's BFloat16::from_float turns
+    about half of all negative values into -inf, half_types.cpp:159-168)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 def keep_top2_of_4(w):
     """2:4 along the last axis: keep the two largest |w| of every group of
     four consecutive entries (NMSparsityPruning(2, 4) on continuous draws)."""

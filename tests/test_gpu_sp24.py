@@ -4,9 +4,11 @@ int8: int32 accumulators and requantised int8 are bit-exact against the
 oracle (quantized_matmul + quantize_tensor) and the golden vectors written
 by the compiled reference; at the full 11008 x 4096 x 512 size every row and
 every column is pinned by exact integer sum identities, and a sample of rows
-by the oracle.  bf16: fp32 output within 1e-2 relative error of the fp32
-product of the bf16-rounded operands (float64 reference; the MFMA sums in a
-different order, so bit equality is not expected).
+by the oracle.  bf16: operands rounded by the oracle's from_float (its
+sign quirk included); fp32 outputs within 1e-4 of sum |w| |x| of the
+float64 product of those operands (products of bf16 values are exact in
+fp32; the MFMA sums in a different order, so bit equality is not
+expected), infinities and NaN exactly where it has them.
 """
 import sys
 
@@ -135,27 +137,98 @@ def test_i8_full_size_properties(ctx):
     assert np.array_equal(Q[rows], O.orc_quantize(F, [os_], [0], O.I8))
 
 
-def rne_bf16(x):
-    """Round-to-nearest-even bf16 bits of finite float32 values."""
-    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+NEG_CARRY = np.float32(np.array([0xBF80C000], np.uint32).view(np.float32)[0])  # bf16 from_float: -inf
+NEG_DOWN = np.float32(np.array([0xBF803FFF], np.uint32).view(np.float32)[0])   # rounds down to -1
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (200, 512, 96), (1024, 2048, 256)])
-def test_bf16_within_tolerance(ctx, M, K, N):
-    rng = np.random.default_rng(M + K + N)
-    w = rng.standard_normal((M, K)).astype(np.float32)
+def round_down_negatives(a):
+    """Negative values with bit 15 cleared: their bf16 rounding never carries
+    out of the low half, where from_float's sign quirk would make them -inf
+    (half of all negative floats); positive values keep their RNE carries."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).copy()
+    u[(u >> 31) == 1] &= np.uint32(0xFFFF7FFF)
+    return u.view(np.float32)
+
+
+def bf16_operands(rng, M, K, N, quirk):
+    """A 2:4 weight and an activation rounded by the reference's
+    BFloat16::from_float (half_types.cpp:132-174, the oracle's
+    orc_f32_to_bf16): positive values round to nearest even (carries
+    included), negative ones round down; with quirk, three kept weights are
+    negatives whose rounding carries, which from_float makes -inf, and some
+    activations are the round-down case next to it."""
+    w = round_down_negatives(rng.standard_normal((M, K)).astype(np.float32))
     w = O.orc_apply_mask(w, O.orc_nm_mask(w.ravel(), 2, 4).reshape(M, K))
-    wb = rne_bf16(w)
-    xb = rne_bf16(rng.standard_normal((K, N)).astype(np.float32))
-    say(f"sp24 bf16 M={M} K={K} N={N}")
-    W = ctx.sp24_pack(wb.astype(np.uint16))
-    Y = W.gemm_bf16(xb.astype(np.uint16))
-    R = O.orc_bf16_to_f32(wb).astype(np.float64) @ O.orc_bf16_to_f32(xb).astype(np.float64)
-    err = np.abs(Y - R) / np.maximum(np.abs(R), 1e-3 * np.abs(R).max())
-    assert err.max() <= 1e-2, err.max()
-    F32 = O.orc_gemm(O.orc_bf16_to_f32(wb), O.orc_bf16_to_f32(xb))   # cpu_gemm on bf16 operands
-    assert (np.abs(Y - F32) <= 1e-2 * np.maximum(np.abs(F32), 1e-3 * np.abs(F32).max())).all()
+    x = round_down_negatives(rng.standard_normal((K, N)).astype(np.float32))
+    if quirk:
+        kept = np.argwhere(w != 0)
+        for r, k in kept[rng.choice(len(kept), 3, replace=False)]:
+            w[r, k] = NEG_CARRY
+        x[rng.random(x.shape) < 0.01] = NEG_DOWN
+    wb = O.orc_f32_to_bf16(w.ravel()).reshape(M, K)
+    xb = O.orc_f32_to_bf16(x.ravel()).reshape(K, N)
+    if quirk:
+        assert (wb == 0xFF80).sum() == 3
+    return wb, xb
+
+
+def check_bf16(Y, wb, xb, rows=None):
+    """Y against the float64 product of the bf16 operands (products of bf16
+    values are exact in fp32, so only the fp32 sums differ): infinities and
+    NaN where it has them, finite outputs within 1e-4 of sum |w| |x|."""
+    wf = O.orc_bf16_to_f32(wb).astype(np.float64)
+    xf = O.orc_bf16_to_f32(xb).astype(np.float64)
+    if rows is not None:
+        wf, Y = wf[rows], Y[rows]
+    with np.errstate(invalid="ignore", over="ignore"):
+        R = wf @ xf
+        S = np.abs(wf) @ np.abs(xf)
+    assert np.array_equal(np.isnan(Y), np.isnan(R))
+    inf = np.isinf(R)
+    assert np.array_equal(Y[inf], R[inf])
+    ok = np.isfinite(R)
+    assert (np.abs(Y[ok] - R[ok]) <= 1e-4 * S[ok] + 1e-30).all(), np.abs(Y[ok] - R[ok]).max()
+    return R
+
+
+# K % 256 == 0 with N % 128 == 0 reads X rows directly (ds_read_b64_tr_b16);
+# the others go through the transposed copy
+@pytest.mark.parametrize("M,K,N,quirk", [(64, 128, 64, False), (200, 512, 96, True), (33, 300, 70, True),
+                                         (1024, 2048, 256, False), (300, 1028, 129, True), (256, 512, 128, True)])
+def test_bf16_within_tolerance(ctx, M, K, N, quirk):
+    import torch
+
+    rng = np.random.default_rng(M + K + N)
+    wb, xb = bf16_operands(rng, M, K, N, quirk)
+    say(f"sp24 bf16 M={M} K={K} N={N} quirk={quirk}")
+    W = ctx.sp24_pack(wb)
+    Y = W.gemm_bf16(xb)
+    R = check_bf16(Y, wb, xb)
+    # device pointers, X rows 8 elements longer than N and Y rows 3 longer
+    dX = torch.from_numpy(np.concatenate([xb, np.zeros((K, 8), np.uint16)], 1).view(np.int16)).cuda()
+    dY = torch.zeros((M, N + 3), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    W.gemm_bf16_dev(dX.data_ptr(), N, dY.data_ptr(), ldx=N + 8, ldy=N + 3)
+    ctx.synchronize()
+    Yd = dY.cpu().numpy()
+    assert np.array_equal(Yd[:, :N].view(np.uint32), Y.view(np.uint32)) and not Yd[:, N:].any()
+    # and the composition with the reference's dense cpu_gemm on those operands
+    F32 = O.orc_gemm(O.orc_bf16_to_f32(wb), O.orc_bf16_to_f32(xb))
+    assert np.array_equal(np.isnan(F32), np.isnan(R)) and np.array_equal(F32[np.isinf(R)], R[np.isinf(R)])
+    W.free()
+
+
+def test_bf16_full_size(ctx):
+    """11008 x 4096 x 512 (the 2:4 benchmark shape) with the from_float
+    quirk in the weight: every output against the float64 product."""
+    rng = np.random.default_rng(3)
+    M, K, N = 11008, 4096, 512
+    wb, xb = bf16_operands(rng, M, K, N, True)
+    say("sp24 bf16 full size 11008 x 4096 x 512")
+    W = ctx.sp24_pack(wb)
+    Y = W.gemm_bf16(xb)
+    check_bf16(Y, wb, xb)
+    W.free()
 
 
 def test_rejects_non_24(ctx):
