@@ -966,75 +966,75 @@ void launch_bal_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx
                        W->bal_col, W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
 }
 
-// Fast 2 <= N <= 8 over the nnz-balanced copy: a persistent workgroup takes
-// groups b and b + gridDim.x (the copy holds at most two per CU), and walks
-// K chunk by chunk: the chunk's X rows are staged in LDS as rows of eight
-// floats (kcw + 1 rows with the zero row, 32 B each), then both groups'
-// records of that chunk are folded into per-lane sums, eight columns at a
-// time (two 16-byte LDS reads and eight FMAs per nonzero).  The sums of a
-// row's lanes meet by shuffles, then across the waves in LDS (waves 8..15
-// add theirs to waves 0..7 first, so the order is fixed).
+// Fast 2 <= N <= 8 over the nnz-balanced copy: a workgroup takes groups b
+// and b + gridDim.x (the copy holds at most two per CU), waves 0..7 the first
+// and 8..15 the second, and walks K chunk by chunk: the chunk's X rows are
+// staged in LDS as rows of eight floats (kcw + 1 rows with the zero row, 32 B
+// each), then each half of the workgroup folds its group's records of that
+// chunk into per-lane sums (the two groups' record streams, and the
+// latencies of their starts, overlap; walked one after the other with all
+// sixteen waves, the second group's start measured as a bubble).  Lanes work
+// in pairs: each lane loads its own record (four nonzeros of one row), takes
+// its partner's by DPP, and reads one 16-byte half of the X row of all eight
+// nonzeros (columns 4h .. 4h + 3 for lane parity h), so a pair reads a whole
+// 32-byte row.  Records are loaded a batch ahead of the one folded, and each
+// group's first batch of a chunk before the chunk is staged.  The sums of a
+// row's lanes meet by shuffles, then across the group's waves in LDS (waves
+// 4..7 of a half add theirs to waves 0..3 first, so the order is fixed).
 template <bool I8, int W, int U, bool XV>
 __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
     int K, int N, int ngroup, int nch, int kcw, const int4* __restrict__ meta, const int2* __restrict__ cmeta,
     const int32_t* __restrict__ perm, const void* __restrict__ vals, const uint16_t* __restrict__ cols,
     const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r,
     int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
-    static_assert(W == 16, "the cross-wave sum pairs waves w and w + 8");
-    constexpr int NT = 64 * W;
+    static_assert(W == 16, "two groups of eight waves; the cross-wave sum pairs waves w and w + 4");
+    constexpr int NT = 64 * W, WG = W / 2;
     extern __shared__ float4 xs[];  // [(kcw + 1) * 2]: row k at xs[2k], xs[2k + 1]
-    __shared__ float part[8][64][8];
-    const int tid = threadIdx.x, lane = tid & 63;
+    __shared__ float part[2][4][64][8];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane & 1;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = wave / WG, gw = wave % WG, gt = tid % (64 * WG);  // group half, wave and thread in it
     using ValT = typename std::conditional<I8, uint32_t, float4>::type;
     const ValT* V = static_cast<const ValT*>(vals);
     const uint2* Cl = reinterpret_cast<const uint2*>(cols);
-    const char* xb = reinterpret_cast<const char*>(xs);
-    int gs[2], lg[2];
-    gs[0] = blockIdx.x;
-    gs[1] = blockIdx.x + gridDim.x;
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) lg[gi] = gs[gi] < ngroup ? meta[gs[gi]].x : 0;
-    float acc[2][8];
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[gi][c] = 0.0f;
-    ValT v[U];
-    uint2 cc[U];
-    auto load = [&](int rec0, int nq, int R, int G, int r, int sub, int b) {
+    const char* xbh = reinterpret_cast<const char*>(xs) + 16 * h;  // this lane's half of every X row
+    const int grp = (int)blockIdx.x + half * (int)gridDim.x;
+    const bool live = grp < ngroup;
+    const int lgR = live ? __builtin_amdgcn_readfirstlane(meta[grp].x) : 0;
+    const int R = 1 << lgR, G = 64 >> lgR;
+    const int r = lane & (R - 1), sub = lane >> lgR, psub = (lane ^ 1) >> lgR;
+    // own[e]: the lane's row, column 4h + e; par[e]: the partner lane's row,
+    // same columns
+    float own[4] = {0.0f, 0.0f, 0.0f, 0.0f}, par[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    ValT va[U], vb[U];
+    uint2 ca[U], cb[U];
+    auto load = [&](ValT* v, uint2* cc, int rec0, int nq, int b) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t at = rec0 + (int64_t)min(b + sub + G * W * u, nq - 1) * R + r;
+            const int64_t at = rec0 + (int64_t)min(b + sub + G * WG * u, nq - 1) * R + r;
             v[u] = V[at];
             cc[u] = Cl[at];
         }
     };
-    // the output rows and scales of both groups (thread t < 8R writes row
-    // t / 8, column t % 8), loaded now rather than as dependent loads at the
-    // end
-    int orow[2] = {0, 0};
-    float oscale[2] = {1.0f, 1.0f};
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-        if (gs[gi] < ngroup && tid < (8 << lg[gi])) {
-            orow[gi] = perm[meta[gs[gi]].y + (tid >> 3)];
-            if constexpr (I8) oscale[gi] = rs[orow[gi]];
-        }
+    // the group's output row and scale (group thread t < 8R writes row t / 8,
+    // column t % 8), loaded now rather than as dependent loads at the end
+    int orow = 0;
+    float oscale = 1.0f;
+    if (live && gt < (8 << lgR)) {
+        orow = perm[meta[grp].y + (gt >> 3)];
+        if constexpr (I8) oscale = rs[orow];
     }
-    // the first group's first records of chunk 0 are requested before X is
-    // staged, so their latency and the staging's overlap
-    bool pre = false;
-    if (gs[0] < ngroup) {
-        const int lgR = __builtin_amdgcn_readfirstlane(lg[0]), R = 1 << lgR, G = 64 >> lgR;
-        const int2 cm = cmeta[gs[0] * nch];
-        const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
-        if (G * wave < nq) {
-            load(rec0, nq, R, G, lane & (R - 1), lane >> lgR, G * wave);
-            pre = true;
-        }
-    }
+    // DPP quad_perm [1, 0, 3, 2]: the partner lane's value
+    auto swap = [](auto v) { return __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false); };
+    const int step = G * WG * U, b0 = G * gw;
+    int2 cm = live ? cmeta[grp * nch] : make_int2(0, 0);
     for (int ch = 0; ch < nch; ++ch) {
+        const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
+        const int nit = b0 < nq ? (nq - b0 + step - 1) / step : 0;  // the wave's batches (uniform)
+        // the chunk's first batch is requested before X is staged, so their
+        // latencies overlap
+        if (nit > 0) load(va, ca, rec0, nq, b0);
+        if (live && ch + 1 < nch) cm = cmeta[grp * nch + ch + 1];
         // stage the chunk's X rows: eight 16-byte (XV) or 4-byte loads per
         // thread in flight, clamped; rows past the chunk or K are zero
         const int k0 = ch * kcw, nq4 = (kcw + 1) * 2;  // float4 slots
@@ -1071,84 +1071,102 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
             }
         }
         __syncthreads();
+        // one batch: U records of this lane and U of its partner; a record
+        // past the chunk's quad rows (a clamped repeat) adds nothing
+        auto fold = [&](const ValT* v, const uint2* cc, int b) {
 #pragma unroll
-        for (int gi = 0; gi < 2; ++gi) {
-            if (gs[gi] >= ngroup) continue;
-            const int lgR = __builtin_amdgcn_readfirstlane(lg[gi]), R = 1 << lgR, G = 64 >> lgR;
-            const int2 cm = cmeta[gs[gi] * nch + ch];
-            const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
-            const int r = lane & (R - 1), sub = lane >> lgR;
-            for (int b = G * wave; b < nq; b += G * W * U) {  // b: the wave's first quad row (uniform)
-                const int g0 = b + sub;
-                if (!(gi == 0 && pre)) load(rec0, nq, R, G, r, sub, b);
-                if (gi == 0) pre = false;
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const bool in = g0 + G * W * u < nq;
-                    float w[4];
-                    if constexpr (I8) {
-                        w[0] = (float)(int8_t)(v[u] & 0xFF);
-                        w[1] = (float)(int8_t)((v[u] >> 8) & 0xFF);
-                        w[2] = (float)(int8_t)((v[u] >> 16) & 0xFF);
-                        w[3] = (float)(int8_t)(v[u] >> 24);
-                    } else {
-                        w[0] = v[u].x; w[1] = v[u].y; w[2] = v[u].z; w[3] = v[u].w;
-                    }
-                    // offsets count x's floats from the start of chunk 0
-                    // (with the zeros after earlier chunks); a staged X row
-                    // is 32 bytes, eight times a float
-                    const uint32_t off[4] = {(cc[u].x & 0xFFFF) - cbase, (cc[u].x >> 16) - cbase,
-                                             (cc[u].y & 0xFFFF) - cbase, (cc[u].y >> 16) - cbase};
+            for (int u = 0; u < U; ++u) {
+                const bool in_own = b + sub + G * WG * u < nq, in_par = b + psub + G * WG * u < nq;
+                float wo[4], wp[4];
+                if constexpr (I8) {
+                    const uint32_t qo = v[u], qp = (uint32_t)swap(v[u]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const float4 lo = *reinterpret_cast<const float4*>(xb + (off[j] << 3));
-                        const float4 hi = *reinterpret_cast<const float4*>(xb + (off[j] << 3) + 16);
-                        if (in) {
-                            acc[gi][0] = __builtin_fmaf(w[j], lo.x, acc[gi][0]);
-                            acc[gi][1] = __builtin_fmaf(w[j], lo.y, acc[gi][1]);
-                            acc[gi][2] = __builtin_fmaf(w[j], lo.z, acc[gi][2]);
-                            acc[gi][3] = __builtin_fmaf(w[j], lo.w, acc[gi][3]);
-                            acc[gi][4] = __builtin_fmaf(w[j], hi.x, acc[gi][4]);
-                            acc[gi][5] = __builtin_fmaf(w[j], hi.y, acc[gi][5]);
-                            acc[gi][6] = __builtin_fmaf(w[j], hi.z, acc[gi][6]);
-                            acc[gi][7] = __builtin_fmaf(w[j], hi.w, acc[gi][7]);
-                        }
+                        wo[j] = (float)(int8_t)((qo >> (8 * j)) & 0xFF);
+                        wp[j] = (float)(int8_t)((qp >> (8 * j)) & 0xFF);
+                    }
+                } else {
+                    wo[0] = v[u].x; wo[1] = v[u].y; wo[2] = v[u].z; wo[3] = v[u].w;
+                    wp[0] = __int_as_float(swap(__float_as_int(v[u].x)));
+                    wp[1] = __int_as_float(swap(__float_as_int(v[u].y)));
+                    wp[2] = __int_as_float(swap(__float_as_int(v[u].z)));
+                    wp[3] = __int_as_float(swap(__float_as_int(v[u].w)));
+                }
+                const uint32_t px = (uint32_t)swap(cc[u].x), py = (uint32_t)swap(cc[u].y);
+                // offsets count x's floats from the start of chunk 0 (with
+                // the zeros after earlier chunks); a staged X row is 32
+                // bytes, eight times a float
+                const uint32_t oo[4] = {(cc[u].x & 0xFFFF) - cbase, (cc[u].x >> 16) - cbase,
+                                        (cc[u].y & 0xFFFF) - cbase, (cc[u].y >> 16) - cbase};
+                const uint32_t op[4] = {(px & 0xFFFF) - cbase, (px >> 16) - cbase, (py & 0xFFFF) - cbase,
+                                        (py >> 16) - cbase};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 xo = *reinterpret_cast<const float4*>(xbh + (oo[j] << 3));
+                    const float4 xp = *reinterpret_cast<const float4*>(xbh + (op[j] << 3));
+                    if (in_own) {
+                        own[0] = __builtin_fmaf(wo[j], xo.x, own[0]);
+                        own[1] = __builtin_fmaf(wo[j], xo.y, own[1]);
+                        own[2] = __builtin_fmaf(wo[j], xo.z, own[2]);
+                        own[3] = __builtin_fmaf(wo[j], xo.w, own[3]);
+                    }
+                    if (in_par) {
+                        par[0] = __builtin_fmaf(wp[j], xp.x, par[0]);
+                        par[1] = __builtin_fmaf(wp[j], xp.y, par[1]);
+                        par[2] = __builtin_fmaf(wp[j], xp.z, par[2]);
+                        par[3] = __builtin_fmaf(wp[j], xp.w, par[3]);
                     }
                 }
             }
+        };
+        // batch i + 1's loads are issued before batch i is folded (past the
+        // last batch they are clamped repeats, never folded)
+        int i = 0;
+        for (; i + 2 <= nit; i += 2) {
+            load(vb, cb, rec0, nq, b0 + (i + 1) * step);
+            fold(va, ca, b0 + i * step);
+            load(va, ca, rec0, nq, b0 + (i + 2) * step);
+            fold(vb, cb, b0 + (i + 1) * step);
         }
+        if (i < nit) fold(va, ca, b0 + i * step);
         __syncthreads();  // the next chunk overwrites X
     }
+    // R = 1: every lane's record and its partner's are of row 0
+    if (R == 1) {
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-        if (gs[gi] >= ngroup) continue;  // uniform
-        const int lgR = __builtin_amdgcn_readfirstlane(lg[gi]), R = 1 << lgR;
-        float* a = acc[gi];
+        for (int e = 0; e < 4; ++e) own[e] += par[e];
+    }
+    // lanes of one row and half: lane ^ s for s = max(R, 2) .. 32
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-            for (int o = R; o < 64; o <<= 1) a[c] += __shfl_xor(a[c], o, 64);
-        if (wave >= 8 && lane < R) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) part[wave - 8][lane][c] = a[c];
+    for (int e = 0; e < 4; ++e)
+        for (int s = R < 2 ? 2 : R; s < 64; s <<= 1) {
+            own[e] += __shfl_xor(own[e], s, 64);
+            if (R > 1) par[e] += __shfl_xor(par[e], s, 64);
         }
-        __syncthreads();
-        if (wave < 8 && lane < R) {
+    // lane r < max(R, 2) holds row r's half h (own) and, for R > 1, row r ^
+    // 1's half h (par): every (row, column) once per wave
+    auto put = [&](float (*dst)[8], bool add) {
+        if (lane < (R < 2 ? 2 : R)) {
+            const int ro = R < 2 ? 0 : lane, rp = lane ^ 1;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) part[wave][lane][c] += a[c];
-        }
-        __syncthreads();
-        if (tid < R * 8) {  // row tid / 8, column tid % 8
-            const int rr = tid >> 3, c = tid & 7;
-            float sum = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 8; ++w) sum += part[w][rr][c];
-            if (c < N) {
-                if constexpr (I8) sum *= oscale[gi];
-                const int64_t f = (int64_t)orow[gi] * ldy_r + (int64_t)c * ldy_c;
-                Y[f] = bias_add(sum, f, bias, c_size, beta, act);
+            for (int e = 0; e < 4; ++e) {
+                dst[ro][4 * h + e] = add ? dst[ro][4 * h + e] + own[e] : own[e];
+                if (R > 1) dst[rp][4 * h + e] = add ? dst[rp][4 * h + e] + par[e] : par[e];
             }
         }
-        __syncthreads();  // part is rewritten for the second group
+    };
+    if (gw >= 4) put(part[half][gw - 4], false);
+    __syncthreads();
+    if (gw < 4) put(part[half][gw], true);
+    __syncthreads();
+    if (live && gt < R * 8) {  // row gt / 8, column gt % 8
+        const int rr = gt >> 3, c = gt & 7;
+        float sum = ((part[half][0][rr][c] + part[half][1][rr][c]) + part[half][2][rr][c]) + part[half][3][rr][c];
+        if (c < N) {
+            if constexpr (I8) sum *= oscale;
+            const int64_t f = (int64_t)orow * ldy_r + (int64_t)c * ldy_c;
+            Y[f] = bias_add(sum, f, bias, c_size, beta, act);
+        }
     }
 }
 
