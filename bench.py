@@ -401,7 +401,10 @@ def bench_decode_int8(ctx):
     28 launches are also captured once into a HIP graph and replayed.  (An
     empty kernel costs about 2.4 us per launch on a stream and 1.6 us in a
     graph, but behind kernels of 6 us and more the dispatch is hidden: the
-    two forms measure the same.)"""
+    two forms measure the same.)  `stacked` times the same layers with the
+    projections that read one activation stacked into one weight (q, k, v:
+    12288 x 4096; gate, up: 22016 x 4096): 4 launches per layer over the same
+    nonzeros and rows, each output row what its own projection gives."""
     import numpy as np
     import torch
 
@@ -420,6 +423,17 @@ def bench_decode_int8(ctx):
             for _ in range(count):
                 seq.append((name, ctx.csr_upload(M_, K_, ip, ix, q, row_scales=sc)))
         layers.append(seq)
+    # q, k, v and gate, up stacked: (tag, K, W) per launch
+    stacked_parts = (("qkv", "qkvo_4096x4096", 3), ("o", "qkvo_4096x4096", 1),
+                     ("gate_up", "gate_up_11008x4096", 2), ("down", "down_4096x11008", 1))
+    stacked = []
+    for _ in range(NL):
+        seq = []
+        for tag, name, count in stacked_parts:
+            M_, K_, _ = shapes[name]
+            ip, ix, q, sc = workloads.csr_vstack([data[name]] * count)
+            seq.append((tag, K_, ctx.csr_upload(M_ * count, K_, ip, ix, q, row_scales=sc)))
+        stacked.append(seq)
     res = {}
     for B, mode in ((1, "fast"), (8, "fast"), (1, "strict"), (8, "strict")):
         bufs = {name: (torch.randn((K_, B), dtype=torch.float32, device="cuda"),
@@ -461,6 +475,24 @@ def bench_decode_int8(ctx):
         torch.cuda.synchronize()
         graph_ms = a.elapsed_time(b) / reps * 32 / NL
         del g
+        sbufs = {tag: (bufs[name][0], torch.empty((W.M, B), dtype=torch.float32, device="cuda"))
+                 for (tag, name, _), (_, _, W) in zip(stacked_parts, stacked[0])}
+
+        def step_stacked():
+            for seq in stacked:
+                for tag, _, W in seq:
+                    X, Y = sbufs[tag]
+                    W.spmm_dev(X.data_ptr(), B, Y.data_ptr(), mode=mode)
+
+        for _ in range(3):
+            step_stacked()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            step_stacked()
+        b.record()
+        torch.cuda.synchronize()
+        stacked_ms = a.elapsed_time(b) / reps * 32 / NL
         nnz = {name: len(data[name][2]) for name in shapes}
         # algorithmic bytes: 1 B value + 2 B column (uint16 suffices for K <=
         # 11008) per nonzero, 8 B per row (pointer and scale), x and y
@@ -468,7 +500,7 @@ def bench_decode_int8(ctx):
                         for name, (M_, K_, count) in shapes.items())
         flops = 32 * sum(count * 2 * nnz[name] * B for name, (_, _, count) in shapes.items())
         out = {}
-        for tag, ms in (("eager", eager_ms), ("graph", graph_ms)):
+        for tag, ms in (("eager", eager_ms), ("graph", graph_ms), ("stacked", stacked_ms)):
             out[tag] = {"step_ms": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
                         "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
                         "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -477,6 +509,9 @@ def bench_decode_int8(ctx):
         log(f"decode int8 batch {B} {mode}: {out}")
     for seq in layers:
         for _, W in seq:
+            W.free()
+    for seq in stacked:
+        for _, _, W in seq:
             W.free()
     return res
 

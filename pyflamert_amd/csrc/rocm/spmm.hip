@@ -524,15 +524,17 @@ void launch_chain_x(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx,
                        W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
 }
 
-// Strict product for 2 <= N <= 8 columns over the row-chain copy with 16-row
-// slabs: every (row, column) pair is its own in-order chain, one lane each,
+// Strict product for 2 <= N <= 8 columns over the row-chain copy, 16 rows
+// per workgroup (a copy with 32- or 64-row slabs, which the N = 1 kernel
+// prefers for tall weights, is taken 16 rows of a slab at a time): every
+// (row, column) pair is its own in-order chain, one lane each,
 // so NC / 4 waves fold (NC = 2, 4 or 8, N <= NC) while four producer waves
 // load the values and offsets two chunks ahead, gather the x rows from global
 // memory (16-byte loads when x rows are aligned and N == NC >= 4) and write
 // RN(w * x[col, n]) for every column.  Steps past a row's count (and quad
 // rows past the slab) give +0; their gather addresses are clamped into x.
 // LDS: 2 x 32 quad rows x NC x 16 rows x 16 B of products.
-constexpr int kChainNR = 16;  // slab height this kernel takes
+constexpr int kChainNR = 16;  // rows per workgroup of this kernel
 constexpr int kChainNP = 4;   // producer waves
 
 template <int NC>
@@ -540,7 +542,7 @@ constexpr int chain_n_folders() { return NC >= 4 ? NC / 4 : 1; }
 
 template <bool I8, int NC, bool XV>
 __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spmm_chain(
-    int K, int N, int cshift, const int32_t* __restrict__ q0, const int32_t* __restrict__ lens,
+    int K, int N, int cshift, int rstride, const int32_t* __restrict__ q0, const int32_t* __restrict__ lens,
     const int32_t* __restrict__ perm, const void* __restrict__ vals, const uint32_t* __restrict__ cols,
     const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r,
     int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
@@ -552,7 +554,11 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
     float4* const buf1 = dyn + CH * NC * R;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int s = blockIdx.x;
+    // a copy with slabs of rstride = 16, 32 or 64 rows: workgroup b takes
+    // rows 16 * (b % (rstride / 16)) .. + 15 of slab b / (rstride / 16) (the
+    // slab's quad rows and record stride are the copy's)
+    const int nsub = rstride / R;
+    const int s = blockIdx.x / nsub, ro = (blockIdx.x % nsub) * R;
     const int qb = q0[s], nq = q0[s + 1] - qb;
     const int nch = (nq + CH - 1) / CH;
     const int iters = (nch + kChainXUnroll) / kChainXUnroll * kChainXUnroll;
@@ -560,7 +566,7 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
         const int c = wave * 64 + lane;  // chain: column c / R of slab row c % R
         const int n = c / R, r = c % R;
         const bool act_lane = c < NC * R && n < N;
-        const int row = act_lane ? perm[s * R + r] : -1;
+        const int row = act_lane ? perm[s * rstride + ro + r] : -1;
         float acc = 0.0f;
         auto rd = [&](const float4* b, float4* v, int batch) {
 #pragma unroll
@@ -600,8 +606,8 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
     const ValT* V = static_cast<const ValT*>(vals);
     const uint2* Cl = reinterpret_cast<const uint2*>(cols);
     const int r = lane % R, sub = lane / R;
-    const int prow = perm[s * R + r];
-    const int len = lens[s * R + r];
+    const int prow = perm[s * rstride + ro + r];
+    const int len = lens[s * rstride + ro + r];
     const float scale = (I8 && prow >= 0) ? rs[prow] : 1.0f;
     const int pw = wave - F;
     ValT v0[T], v1[T], v2[T];
@@ -610,7 +616,7 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int g = max(min(i * CH + (pw + P * t) * QW + sub, nq - 1), 0);
-            const int64_t at = (int64_t)(qb + g) * R + r;
+            const int64_t at = (int64_t)(qb + g) * rstride + ro + r;
             v[t] = V[at];
             cc[t] = Cl[at];
         }
@@ -696,8 +702,9 @@ void launch_chain_n(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64
                                     (int)lds));
         if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)W->chain_nslab), dim3(64 * (chain_n_folders<NC>() + kChainNP)), lds,
-                       ctx->stream, (int)W->K, N, W->chain_xlds ? 2 : 0, W->chain_q0, W->chain_len, W->chain_perm,
+    const unsigned grid = (unsigned)(W->chain_nslab * (W->chain_rows / kChainNR));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * (chain_n_folders<NC>() + kChainNP)), lds, ctx->stream,
+                       (int)W->K, N, W->chain_xlds ? 2 : 0, (int)W->chain_rows, W->chain_q0, W->chain_len, W->chain_perm,
                        W->chain_val, static_cast<const uint32_t*>(W->chain_col), W->row_scale, X, ldx, Y, ldy_r,
                        ldy_c, bias, c_size, beta, act);
 }
@@ -1601,7 +1608,7 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
         if (W->chain_rows == 16) launch_chain_x<I8, 16>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else if (W->chain_rows == 32) launch_chain_x<I8, 32>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
         else launch_chain_x<I8, 64>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
-    } else if (N >= 2 && N <= 8 && W->chain_q0 != nullptr && W->chain_rows == kChainNR && W->chain_c16) {
+    } else if (N >= 2 && N <= 8 && W->chain_q0 != nullptr && W->chain_rows % kChainNR == 0 && W->chain_c16) {
         launch_chain_cols<I8>(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else if (N == 1 && W->chain_q0 != nullptr && W->K * ldx < INT32_MAX) {
         const dim3 grid((unsigned)W->chain_nslab), block(64 * (kChainP + 1));

@@ -126,3 +126,24 @@ def dequant_rows(ip, q, scale):
     """float32 values RN((float)q * scale[row]) of an int8 CSR."""
     rows = np.repeat(np.arange(len(ip) - 1), np.diff(ip))
     return (q.astype(np.float32) * scale[rows]).astype(np.float32)
+
+
+def csr_vstack(parts):
+    """Row-wise concatenation of CSR matrices with the same K: parts are
+    (indptr, indices, values[, row_scales]) tuples; returns the same tuple
+    for the stacked matrix (rows of parts[0] first).  Sibling projections
+    that read one activation (q, k and v; gate and up) stacked this way run
+    as one product whose output rows are the parts' outputs in order."""
+    ips, ixs, vs = [], [], []
+    base = 0
+    for p in parts:
+        ip = np.asarray(p[0], np.int64)
+        ips.append(ip[:-1] + base if ips else ip[:-1])
+        base += int(ip[-1])
+        ixs.append(np.asarray(p[1]))
+        vs.append(np.asarray(p[2]))
+    indptr = np.concatenate(ips + [np.array([base], np.int64)])
+    out = (indptr, np.concatenate(ixs), np.concatenate(vs))
+    if all(len(p) > 3 for p in parts):
+        out += (np.concatenate([np.asarray(p[3], np.float32) for p in parts]),)
+    return out

@@ -116,6 +116,55 @@ def test_decode_fast_normwise(decode_layer):
         assert close_normwise(W.spmm(Xa, mode="fast"), O.orc_csr_spmm(M, K, ip, ix, vals, Xa)), (name, B)
 
 
+def test_decode_stacked_siblings(ctx):
+    """q, k and v (three different 4096 x 4096 weights) stacked into one
+    12288 x 4096 product, as the decode bench's stacked form runs them:
+    strict is bit-exact against the oracle on each projection alone, fast
+    within 1e-5 normwise; batch 1 and 8."""
+    M, K = DECODE["qkvo_4096x4096"]
+    parts = [workloads.csr_int8_lognormal(M, K, 0.3, 0.5, 0.02, seed=40 + i) for i in range(3)]
+    ip, ix, q, sc = workloads.csr_vstack(parts)
+    W = ctx.csr_upload(3 * M, K, ip, ix, q, row_scales=sc)
+    try:
+        for B in (1, 8):
+            X = workloads.dense_normal((K, B), 1.0, seed=300 + B)
+            Xa = X[:, 0].copy() if B == 1 else X
+            refs = [O.orc_csr_spmm(M, K, p[0], p[1], workloads.dequant_rows(p[0], p[2], p[3]), Xa) for p in parts]
+            for mode in ("strict", "fast"):
+                say(f"decode stacked q/k/v 12288x4096 batch {B} {mode}")
+                Y = W.spmm(Xa, mode=mode)
+                for i, R in enumerate(refs):
+                    Yi = Y[i * M:(i + 1) * M]
+                    if mode == "strict":
+                        assert bits_equal(Yi, R), (B, i, first_diff(Yi, R))
+                    else:
+                        assert close_normwise(Yi, R), (B, i)
+    finally:
+        W.free()
+
+
+@pytest.mark.parametrize("count", [2, 3])
+def test_decode_stacked_tall_strict(ctx, count):
+    """gate and up stacked (22016 x 4096), and three 11008 x 4096 weights
+    (33024 rows): tall enough that the row-chain copy takes 32- and 64-row
+    slabs for the vector kernel; the 2..8-column strict kernel walks them 16
+    rows at a time.  Bit-exact against the oracle at batch 3 and 8."""
+    M, K = DECODE["gate_up_11008x4096"]
+    parts = [workloads.csr_int8_lognormal(M, K, 0.3, 0.5, 0.02, seed=50 + i) for i in range(count)]
+    ip, ix, q, sc = workloads.csr_vstack(parts)
+    vals = workloads.dequant_rows(ip, q, sc)
+    W = ctx.csr_upload(count * M, K, ip, ix, q, row_scales=sc)
+    try:
+        for B in (3, 8):
+            X = workloads.dense_normal((K, B), 1.0, seed=400 + B)
+            say(f"decode stacked {count} x 11008x4096 batch {B} strict")
+            Y = W.spmm(X, mode="strict")
+            R = O.orc_csr_spmm(count * M, K, ip, ix, vals, X)
+            assert bits_equal(Y, R), (count, B, first_diff(Y, R))
+    finally:
+        W.free()
+
+
 def test_decode_device_pointers_strided(ctx, decode_layer):
     """The device-pointer entry the bench times: batch 8 with X and Y rows
     padded (ldx 12, ldy 10), both modes."""
