@@ -21,6 +21,8 @@ import pytest
 from oracle import oracle as O
 from pyflamert_amd import workloads
 
+from bounds import gamma_bound_ok
+
 pytestmark = pytest.mark.gpu
 
 DECODE = {"qkvo_4096x4096": (4096, 4096), "gate_up_11008x4096": (11008, 4096),
@@ -114,6 +116,36 @@ def test_decode_fast_normwise(decode_layer):
         Xa = Xb[:, 0].copy() if B == 1 else Xb
         say(f"decode {name} batch {B} fast, NaN and -inf in X")
         assert close_normwise(W.spmm(Xa, mode="fast"), O.orc_csr_spmm(M, K, ip, ix, vals, Xa)), (name, B)
+
+
+def test_fast_mode_forward_error_bound(ctx, decode_layer):
+    """Fast mode against the error bound every summation order meets (not
+    against the oracle's own order, which near cancelling rows differs from
+    the exact sum by as much): batch 1, 2 and 8 at the decode shapes."""
+    name, M, K, ip, ix, vals, W = decode_layer
+    for B in (1, 2, 8):
+        X = workloads.dense_normal((K, B), 1.0, seed=500 + B)
+        Xa = X[:, 0].copy() if B == 1 else X
+        say(f"decode {name} batch {B} fast, forward error bound")
+        ok, worst = gamma_bound_ok(W.spmm(Xa, mode="fast"), M, K, ip, ix, vals, Xa)
+        assert ok, (name, B, worst)
+
+
+@pytest.mark.parametrize("N", [1, 16, 64, 256])
+def test_fast_mode_forward_error_bound_uniform(ctx, N):
+    """The same bound for the 4096 x 4096, 10 % fp32 weight at N = 1 .. 256
+    (the column-slice and balanced kernels with fused multiply-adds)."""
+    M = K = 4096
+    ip, ix, v = workloads.csr_uniform(M, K, 0.1, 0.02, seed=1234)
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    try:
+        X = workloads.dense_normal((K, N), 1.0, seed=600 + N)
+        Xa = X[:, 0].copy() if N == 1 else X
+        say(f"uniform 4096x4096 N={N} fast, forward error bound")
+        ok, worst = gamma_bound_ok(W.spmm(Xa, mode="fast"), M, K, ip, ix, v, Xa, extra=1)
+        assert ok, (N, worst)
+    finally:
+        W.free()
 
 
 def test_decode_stacked_siblings(ctx):

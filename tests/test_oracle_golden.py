@@ -349,3 +349,27 @@ def test_neighbours_golden(golden):
     d = x - x.mean(1, keepdims=True)
     ln64 = (sc * d / np.sqrt((d * d).mean(1, keepdims=True) + 1e-5) + bi).astype(np.float32)
     assert not same(ln64, g["ln_y"])
+
+
+def test_forward_error_bound_helper():
+    """The bound the fast-mode GPU tests use: the oracle's storage-order sums
+    and a reversed-order float32 sum (another summation order) meet it; an
+    output off by 1e-4 of the largest fails it."""
+    from bounds import gamma_bound_ok
+    from pyflamert_amd import workloads
+
+    M = K = 512
+    ip, ix, v = workloads.csr_uniform(M, K, 0.2, 0.02, seed=11)
+    X = workloads.dense_normal((K, 4), 1.0, seed=12)
+    R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+    assert gamma_bound_ok(R, M, K, ip, ix, v, X, extra=1)[0]
+    rev = np.zeros_like(R)
+    for r in range(M):
+        acc = np.zeros(4, np.float32)
+        for j in range(ip[r + 1] - 1, ip[r] - 1, -1):
+            acc = (acc + v[j] * X[ix[j]]).astype(np.float32)
+        rev[r] = acc
+    assert gamma_bound_ok(rev, M, K, ip, ix, v, X, extra=1)[0]
+    bad = R.copy()
+    bad[7, 2] += np.float32(1e-4) * np.abs(R).max()
+    assert not gamma_bound_ok(bad, M, K, ip, ix, v, X, extra=1)[0]
