@@ -1388,21 +1388,27 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
 // against 6.6k clocks for the last chunk, which stages nothing; with a DMA
 // in flight the compiler makes every later LDS read of that wave wait for
 // all its loads.)
-template <bool XVEC, int W>
-constexpr bool sell_stager() { return XVEC && W <= 8; }
-template <bool XVEC, int W>
-constexpr int sell_threads() { return 64 * (W + (sell_stager<XVEC, W>() ? 1 : 0)); }
+template <bool XVEC, int W, bool XT>
+constexpr bool sell_stager() { return XVEC && !XT && W <= 8; }
+template <bool XVEC, int W, bool XT>
+constexpr int sell_threads() { return 64 * (W + (sell_stager<XVEC, W, XT>() ? 1 : 0)); }
 
-template <bool FAST, bool XVEC, int W>
-__global__ __launch_bounds__((sell_threads<XVEC, W>())) void k_spmm_sell(
+// XT (16-wave launches): X is given transposed, as the Gemm form's
+// activation A (N x K, row-major, rows ldx floats apart, 16-byte aligned,
+// K % 4 == 0): every chunk is staged from A's rows through registers into
+// the same LDS layout, scaled by alpha when `scale` (RN(alpha * a), the
+// operand the reference's Gemm multiplies), so no transposed copy is
+// written first.
+template <bool FAST, bool XVEC, int W, bool XT>
+__global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
     int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ soff, const int4* __restrict__ blk, const float* __restrict__ X,
     int64_t ldx, float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, int yvec,
-    const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    const float* __restrict__ bias, int64_t c_size, float beta, int act, float alpha, int scale) {
     // two buffers of kc + 1 rows of 16 floats; row kc of each is zero
     extern __shared__ float4 xs[];
     constexpr int NT = 64 * W;  // the walking waves' threads
-    constexpr bool STAGER = sell_stager<XVEC, W>();
+    constexpr bool STAGER = sell_stager<XVEC, W, XT>();
     constexpr int DPI = sell_loads_per_iter<W>();
     const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, q = lane & 3;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1444,8 +1450,43 @@ __global__ __launch_bounds__((sell_threads<XVEC, W>())) void k_spmm_sell(
             xb[e] = v;
         }
     };
+    // XT staging of chunk c by threads t, t + nthr, ..: piece e is the float4
+    // of A's row n0 + e % 16 at k = 4 (e / 16) (eight loads in flight,
+    // clamped addresses), written as four floats of four LDS rows; piece e
+    // writes its floats in the order j = (i + e / 16) % 4 (i = 0..3), so the
+    // four groups of 16 lanes in one write instruction hit four different
+    // 16-bank quarters (rows 64 B apart would otherwise all meet in one).
+    // Rows past N or K are zero.
+    auto stage_xt = [&](int c, int t, int nthr) {
+        const int k0 = c * kc, total = 4 * kc;  // 16 rows x kc / 4 pieces
+        float* xb = reinterpret_cast<float*>(xs + (c & 1) * bufq);
+        for (int e0 = 0; e0 < total; e0 += 8 * nthr) {
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = min(e0 + t + nthr * i, total - 1), n = e & 15, k = k0 + 4 * (e >> 4);
+                v[i] = *reinterpret_cast<const float4*>(X + (int64_t)min(n0 + n, N - 1) * ldx + min(k, K - 4));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = e0 + t + nthr * i;
+                if (e < total) {
+                    const int n = e & 15, kq = e >> 4, kl = 4 * kq;
+                    const bool ok = n0 + n < N && k0 + kl < K;
+                    const float a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const int j = (ii + kq) & 3;
+                        const float x = j == 0 ? a[0] : (j == 1 ? a[1] : (j == 2 ? a[2] : a[3]));
+                        const float y = scale ? alpha * x : x;
+                        xb[(kl + j) * 16 + n] = ok ? y : 0.0f;
+                    }
+                }
+            }
+        }
+    };
     auto sync_chunk = [&]() {
-        if constexpr (XVEC) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads have landed
+        if constexpr (XVEC && !XT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads have landed
         __syncthreads();
     };
 
@@ -1483,7 +1524,9 @@ __global__ __launch_bounds__((sell_threads<XVEC, W>())) void k_spmm_sell(
             if (c + 1 < nch) __syncthreads();
         }
     } else {
-    if constexpr (XVEC) {
+    if constexpr (XT) {
+        stage_xt(0, tid, NT);
+    } else if constexpr (XVEC) {
         for (int i = 0; i < nd; ++i) dma(0, i);
     } else {
         stage_regs(0);
@@ -1500,7 +1543,7 @@ __global__ __launch_bounds__((sell_threads<XVEC, W>())) void k_spmm_sell(
             float4* nxt = xs + ((c + 1) & 1) * bufq;
             // the 16-wave launch (four waves per SIMD hide each other's
             // latencies) stages whole chunks between walks instead
-            if (XVEC && W <= 8 && more)
+            if (XVEC && !XT && W <= 8 && more)
                 sell_walk<FAST, true, DPI>(blk, s0 + lane, T, xb, nxt, xcol + (int64_t)k1 * ldx, ldx, lane, wave, W,
                                            nld - 1, min(kc, K - k1) - 1, d, a0, a1, a2, a3);
             else
@@ -1508,7 +1551,9 @@ __global__ __launch_bounds__((sell_threads<XVEC, W>())) void k_spmm_sell(
                                             a1, a2, a3);
         }
         if (more) {
-            if constexpr (XVEC) {
+            if constexpr (XT) {
+                stage_xt(c + 1, tid, NT);  // the other buffer: last read in chunk c - 1
+            } else if constexpr (XVEC) {
                 for (; d < nd; ++d) dma(c + 1, d);
             } else {
                 stage_regs(c + 1);  // the other buffer: last read in chunk c - 1
@@ -1558,10 +1603,11 @@ int next_pow2(int n) {
 
 
 // Column-slice kernel launch with W waves per workgroup.
-template <bool FAST, bool XVEC, int W>
+template <bool FAST, bool XVEC, int W, bool XT>
 void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
-    auto kern = k_spmm_sell<FAST, XVEC, W>;
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act,
+                   float alpha) {
+    auto kern = k_spmm_sell<FAST, XVEC, W, XT>;
     const size_t lds = (size_t)(Wt->sell_kc + 1) * 64 * 2;
     // more than 64 KiB of dynamic LDS has to be allowed per kernel and device
     static uint64_t allowed = 0;  // bit d: done on device d (< 64)
@@ -1572,42 +1618,63 @@ void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
         if (bit && lds == (size_t)(pfr::kSellMaxKC + 1) * 64 * 2) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
     }
     dim3 grid((unsigned)((Wt->sell_nslab + W - 1) / W), (unsigned)((N + pfr::kSellCols - 1) / pfr::kSellCols));
-    hipLaunchKernelGGL(kern, grid, dim3(sell_threads<XVEC, W>()), lds, ctx->stream, N, (int)Wt->K, Wt->sell_kc,
-                       Wt->sell_nch,
-                       Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, Wt->sell_blk, X, ldx, Y, ldy_r, ldy_c, yvec,
-                       bias, c_size, beta, act);
+    hipLaunchKernelGGL(kern, grid, dim3(sell_threads<XVEC, W, XT>()), lds, ctx->stream, N, (int)Wt->K,
+                       Wt->sell_kc, Wt->sell_nch, Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, Wt->sell_blk, X, ldx,
+                       Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act, alpha, alpha != 1.0f ? 1 : 0);
 }
 
-template <bool FAST, bool XVEC>
-void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act) {
-    // One workgroup runs per CU (its LDS takes most of the CU), so the launch
-    // takes ceil(workgroups / CUs) rounds.  A round of 4-, 8- and 16-wave
-    // workgroups takes about 1 : 1.30 : 2.14 (measured on the 4096 x 4096,
-    // 10 % weight at N = 64, 128 and 256, one round each); the wave count
-    // with the fewest estimated clocks runs, the larger on a tie.  Fewer than
-    // four waves lose: each wave then stages more of X than it walks.
+// Waves per workgroup of the column-slice launch for N columns, and its
+// rounds.  One workgroup runs per CU (its LDS takes most of the CU), so the
+// launch takes ceil(workgroups / CUs) rounds.  A round of 4-, 8- and 16-wave
+// workgroups takes about 1 : 1.30 : 2.14 (measured on the 4096 x 4096, 10 %
+// weight at N = 64, 128 and 256, one round each); the wave count with the
+// fewest estimated clocks runs, the larger on a tie.  Fewer than four waves
+// lose: each wave then stages more of X than it walks.
+int sell_waves(const pfr_ctx* ctx, const pfr_csr* Wt, int64_t N, int64_t* rounds_out = nullptr) {
     const int64_t slices = (N + pfr::kSellCols - 1) / pfr::kSellCols;
     auto rounds = [&](int64_t w) { return ((Wt->sell_nslab + w - 1) / w * slices + ctx->num_cu - 1) / ctx->num_cu; };
     const int64_t c16 = rounds(16) * 214, c8 = rounds(8) * 130, c4 = rounds(4) * 100;
-#define PFR_SELLW(WV) launch_sell_w<FAST, XVEC, WV>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act)
-    if (c16 <= c8 && c16 <= c4) PFR_SELLW(16);
-    else if (c8 <= c4) PFR_SELLW(8);
-    else PFR_SELLW(4);
+    const int w = (c16 <= c8 && c16 <= c4) ? 16 : (c8 <= c4 ? 8 : 4);
+    if (rounds_out) *rounds_out = rounds(w);
+    return w;
+}
+
+template <bool FAST, bool XVEC, bool XT>
+void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
+                   int64_t ldy_r, int64_t ldy_c, int yvec, const float* bias, int64_t c_size, float beta, int act,
+                   float alpha) {
+#define PFR_SELLW(WV) \
+    launch_sell_w<FAST, XVEC, WV, XT>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act, alpha)
+    const int w = sell_waves(ctx, Wt, N);
+    if constexpr (XT) {
+        PFR_SELLW(16);  // the transposed activation is taken only where 16 waves run (sell_one_round)
+    } else {
+        if (w == 16) PFR_SELLW(16);
+        else if (w == 8) PFR_SELLW(8);
+        else PFR_SELLW(4);
+    }
 #undef PFR_SELLW
 }
 
+// xt: X is the transposed activation (see k_spmm_sell), alpha its scale.
 void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
-                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, bool fast, int act) {
+                 int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, bool fast, int act,
+                 bool xt = false, float alpha = 1.0f) {
     const bool xvec = (ldx % 4 == 0) && (N % 4 == 0) && aligned16(X);
     const int yvec = (ldy_c == 1 && ldy_r % 4 == 0 && aligned16(Y) && bias == nullptr) ? 1 : 0;
-    if (fast) {
-        if (xvec) launch_sell_x<true, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
-        else launch_sell_x<true, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
+#define PFR_SELLX(F, XV, T) \
+    launch_sell_x<F, XV, T>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act, alpha)
+    if (xt) {
+        if (fast) PFR_SELLX(true, false, true);
+        else PFR_SELLX(false, false, true);
+    } else if (fast) {
+        if (xvec) PFR_SELLX(true, true, false);
+        else PFR_SELLX(true, false, false);
     } else {
-        if (xvec) launch_sell_x<false, true>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
-        else launch_sell_x<false, false>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act);
+        if (xvec) PFR_SELLX(false, true, false);
+        else PFR_SELLX(false, false, false);
     }
+#undef PFR_SELLX
 }
 
 // Row, small-N and vector kernels for one value type.
@@ -1717,18 +1784,23 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
 // and an inf mask (ballots), and only a column with either walks the rows,
 // writing the epilogue of NaN (bias and activation as the product kernels
 // apply them) where the rule says so.  Columns without non-finite values --
-// the normal case -- cost one read of X.
-__global__ __launch_bounds__(256) void k_nonfinite_fix(const float* __restrict__ X, int64_t ldx, int64_t K,
-                                                       int64_t N, int64_t M, const uint64_t* __restrict__ bm,
-                                                       int64_t nw, float* __restrict__ Y, int64_t ldy_r,
-                                                       int64_t ldy_c, const float* __restrict__ bias,
-                                                       int64_t c_size, float beta, int act) {
+// the normal case -- cost one read of X.  x[k, c] is X[k * sk + c * sn]
+// (sn = 1: X as the products read it; sk = 1: the Gemm form's activation
+// read in place), times alpha when `scale`.
+__global__ __launch_bounds__(256) void k_nonfinite_fix(const float* __restrict__ X, int64_t sk, int64_t sn,
+                                                       float alpha, int scale, int64_t K, int64_t N, int64_t M,
+                                                       const uint64_t* __restrict__ bm, int64_t nw,
+                                                       float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c,
+                                                       const float* __restrict__ bias, int64_t c_size, float beta,
+                                                       int act) {
     __shared__ float t[64][65];  // t[c][k]
     const int64_t kt = blockIdx.x, k0 = kt * 64, c0 = (int64_t)blockIdx.y * 64;
     for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-        const int cc = e % 64, kk = e / 64;
+        // consecutive threads along whichever index X's rows run
+        const int cc = sn == 1 ? e % 64 : e / 64, kk = sn == 1 ? e / 64 : e % 64;
         const int64_t k = k0 + kk, c = c0 + cc;
-        t[cc][kk] = (k < K && c < N) ? X[k * ldx + c] : 0.0f;
+        const float v = (k < K && c < N) ? X[k * sk + c * sn] : 0.0f;
+        t[cc][kk] = scale ? alpha * v : v;
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1748,14 +1820,29 @@ __global__ __launch_bounds__(256) void k_nonfinite_fix(const float* __restrict__
     }
 }
 
+// The column-slice kernel serves this product (float32 weight, N >= 16).
+bool sell_serves(const pfr_csr* W, int64_t N) {
+    return W->vdt != PFR_I8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535;
+}
+
+// Its launch for N columns runs in one round, with the 16-wave workgroups
+// (where every wave of the workgroup stages).
+bool sell_one_round(const pfr_ctx* ctx, const pfr_csr* W, int64_t N) {
+    int64_t rounds = 0;
+    return sell_waves(ctx, W, N, &rounds) == 16 && rounds == 1;
+}
+
 // Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
+// xt: X is the Gemm form's activation A (N x K, rows ldx apart) read in
+// place, scaled by alpha; only where sell_serves.
 void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
                  int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta,
-                 bool fast, int act) {
+                 bool fast, int act, bool xt = false, float alpha = 1.0f) {
     if (W->M == 0 || N == 0) return;
     const bool i8 = W->vdt == PFR_I8;
-    if (!i8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535) {
-        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast, act);
+    pfr::require(!xt || sell_serves(W, N), "transposed activation without the column-slice copy");
+    if (sell_serves(W, N)) {
+        launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast, act, xt, alpha);
     } else if (i8) {
         if (fast) launch_csr_kernels<true, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         else launch_csr_kernels<false, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
@@ -1767,7 +1854,8 @@ void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int6
     if (W->pattern != nullptr && W->K > 0) {
         pfr::require((N + 63) / 64 < 65536, "too many columns for the non-finite fix-up's grid");
         const dim3 grid((unsigned)((W->K + 63) / 64), (unsigned)((N + 63) / 64));
-        hipLaunchKernelGGL(k_nonfinite_fix, grid, dim3(256), 0, ctx->stream, X, ldx, W->K, N, W->M, W->pattern,
+        hipLaunchKernelGGL(k_nonfinite_fix, grid, dim3(256), 0, ctx->stream, X, xt ? (int64_t)1 : ldx,
+                           xt ? ldx : (int64_t)1, alpha, xt && alpha != 1.0f ? 1 : 0, W->K, N, W->M, W->pattern,
                            W->pattern_nw, Y, ldy_r, ldy_c, bias, c_size, beta, act);
         PFR_HIP(hipGetLastError());
     }
@@ -1824,6 +1912,17 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     };
     if (K == 0) {
         // No terms: every output is +0 (+ bias); At is never read.
+    } else if (!transA && ws == nullptr && sell_serves(BT, Mb) && K % 4 == 0 && aligned16(A) &&
+               sell_one_round(ctx, BT, Mb)) {
+        // the column-slice kernel stages A's rows itself, transposed and
+        // scaled on the way into LDS (the allocation-free entry keeps its
+        // workspace copy and the size limit it states).  Its workgroups
+        // stage through registers, more slowly than the direct-to-LDS copy of
+        // a transposed A, so this pays off when the launch runs in one round
+        // (every workgroup stages once, side by side): 768 x 768 at 1024
+        // tokens 26.0 -> 21.7 us; 3072 x 768 (three rounds) 66.1 -> 67.8 us.
+        launch_spmm(ctx, BT, A, Mb, K, Y, 1, Nf, C, c_size, beta, mode == PFR_MODE_FAST, act, true, alpha);
+        return;
     } else if (!transA) {
         float* t = tbuf();
         dim3 grid((unsigned)((K + 63) / 64), (unsigned)((Mb + 63) / 64));

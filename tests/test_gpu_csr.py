@@ -135,11 +135,14 @@ def test_gemm_form_vs_oracle(ctx, Mb):
     B[rng.random(B.shape) < 0.8] = 0.0
     A = rng.standard_normal((Mb, K)).astype(np.float32)
     bias = rng.standard_normal(Nf).astype(np.float32)
-    say(f"gemm form Mb={Mb}")
     BT = ctx.csr_from_dense(B, transpose=True)
-    Y = ctx.gemm_csr(A, BT, 1.0, 1.0, bias)
-    R = O.orc_gemm(A, B, bias, 1.0, 1.0)
-    assert bits_equal(Y, R), first_diff(Y, R)
+    # alpha != 1 scales A as it is staged (Mb >= 16: the column-slice kernel
+    # reads A in place) or in the transposed copy
+    for alpha, beta in ((1.0, 1.0), (0.37, -0.5)):
+        say(f"gemm form Mb={Mb} alpha={alpha} beta={beta}")
+        Y = ctx.gemm_csr(A, BT, alpha, beta, bias)
+        R = O.orc_gemm(A, B, bias, alpha, beta)
+        assert bits_equal(Y, R), (alpha, first_diff(Y, R))
 
 
 def test_edge_cases(ctx):
