@@ -1389,16 +1389,17 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
 // in flight the compiler makes every later LDS read of that wave wait for
 // all its loads.)
 template <bool XVEC, int W, bool XT>
-constexpr bool sell_stager() { return XVEC && !XT && W <= 8; }
+constexpr bool sell_stager() { return (XVEC || XT) && W <= 8; }
 template <bool XVEC, int W, bool XT>
 constexpr int sell_threads() { return 64 * (W + (sell_stager<XVEC, W, XT>() ? 1 : 0)); }
 
-// XT (16-wave launches): X is given transposed, as the Gemm form's
-// activation A (N x K, row-major, rows ldx floats apart, 16-byte aligned,
-// K % 4 == 0): every chunk is staged from A's rows through registers into
-// the same LDS layout, scaled by alpha when `scale` (RN(alpha * a), the
-// operand the reference's Gemm multiplies), so no transposed copy is
-// written first.
+// XT: X is given transposed, as the Gemm form's activation A (N x K,
+// row-major, rows ldx floats apart, 16-byte aligned, K % 4 == 0): each
+// chunk is staged from A's rows through registers into the same LDS layout,
+// scaled by alpha when `scale` (RN(alpha * a), the operand the reference's
+// Gemm multiplies), so no transposed copy is written first.  The 16-wave
+// launch stages every chunk with all its waves; the 4- and 8-wave launches
+// take it only for one chunk, staged by all their waves.
 template <bool FAST, bool XVEC, int W, bool XT>
 __global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
     int N, int K, int kc, int nch, int nslab, const int32_t* __restrict__ perm,
@@ -1495,15 +1496,21 @@ __global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
             // the staging wave: every 16-row load of each chunk, one chunk
             // ahead of the walk, then the same barriers as the walking waves
             auto stage = [&](int c) {
-                const int k0 = c * kc, last = min(kc, K - k0) - 1;
-                lds_char* dst = (lds_char*)(xs + (c & 1) * bufq);
-                for (int j = 0; j < nld; ++j) {
-                    const float* src = xcol + (int64_t)(k0 + min(j * 16 + r, last)) * ldx;
-                    __builtin_amdgcn_global_load_lds(src, dst + j * 1024, 16, 0, 0);
+                if constexpr (XT) {
+                    stage_xt(c, lane, 64);
+                } else {
+                    const int k0 = c * kc, last = min(kc, K - k0) - 1;
+                    lds_char* dst = (lds_char*)(xs + (c & 1) * bufq);
+                    for (int j = 0; j < nld; ++j) {
+                        const float* src = xcol + (int64_t)(k0 + min(j * 16 + r, last)) * ldx;
+                        __builtin_amdgcn_global_load_lds(src, dst + j * 1024, 16, 0, 0);
+                    }
+                    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the chunk has landed
                 }
-                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the chunk has landed
             };
-            stage(0);
+            // XT: every thread stages chunk 0 (launched only with one chunk)
+            if constexpr (XT) stage_xt(0, tid, NT + 64);
+            else stage(0);
             __syncthreads();
             for (int c = 0; c + 1 < nch; ++c) {
                 stage(c + 1);  // the other buffer: last read in chunk c - 1
@@ -1511,6 +1518,7 @@ __global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
             }
             return;
         }
+        if constexpr (XT) stage_xt(0, tid, NT + 64);
         __syncthreads();
         for (int c = 0; c < nch; ++c) {
             const char* xb = reinterpret_cast<const char*>(xs + (c & 1) * bufq) + q * 16;
@@ -1646,13 +1654,9 @@ void launch_sell_x(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
 #define PFR_SELLW(WV) \
     launch_sell_w<FAST, XVEC, WV, XT>(ctx, Wt, X, N, ldx, Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act, alpha)
     const int w = sell_waves(ctx, Wt, N);
-    if constexpr (XT) {
-        PFR_SELLW(16);  // the transposed activation is taken only where 16 waves run (sell_one_round)
-    } else {
-        if (w == 16) PFR_SELLW(16);
-        else if (w == 8) PFR_SELLW(8);
-        else PFR_SELLW(4);
-    }
+    if (w == 16) PFR_SELLW(16);
+    else if (w == 8) PFR_SELLW(8);
+    else PFR_SELLW(4);
 #undef PFR_SELLW
 }
 
@@ -1825,11 +1829,13 @@ bool sell_serves(const pfr_csr* W, int64_t N) {
     return W->vdt != PFR_I8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535;
 }
 
-// Its launch for N columns runs in one round, with the 16-wave workgroups
-// (where every wave of the workgroup stages).
+// Its launch for N columns runs in one round, with 16-wave workgroups or,
+// for a single chunk, 4 or 8 (their chunk 0 is staged by every wave; later
+// chunks would fall to the staging wave alone).
 bool sell_one_round(const pfr_ctx* ctx, const pfr_csr* W, int64_t N) {
     int64_t rounds = 0;
-    return sell_waves(ctx, W, N, &rounds) == 16 && rounds == 1;
+    const int w = sell_waves(ctx, W, N, &rounds);
+    return rounds == 1 && (w == 16 || W->sell_nch == 1);
 }
 
 // Launch the kernel that fits N.  Output (row, c) -> Y[row*ldy_r + c*ldy_c].
