@@ -202,7 +202,7 @@ constexpr int kSellRows = 16;      // rows per slab (one wave: 4 lanes x 4 colum
 constexpr int kSellCols = 16;      // columns of X per workgroup slice
 constexpr int kSellMaxKC = 1024;   // K rows per LDS chunk (1024 x 64 B = 64 KiB, two buffers)
 constexpr int kSellStepPad = 8;    // steps per (slab, chunk) run are a multiple of this (one group)
-constexpr int kSellTail = 256;     // int4 after the last run, read by the unconditional prefetch
+constexpr int kSellTail = 512;     // int4 after the last run, read by the unconditional prefetch (8 groups)
 constexpr int kBalChunk = 4096;    // most columns per chunk of the balanced copy
 }
 

@@ -1366,6 +1366,90 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
     if constexpr (MORE) store_next();
 }
 
+// The walk of one run for the 4-wave launch's walking waves (one wave per
+// SIMD, nothing else to hide their latencies): a ring of eight groups' int4
+// (loads seven groups ahead), the X rows of group g + 1 read from LDS before
+// the products of group g, kept apart by a scheduling barrier so the reads
+// are issued a whole group before their use, and in strict mode the group's
+// 32 products computed before its adds (in storage order), so no add waits
+// on the multiply just before it.  Measured against the plain walk on the
+// 4096 x 4096, 10 % weight: N = 16 19.6 -> 17.3 us, N = 64 20.4 -> 19.0 us
+// strict and 19.1 -> 15.8 us fast; with two waves per SIMD (the 8-wave
+// launch) it did not help.
+template <bool FAST>
+__device__ __forceinline__ void sell_walk_pipe(const int4* __restrict__ blk, int p, int T, const char* __restrict__ xb,
+                                               float& a0, float& a1, float& a2, float& a3) {
+    constexpr int R = 8;
+    auto fetch = [&](const int4 w, float4 (&xv)[8]) {
+        static_for<0, 8>([&](auto tc) {
+            constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+            const int o = __builtin_amdgcn_mov_dpp((t & 1) ? w.z : w.x, ctrl, 0xF, 0xF, true);
+            xv[t] = *reinterpret_cast<const float4*>(xb + o);
+        });
+    };
+    auto accum = [&](const int4 w, const float4 (&xv)[8]) {
+        if constexpr (FAST) {
+            static_for<0, 8>([&](auto tc) {
+                constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+                const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
+                a0 = __builtin_fmaf(wv, xv[t].x, a0);
+                a1 = __builtin_fmaf(wv, xv[t].y, a1);
+                a2 = __builtin_fmaf(wv, xv[t].z, a2);
+                a3 = __builtin_fmaf(wv, xv[t].w, a3);
+            });
+        } else {
+            // the group's 32 products first, then the adds in storage order
+            float pr[8][4];
+            static_for<0, 8>([&](auto tc) {
+                constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+                const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
+                pr[t][0] = wv * xv[t].x;
+                pr[t][1] = wv * xv[t].y;
+                pr[t][2] = wv * xv[t].z;
+                pr[t][3] = wv * xv[t].w;
+            });
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                a0 = a0 + pr[t][0];
+                a1 = a1 + pr[t][1];
+                a2 = a2 + pr[t][2];
+                a3 = a3 + pr[t][3];
+            }
+        }
+    };
+    int4 wr[R];
+    static_for<0, R>([&](auto ic) { wr[decltype(ic)::value] = blk[p + 64 * decltype(ic)::value]; });
+    float4 xa[8], xc[8];
+    fetch(wr[0], xa);  // in bounds and unused when T = 0
+    auto group = [&](auto ic, bool has_next) {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i & 1) {
+            if (has_next) fetch(wr[(i + 1) % R], xa);
+            __builtin_amdgcn_sched_barrier(0);
+            accum(wr[i], xc);
+        } else {
+            if (has_next) fetch(wr[(i + 1) % R], xc);
+            __builtin_amdgcn_sched_barrier(0);
+            accum(wr[i], xa);
+        }
+    };
+    int t = 0;
+    for (; t + R <= T; t += R) {
+        static_for<0, R>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            group(ic, true);  // past the run's end the next group's reads are in bounds and unused
+            wr[i] = blk[p + 64 * (R + i)];
+            asm volatile("" ::: "memory");
+        });
+        p += 64 * R;
+    }
+    static_for<0, R - 1>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        if (t + i < T) group(ic, t + i + 1 < T);
+    });
+}
+
 // Column-slice kernel over the sliced-ELL copy (layout at pfr_csr::sell_blk).
 // A workgroup of W waves owns W slabs (16 rows each) and one 16-column slice
 // of X.  X is staged chunk by chunk (kc rows of 64 B) into two LDS buffers:
@@ -1526,8 +1610,11 @@ __global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
             if (slab < nslab) {
                 const int s0 = soff[slab * (nch + 1) + c], s1 = soff[slab * (nch + 1) + c + 1];
                 const int T = __builtin_amdgcn_readfirstlane((s1 - s0) / 64);
-                sell_walk<FAST, false, DPI>(blk, s0 + lane, T, xb, xs, xcol, ldx, lane, wave, W, nld - 1, 0, d, a0,
-                                            a1, a2, a3);
+                if constexpr (W == 4)
+                    sell_walk_pipe<FAST>(blk, s0 + lane, T, xb, a0, a1, a2, a3);
+                else
+                    sell_walk<FAST, false, DPI>(blk, s0 + lane, T, xb, xs, xcol, ldx, lane, wave, W, nld - 1, 0, d,
+                                                a0, a1, a2, a3);
             }
             if (c + 1 < nch) __syncthreads();
         }
