@@ -1312,6 +1312,7 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
             const int o = __builtin_amdgcn_mov_dpp((t & 1) ? w.z : w.x, ctrl, 0xF, 0xF, true);
             xv[t] = *reinterpret_cast<const float4*>(xb + o);
         });
+        if constexpr (FAST) {
         static_for<0, 8>([&](auto tc) {
             constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
             const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
@@ -1320,6 +1321,28 @@ __device__ __forceinline__ void sell_walk(const int4* __restrict__ blk, int p, i
             a2 = madd<FAST>(a2, wv, xv[t].z);
             a3 = madd<FAST>(a3, wv, xv[t].w);
         });
+        } else {
+            // the group's 32 products first, then the adds in storage order
+            // behind a scheduling barrier, so no add waits on the multiply
+            // just before it (N = 256: 44.8 -> 43.2 us, same bits)
+            float pr[8][4];
+            static_for<0, 8>([&](auto tc) {
+                constexpr int t = decltype(tc)::value, ctrl = (t / 2) * 0x55;
+                const float wv = __int_as_float(__builtin_amdgcn_mov_dpp((t & 1) ? w.w : w.y, ctrl, 0xF, 0xF, true));
+                pr[t][0] = wv * xv[t].x;
+                pr[t][1] = wv * xv[t].y;
+                pr[t][2] = wv * xv[t].z;
+                pr[t][3] = wv * xv[t].w;
+            });
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                a0 = a0 + pr[t][0];
+                a1 = a1 + pr[t][1];
+                a2 = a2 + pr[t][2];
+                a3 = a3 + pr[t][3];
+            }
+        }
     };
     const int r = lane >> 2;
     constexpr int ND = MORE ? DPI : 1;
