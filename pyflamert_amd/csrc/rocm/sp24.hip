@@ -41,6 +41,10 @@ struct pfr_sp24 {
     float* w_scale = nullptr; // [M] (per-tensor scales expanded)
     float w_scale_max = 0.0f; // the largest of them
     int32_t* row_sum = nullptr;  // int8: [Mp] sum over k of W[m, k] (the zero-point correction)
+    // int8: idx regrouped by four row blocks, [Mp/64][Kp/128][64][4]: element
+    // r of lane l is idx[(4g + r)][step][l], so a wave owning row blocks 4g ..
+    // 4g + 3 loads a step's positions with one 16-byte load per lane
+    uint32_t* idx4 = nullptr;
 };
 
 namespace {
@@ -51,7 +55,7 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 void free_sp24(pfr_sp24* w) {
     if (!w) return;
-    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale, (void*)w->row_sum})
+    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale, (void*)w->row_sum, (void*)w->idx4})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -233,21 +237,45 @@ __device__ __forceinline__ int xrow_swizzle(int k) { return ((k >> 1) & 3) | (((
 // integer and the addend is below half an ulp.  The clamp runs in float
 // (exact on integers), and one select supplies the x86 value.
 // INRANGE: p is known finite with |p| < 2^31 (the host bounds |acc| * scale
-// * (1 / out_scale) for the whole launch), so the select is not needed.
+// * (1 / out_scale) for the whole launch), so the select is not needed, and
+// the clamp can come first: rounding is monotone and the bounds are
+// integers, so clamping p to [-128, 127] and then rounding gives the same
+// value, and the conversion to int (which truncates) does the trunc.
 template <bool INRANGE>
 __device__ __forceinline__ int32_t round_clamp_i8(float p) {
+    if constexpr (INRANGE) {
+        const float c = __builtin_amdgcn_fmed3f(p, -128.0f, 127.0f);
+        return (int32_t)(c + __builtin_copysignf(0.49999997f, c));
+    }
     const float r = __builtin_truncf(p + __builtin_copysignf(0.49999997f, p));
     const float c = __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
-    if constexpr (INRANGE) return (int32_t)c;
     return (int32_t)(__builtin_fabsf(r) < 2147483648.0f ? c : -128.0f);
+}
+
+// The per-row weight scales of this lane's 16 output rows of the int8 2:4
+// GEMM's tile (wave w: row blocks mb0 + 4w + i, rows 4kb + r of each), from
+// clamped rows, loaded together so they cost one load latency.
+__device__ __forceinline__ void sp24_i8_row_scales(float (&wsv)[4][4], const float* __restrict__ ws, int64_t mb0,
+                                                   int M) {
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), kb = (t & 63) >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wsv[i][r] = ws[min((int)(mb0 + w * 4 + i) * 16 + 4 * kb + r, M - 1)];
 }
 
 // The epilogue of the int8 2:4 GEMM: wave w of the workgroup holds the
 // accumulators of tile rows 64w .. 64w + 63 (row blocks 4w + i) x columns
-// 16j + c; tile is an LDS buffer of 256 x 128 bytes no longer in use.
+// 16j + c; tile + 128 ml (ml in 64w .. 64w + 63) is LDS no longer in use,
+// which only wave w touches: each wave requantises its rows there and
+// stores them itself, so the waves need no barrier between the two.  The
+// 16-byte chunk j of row ml sits at chunk j ^ ((ml >> 2) & 3): a byte write
+// covers rows 4kb + r of a row block (kb = 0..3), whose 128-byte rows would
+// otherwise all start in the same bank, and the 16-byte reads of two
+// neighbouring rows stay on distinct banks.
 template <int OUT>
 __device__ __forceinline__ void sp24_i8_epilogue(
-    const v4i (&acc)[4][8], char* tile, int64_t mb0, int64_t n0, int M, int N, const float* __restrict__ ws,
+    const v4i (&acc)[4][8], char* tile, int64_t mb0, int64_t n0, int M, int N, const float (&wsv)[4][4],
     float xs, float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec,
     int32_t x_zp, int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
     const int32_t* __restrict__ row_sum) {
@@ -256,17 +284,14 @@ __device__ __forceinline__ void sp24_i8_epilogue(
     const float xs_eff = xs_dev ? *xs_dev : xs;
     const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
     const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
-    // This lane's 16 rows: their scales (and row sums, for a zero-point
-    // correction) loaded together, from clamped rows, so the epilogue waits
-    // for one load latency rather than one per row.
-    float wsv[4][4];
+    // the row sums of this lane's 16 rows, for a zero-point correction
+    // (loaded together, from clamped rows)
     uint32_t rsv[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = min((int)(mb0 + w * 4 + i) * 16 + 4 * kb + r, M - 1);
-            if constexpr (OUT != PFR_SP24_OUT_I32) wsv[i][r] = ws[m];
             rsv[i][r] = zcorr ? (uint32_t)row_sum[m] : 0u;
         }
     // the exact accumulator of a row (int32 wrap-around arithmetic; the true
@@ -296,7 +321,7 @@ __device__ __forceinline__ void sp24_i8_epilogue(
                             q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(prod)) + (uint32_t)out_zp);
                             q = q < -128 ? -128 : (q > 127 ? 127 : q);
                         }
-                        tile[ml * 128 + 16 * j + c] = (char)q;
+                        tile[ml * 128 + 16 * (j ^ ((ml >> 2) & 3)) + c] = (char)q;
                     }
                 }
             }
@@ -308,18 +333,26 @@ __device__ __forceinline__ void sp24_i8_epilogue(
             requant(std::false_type{}, std::false_type{});
         }
         __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
-        __builtin_amdgcn_s_barrier();
+        // the wave's 64 rows x 8 pieces, 8 per lane: all read from LDS first,
+        // then stored
+        v4i piece[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {  // 256 rows x 8 pieces = 8 per thread
-            const int q16 = t + kI8Threads * i, ml = q16 >> 3, cc = q16 & 7;
+        for (int i = 0; i < 8; ++i) {
+            const int q16 = l + 64 * i, ml = 64 * w + (q16 >> 3), cc = q16 & 7;
+            piece[i] = *reinterpret_cast<const v4i*>(tile + ml * 128 + 16 * (cc ^ ((ml >> 2) & 3)));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q16 = l + 64 * i, ml = 64 * w + (q16 >> 3), cc = q16 & 7;
             const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
             if (m >= M) continue;
             int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
-            const char* src = tile + ml * 128 + 16 * cc;
             if (yvec && n + 16 <= N) {
-                *reinterpret_cast<v4i*>(yr + n) = *reinterpret_cast<const v4i*>(src);
+                *reinterpret_cast<v4i*>(yr + n) = piece[i];
             } else {
-                for (int b = 0; b < 16 && n + b < N; ++b) yr[n + b] = src[b];
+#pragma unroll
+                for (int b = 0; b < 16; ++b)
+                    if (n + b < N) yr[n + b] = (int8_t)(piece[i][b / 4] >> (8 * (b % 4)));
             }
         }
     } else {
@@ -523,7 +556,220 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
     step(fb, fa, st3, st0, -1);
     __builtin_amdgcn_s_waitcnt(0);  // the tail's loads have landed
     __builtin_amdgcn_s_barrier();
-    sp24_i8_epilogue<OUT>(acc, st0, mb0, n0, M, N, ws, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
+    float wsv[4][4];
+    if constexpr (OUT != PFR_SP24_OUT_I32) sp24_i8_row_scales(wsv, ws, mb0, M);
+    sp24_i8_epilogue<OUT>(acc, st0, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
+                          xs_dev, zp_dev, row_sum);
+}
+
+// int8 2:4 GEMM with the weight streamed into registers: the tile, waves
+// and MFMA order of k_sp24_i8 (256 x 128 outputs, wave w owning rows 64w ..
+// 64w + 63 and all 128 columns), but each wave loads its own four row
+// blocks' packed values and positions straight from global memory into a
+// ring of eight register slots (one per k step, 20 VGPRs each; the packed
+// order is the MFMA's lane order, so one 16-byte load per row block and
+// step, and one for the four blocks' positions from the regrouped idx4),
+// and only X goes through LDS, in eight 16 KiB stages filled by
+// direct-to-LDS loads.  Against k_sp24_i8 this takes the weight's 20 KiB per
+// step out of LDS (written once, read once: 40 KiB of the 120 KiB of LDS
+// traffic per step) and keeps seven steps of loads in flight per wave
+// instead of three, which the weight, streamed from HBM, needs to cover its
+// latency: nine loads per step, so seven steps are the 63 vector-memory
+// instructions a wave can have outstanding.
+// Per step s (slot and stage u = s % 8) each wave runs the 32 MFMAs of
+// column blocks j = 0..7, reading the B fragment of column block j + 3
+// (the next step's blocks 0..2 for j >= 5) from LDS while block j's MFMAs
+// run, in a ring of four fragment registers.  Before reading the next
+// step's first block it waits for its own loads of step s + 1 (vmcnt: the
+// loads of steps s + 2 .. s + 6, 12 per step, may still be in flight) and
+// for its LDS reads, and meets the other waves at the barrier: stage s + 1
+// is then complete, and every wave has read all of stage s, so the loads of
+// step s + 7 can go to stage (s + 7) % 8 and register slot (s + 7) % 8 (the
+// previous step's).  Steps past the end load the last step again, into
+// slots nothing reads, so the count of loads per step, and every wait,
+// stays fixed.  X is the row-major activation (XROW form of k_sp24_i8);
+// nkt is a multiple of 8.  The eight stages are separate arrays so the
+// compiler's wait counting sees that a stage load never writes the stages
+// being read.
+constexpr int kRSlots = 8, kRLead = 7, kRLoads = 9, kRStage = 128 * 128;
+// the last step issued before step s's loads (sr_last(0): the prologue's)
+constexpr int sr_last(int s) { return s + kRLead - 1; }
+
+template <int OUT, int NKT>
+__global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
+    int nkt_arg, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
+    const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
+    float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec, int ntn,
+    int32_t x_zp, int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
+    const int32_t* __restrict__ row_sum) {
+    __shared__ __attribute__((aligned(1024))) char b0[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b1[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b2[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b3[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b4[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b5[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b6[kRStage];
+    __shared__ __attribute__((aligned(1024))) char b7[kRStage];
+    __shared__ __attribute__((aligned(16))) float scl[kI8TileM];  // the tile's row scales
+    constexpr int nkt = NKT;
+    (void)nkt_arg;
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
+    const int kb = l >> 4, c = l & 15;
+    int mt, nt;
+    {
+        const int G = (int)gridDim.x, L = (int)blockIdx.x, xcd = L & 7, slot = L >> 3;
+        const int q = G >> 3, rem = G & 7;
+        const int T = xcd * q + min(xcd, rem) + slot;
+        mt = T / ntn;
+        nt = T % ntn;
+    }
+    const int64_t mb0 = (int64_t)mt * (kI8TileM / 16);
+    const int64_t n0 = (int64_t)nt * kI8TileN;
+    auto stage = [&](auto uc) -> char* {
+        constexpr int u = decltype(uc)::value;
+        if constexpr (u == 0) return b0;
+        else if constexpr (u == 1) return b1;
+        else if constexpr (u == 2) return b2;
+        else if constexpr (u == 3) return b3;
+        else if constexpr (u == 4) return b4;
+        else if constexpr (u == 5) return b5;
+        else if constexpr (u == 6) return b6;
+        else return b7;
+    };
+    // this wave's row blocks mb0 + 4w + i: element (row block, step) at
+    // (rb * nkt + step) * 64 + lane
+    const v4i* abase = A + (mb0 + 4 * w) * nkt * 64 + l;
+    const v4i* ibase = reinterpret_cast<const v4i*>(I) + (mb0 / 4 + w) * nkt * 64 + l;
+    const int64_t rbs = (int64_t)nkt * 64;
+    // B: the step's 128 X rows, row n = 8 (w + 4i) + l / 8 loaded by this
+    // lane (16-byte chunk (l % 8) ^ xrow_swizzle(n) of the tile's 128 columns)
+    const v4i* bsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = 8 * (w + 4 * i) + (l >> 3);
+        const int chunk = (l & 7) ^ xrow_swizzle(n);
+        bsrc[i] = reinterpret_cast<const v4i*>(B + (int64_t)n * ldb + n0 + 16 * chunk);
+    }
+    const int64_t b_step = 128 * ldb / 16;  // v4i per k step
+    v4i ar[kRSlots][4];
+    v4i ir[kRSlots];
+    // the nine loads of step TS (a compile-time step, below nkt) into slot
+    // and stage TS % 8
+    auto issue = [&](auto tc) {
+        constexpr int ts = decltype(tc)::value, u = ts % kRSlots;
+        char* st = stage(std::integral_constant<int, u>{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ar[u][i] = abase[i * rbs + ts * 64];
+        ir[u] = ibase[ts * 64];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)ts * b_step, PFR_LDS(st + 8 * (w + 4 * i) * 128), 16,
+                                             0, 0);
+    };
+    // B fragment of column block j from a stage (see k_sp24_i8, XROW form)
+    const int trk = (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
+    const int trf = xrow_swizzle(16 * kb + (c >> 1));
+    auto fetch_b = [&](v8i& f, const char* st, int j) {
+        v2i q[4];
+        const char* bp = st + trk + 16 * (j ^ trf);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            q[r] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (__attribute__((address_space(3))) v2i*)(bp + 1024 * (r & 1) + 8192 * (r >> 1)));
+        f = v8i{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
+    };
+    v4i acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    v8i bq[4];
+    auto vm_wait = [](int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (0 << 8); };
+    // the epilogue's row scales go to LDS ahead of everything (their latency
+    // is then hidden by the whole product): row 64w + l by lane l of wave w,
+    // clamped to the last row
+    if constexpr (OUT != PFR_SP24_OUT_I32)
+        __builtin_amdgcn_global_load_lds(ws + min((int)(mb0 * 16) + t, M - 1), PFR_LDS(scl + 64 * w), 4, 0, 0);
+    // Load schedule: the prologue issues steps 0 .. 6 and waits for step 0;
+    // then step s issues, after its barrier, step s + 7 (none past the end).
+    // The wait of step s is for step s + 1: the steps issued after it, nine
+    // loads each, may still be in flight (all counts are compile-time).
+    // (Issuing fewer steps up front and catching up two per step starts the
+    // MFMAs ~3k clocks earlier but costs more than that in the first steps:
+    // the CU's address unit, not the latency, paces the loads there.)  Every wave issues step 0
+    // before any wave issues step 1 (a barrier): the address unit takes
+    // loads in arrival order, and the first MFMAs wait for every wave's step
+    // 0.  Each step's loads are kept apart by scheduling barriers: the waits
+    // count them in step order, and the LDS stages are filled by loads the
+    // compiler does not wait for itself.
+    auto prologue_issue = [&](auto tc) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue(tc);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    static_assert(nkt > sr_last(0), "the prologue issues seven steps");
+    prologue_issue(std::integral_constant<int, 0>{});
+    __builtin_amdgcn_s_barrier();
+    static_for<1, sr_last(0) + 1>([&](auto tc) { prologue_issue(tc); });
+    __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * sr_last(0)));
+    __builtin_amdgcn_s_barrier();
+    fetch_b(bq[0], b0, 0);
+    fetch_b(bq[1], b0, 1);
+    fetch_b(bq[2], b0, 2);
+    // step S (compile-time)
+    auto step = [&](auto sc) {
+        constexpr int S = decltype(sc)::value, u = S % kRSlots, un = (u + 1) % kRSlots;
+        constexpr int first = sr_last(S) + 1, last = std::min(sr_last(S + 1), nkt - 1);
+        constexpr int later = std::max(0, std::min(sr_last(S), nkt - 1) - S - 1);  // issued after step S + 1
+        const char* cur = stage(std::integral_constant<int, u>{});
+        const char* nxt = stage(std::integral_constant<int, un>{});
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, 5>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            fetch_b(bq[(j + 3) % 4], cur, j + 3);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(ar[u][i], bq[j % 4], acc[i][j], ir[u][i], 0, 0);
+        });
+        static_for<0, 20>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * later));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<first, last + 1>([&](auto tc) { issue(tc); });
+        static_for<5, 8>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            fetch_b(bq[(j + 3) % 4], nxt, j - 5);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(ar[u][i], bq[j % 4], acc[i][j], ir[u][i], 0, 0);
+        });
+        static_for<0, 12>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            if constexpr (g < kRLoads * std::max(0, last - first + 1))
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (next loads)
+        });
+    };
+    static_for<0, nkt>([&](auto sc) { step(sc); });
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0);  // the repeated loads have landed
+    __builtin_amdgcn_s_barrier();
+    char* tile = (w == 0 ? b0 : (w == 1 ? b2 : (w == 2 ? b4 : b6))) - w * 64 * 128;
+    float wsv[4][4];
+    if constexpr (OUT != PFR_SP24_OUT_I32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v4f v = *reinterpret_cast<const v4f*>(scl + (w * 4 + i) * 16 + 4 * kb);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wsv[i][r] = v[r];
+        }
+    }
+    sp24_i8_epilogue<OUT>(acc, tile, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
                           xs_dev, zp_dev, row_sum);
 }
 
@@ -965,6 +1211,18 @@ __global__ __launch_bounds__(256) void k_sp24_pack_bf16(const uint16_t* __restri
 
 // Row sums of an int8 weight (the zero-point correction), one workgroup per
 // row.
+// idx4[((g * nkt + s) * 64 + l) * 4 + r] = idx[((4g + r) * nkt + s) * 64 + l]
+__global__ __launch_bounds__(256) void k_sp24_idx4(const uint32_t* __restrict__ idx, int64_t ngrp, int64_t nkt,
+                                                   v4i* __restrict__ idx4) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (g, s, l)
+    if (e >= ngrp * nkt * 64) return;
+    const int64_t g = e / (nkt * 64), sl = e % (nkt * 64);
+    v4i v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = (int)idx[(4 * g + r) * nkt * 64 + sl];
+    idx4[e] = v;
+}
+
 __global__ __launch_bounds__(256) void k_sp24_row_sum(const int8_t* __restrict__ W, int64_t K,
                                                       int32_t* __restrict__ rs) {
     __shared__ int part[4];
@@ -1123,9 +1381,17 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     hipLaunchKernelGGL((k_sp24_i8<OUTK, XR>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, B, ldb,    \
                        (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
+#define PFR_SP24_LAUNCH_R(OUTK)                                                                                \
+    hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx4, B, ldb,       \
+                       (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
+                       x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
+    // the register-streamed kernel for the X-row form when its eight-step
+    // ring divides the steps
+    const bool rring = xrow && nkt == 32;
 #define PFR_SP24_LAUNCH(OUTK)                      \
     do {                                           \
-        if (xrow) PFR_SP24_LAUNCH_X(OUTK, true);   \
+        if (rring) PFR_SP24_LAUNCH_R(OUTK);        \
+        else if (xrow) PFR_SP24_LAUNCH_X(OUTK, true);   \
         else PFR_SP24_LAUNCH_X(OUTK, false);       \
     } while (0)
     switch (out_kind) {
@@ -1134,6 +1400,7 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
         default: PFR_SP24_LAUNCH(PFR_SP24_OUT_I8);
     }
 #undef PFR_SP24_LAUNCH
+#undef PFR_SP24_LAUNCH_R
 #undef PFR_SP24_LAUNCH_X
     PFR_HIP(hipGetLastError());
 }
@@ -1263,6 +1530,14 @@ int sp24_pack_any(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype d
         try {
             PFR_HIP(hipMalloc(&w->w_scale, sizeof(float) * (size_t)(M > 0 ? M : 1)));
             if (M) PFR_HIP(hipMemcpy(w->w_scale, scales.data(), sizeof(float) * (size_t)M, hipMemcpyHostToDevice));
+            if (dtype == PFR_I8) {
+                const int64_t ngrp = w->Mp / 64, nkt = w->Kp / 128, n = ngrp * nkt * 64;
+                PFR_HIP(hipMalloc(&w->idx4, (size_t)n * 16));
+                hipLaunchKernelGGL(k_sp24_idx4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, w->idx,
+                                   ngrp, nkt, reinterpret_cast<v4i*>(w->idx4));
+                PFR_HIP(hipGetLastError());
+                PFR_HIP(hipStreamSynchronize(ctx->stream));
+            }
         } catch (...) {
             free_sp24(w);
             throw;

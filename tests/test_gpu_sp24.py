@@ -61,6 +61,30 @@ def test_i8_accumulators_exact(ctx, M, K, N):
     assert np.array_equal(Y, O.orc_int8_matmul_acc(q, X))
 
 
+def test_i8_register_streamed_forms(ctx):
+    """K = 4096 with N a multiple of 128 and a row-major X runs the kernel
+    that streams the weight into registers (32 k steps): ragged M, every
+    output form (int32 accumulators, float, requantised int8 with a zero
+    point) and a uint8 activation with a zero point, against the oracle and
+    exact int64 products."""
+    rng = np.random.default_rng(21)
+    M, K, N = 700, 4096, 256
+    q, s = rand_24_int8(rng, M, K, zero_frac=0.1)
+    X = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    say(f"sp24 i8 register-streamed M={M} K={K} N={N}")
+    W = ctx.sp24_pack(q, s)
+    assert np.array_equal(W.gemm_i8(X, out="i32"), O.orc_int8_matmul_acc(q, X))
+    F = W.gemm_i8(X, x_scale=0.05, out="f32")
+    R = O.orc_quantized_matmul_rowscale(q, X, s, 0.05)
+    assert np.array_equal(F.view(np.uint32), R.view(np.uint32))
+    os_, oz = O.orc_dynamic_params(R)
+    Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=float(os_), out_zp=int(oz))
+    assert np.array_equal(Q, O.orc_quantize(R, [os_], [oz], O.I8))
+    Xu = rng.integers(0, 256, (K, N)).astype(np.uint8)
+    Yu = W.gemm_q(Xu, 1.0, 131, out="i32")
+    assert np.array_equal(Yu.astype(np.int64), q.astype(np.int64) @ (Xu.astype(np.int64) - 131))
+
+
 def test_i8_rowscale_float_and_requant(ctx):
     rng = np.random.default_rng(11)
     M, K, N = 96, 512, 80
