@@ -41,10 +41,11 @@ struct pfr_sp24 {
     float* w_scale = nullptr; // [M] (per-tensor scales expanded)
     float w_scale_max = 0.0f; // the largest of them
     int32_t* row_sum = nullptr;  // int8: [Mp] sum over k of W[m, k] (the zero-point correction)
-    // int8: idx regrouped by four row blocks, [Mp/64][Kp/128][64][4]: element
-    // r of lane l is idx[(4g + r)][step][l], so a wave owning row blocks 4g ..
-    // 4g + 3 loads a step's positions with one 16-byte load per lane
-    uint32_t* idx4 = nullptr;
+    // int8: idx regrouped by kRB row blocks, [ceil(Mp/16/kRB)][Kp/128][64][4]:
+    // element r < kRB of lane l is idx[kRB g + r][step][l] (other elements
+    // and row blocks past Mp/16 are 0), so a wave owning row blocks kRB g ..
+    // kRB g + kRB - 1 loads a step's positions with one load per lane
+    uint32_t* idxw = nullptr;
 };
 
 namespace {
@@ -55,7 +56,7 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 void free_sp24(pfr_sp24* w) {
     if (!w) return;
-    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale, (void*)w->row_sum, (void*)w->idx4})
+    for (void* p : {w->a, (void*)w->idx, (void*)w->w_scale, (void*)w->row_sum, (void*)w->idxw})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -265,17 +266,18 @@ __device__ __forceinline__ void sp24_i8_row_scales(float (&wsv)[4][4], const flo
 }
 
 // The epilogue of the int8 2:4 GEMM: wave w of the workgroup holds the
-// accumulators of tile rows 64w .. 64w + 63 (row blocks 4w + i) x columns
-// 16j + c; tile + 128 ml (ml in 64w .. 64w + 63) is LDS no longer in use,
-// which only wave w touches: each wave requantises its rows there and
-// stores them itself, so the waves need no barrier between the two.  The
+// accumulators of the RB row blocks RB w + i of the tile (rows 16 RB w ..
+// 16 RB w + 16 RB - 1) x columns 16j + c; tile + 128 ml (ml in those rows)
+// is LDS no longer in use, which only wave w touches: each wave requantises
+// its rows there and stores them itself, so the waves need no barrier
+// between the two.  The
 // 16-byte chunk j of row ml sits at chunk j ^ ((ml >> 2) & 3): a byte write
 // covers rows 4kb + r of a row block (kb = 0..3), whose 128-byte rows would
 // otherwise all start in the same bank, and the 16-byte reads of two
 // neighbouring rows stay on distinct banks.
-template <int OUT>
+template <int OUT, int RB>
 __device__ __forceinline__ void sp24_i8_epilogue(
-    const v4i (&acc)[4][8], char* tile, int64_t mb0, int64_t n0, int M, int N, const float (&wsv)[4][4],
+    const v4i (&acc)[RB][8], char* tile, int64_t mb0, int64_t n0, int M, int N, const float (&wsv)[RB][4],
     float xs, float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec,
     int32_t x_zp, int32_t zp_shift, const float* __restrict__ xs_dev, const uint8_t* __restrict__ zp_dev,
     const int32_t* __restrict__ row_sum) {
@@ -284,31 +286,32 @@ __device__ __forceinline__ void sp24_i8_epilogue(
     const float xs_eff = xs_dev ? *xs_dev : xs;
     const int32_t zpv = zp_dev ? (int32_t)*zp_dev : x_zp;
     const uint32_t zcorr = (uint32_t)(zpv - zp_shift);
-    // the row sums of this lane's 16 rows, for a zero-point correction
+    // the row sums of this lane's 4 RB rows, for a zero-point correction
     // (loaded together, from clamped rows)
-    uint32_t rsv[4][4];
+    uint32_t rsv[RB][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int m = min((int)(mb0 + w * 4 + i) * 16 + 4 * kb + r, M - 1);
+            const int m = min((int)(mb0 + w * RB + i) * 16 + 4 * kb + r, M - 1);
             rsv[i][r] = zcorr ? (uint32_t)row_sum[m] : 0u;
         }
     // the exact accumulator of a row (int32 wrap-around arithmetic; the true
     // value is within int32 for K < 2^17)
     auto exact = [&](int32_t a, uint32_t rs) { return (int32_t)((uint32_t)a - zcorr * rs); };
     if constexpr (OUT == PFR_SP24_OUT_I8) {
-        // requantise into the LDS tile [256][128], then store 16-byte row pieces
+        // requantise into the LDS tile (128-byte rows), then store 16-byte row
+        // pieces
         // ZERO: no zero-point correction and output zero point 0 (the usual
         // symmetric case; the terms it drops are exact identities), chosen
         // once per workgroup so the per-output work shrinks
         auto requant = [&](auto zero, auto inr) {
             constexpr bool ZERO = decltype(zero)::value, INRANGE = decltype(inr)::value;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < RB; ++i) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int ml = (w * 4 + i) * 16 + 4 * kb + r;
+                    const int ml = (w * RB + i) * 16 + 4 * kb + r;
                     const int m = (int)(mb0 * 16) + ml;
                     const float sab = m < M ? wsv[i][r] * xs_eff : 0.0f;  // a_scale * b_scale (quant_ops.cpp:435)
 #pragma unroll
@@ -333,17 +336,17 @@ __device__ __forceinline__ void sp24_i8_epilogue(
             requant(std::false_type{}, std::false_type{});
         }
         __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
-        // the wave's 64 rows x 8 pieces, 8 per lane: all read from LDS first,
-        // then stored
-        v4i piece[8];
+        // the wave's 16 RB rows x 8 pieces, 2 RB per lane: all read from LDS
+        // first, then stored
+        v4i piece[2 * RB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int q16 = l + 64 * i, ml = 64 * w + (q16 >> 3), cc = q16 & 7;
+        for (int i = 0; i < 2 * RB; ++i) {
+            const int q16 = l + 64 * i, ml = 16 * RB * w + (q16 >> 3), cc = q16 & 7;
             piece[i] = *reinterpret_cast<const v4i*>(tile + ml * 128 + 16 * (cc ^ ((ml >> 2) & 3)));
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int q16 = l + 64 * i, ml = 64 * w + (q16 >> 3), cc = q16 & 7;
+        for (int i = 0; i < 2 * RB; ++i) {
+            const int q16 = l + 64 * i, ml = 16 * RB * w + (q16 >> 3), cc = q16 & 7;
             const int64_t m = mb0 * 16 + ml, n = n0 + 16 * cc;
             if (m >= M) continue;
             int8_t* yr = static_cast<int8_t*>(Y) + m * ldy;
@@ -357,10 +360,10 @@ __device__ __forceinline__ void sp24_i8_epilogue(
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < RB; ++i) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = (int)(mb0 + w * 4 + i) * 16 + 4 * kb + r;
+                const int m = (int)(mb0 + w * RB + i) * 16 + 4 * kb + r;
                 if (m >= M) continue;
                 float sab = 1.0f;
                 if constexpr (OUT == PFR_SP24_OUT_F32) sab = wsv[i][r] * xs_eff;
@@ -558,44 +561,47 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
     __builtin_amdgcn_s_barrier();
     float wsv[4][4];
     if constexpr (OUT != PFR_SP24_OUT_I32) sp24_i8_row_scales(wsv, ws, mb0, M);
-    sp24_i8_epilogue<OUT>(acc, st0, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
+    sp24_i8_epilogue<OUT, 4>(acc, st0, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
                           xs_dev, zp_dev, row_sum);
 }
 
-// int8 2:4 GEMM with the weight streamed into registers: the tile, waves
-// and MFMA order of k_sp24_i8 (256 x 128 outputs, wave w owning rows 64w ..
-// 64w + 63 and all 128 columns), but each wave loads its own four row
-// blocks' packed values and positions straight from global memory into a
-// ring of eight register slots (one per k step, 20 VGPRs each; the packed
-// order is the MFMA's lane order, so one 16-byte load per row block and
-// step, and one for the four blocks' positions from the regrouped idx4),
-// and only X goes through LDS, in eight 16 KiB stages filled by
-// direct-to-LDS loads.  Against k_sp24_i8 this takes the weight's 20 KiB per
-// step out of LDS (written once, read once: 40 KiB of the 120 KiB of LDS
-// traffic per step) and keeps seven steps of loads in flight per wave
-// instead of three, which the weight, streamed from HBM, needs to cover its
-// latency: nine loads per step, so seven steps are the 63 vector-memory
-// instructions a wave can have outstanding.
-// Per step s (slot and stage u = s % 8) each wave runs the 32 MFMAs of
+// int8 2:4 GEMM with the weight streamed into registers.  Tiles of 64 RB
+// x 128 outputs, four waves (one per SIMD), wave w owning RB row blocks
+// (rows 16 RB w .. 16 RB w + 16 RB - 1) and all 128 columns, with
+// k_sp24_i8's MFMA order; each wave loads its own row blocks' packed values
+// and positions straight from global memory into a ring of eight register
+// slots (one per k step; the packed order is the MFMA's lane order, so one
+// 16-byte load per row block and step, and one for the row blocks'
+// positions from the regrouped idxw), and only X goes through LDS, in eight
+// 16 KiB stages filled by direct-to-LDS loads.  Against k_sp24_i8 this
+// takes the weight out of LDS (40 KiB of writes and reads per step at RB =
+// 4) and keeps seven steps of loads in flight per wave instead of three,
+// which the weight, streamed from HBM, needs to cover its latency: RB + 5
+// loads per step, so seven steps stay within the 63 vector-memory
+// instructions a wave can have outstanding.  RB = 4 (256-row tiles) is
+// used: RB = 3 (192-row tiles, 232 tiles for 11008 x 512 instead of 172,
+// 31 KiB loaded per CU and step instead of 36) measured slower, 29.4
+// against 28.2 us, as every tile also streams all of X.
+// Per step s (slot and stage u = s % 8) each wave runs the 8 RB MFMAs of
 // column blocks j = 0..7, reading the B fragment of column block j + 3
 // (the next step's blocks 0..2 for j >= 5) from LDS while block j's MFMAs
 // run, in a ring of four fragment registers.  Before reading the next
 // step's first block it waits for its own loads of step s + 1 (vmcnt: the
-// loads of steps s + 2 .. s + 6, 12 per step, may still be in flight) and
-// for its LDS reads, and meets the other waves at the barrier: stage s + 1
-// is then complete, and every wave has read all of stage s, so the loads of
-// step s + 7 can go to stage (s + 7) % 8 and register slot (s + 7) % 8 (the
-// previous step's).  Steps past the end load the last step again, into
-// slots nothing reads, so the count of loads per step, and every wait,
-// stays fixed.  X is the row-major activation (XROW form of k_sp24_i8);
-// nkt is a multiple of 8.  The eight stages are separate arrays so the
-// compiler's wait counting sees that a stage load never writes the stages
-// being read.
-constexpr int kRSlots = 8, kRLead = 7, kRLoads = 9, kRStage = 128 * 128;
+// loads of the steps issued after it may still be in flight) and for its
+// LDS reads, and meets the other waves at the barrier: stage s + 1 is then
+// complete, and every wave has read all of stage s, so the loads of step s
+// + 7 can go to stage (s + 7) % 8 and register slot (s + 7) % 8 (the
+// previous step's).  X is the row-major activation (XROW form of
+// k_sp24_i8).  The NKT steps are fully unrolled, so every wait count is a
+// compile-time constant (as a loop the compiler's wait counting loses track
+// of the ring at the back edge and drains all loads there).  The eight
+// stages are separate arrays so the compiler's wait counting sees that a
+// stage load never writes the stages being read.
+constexpr int kRSlots = 8, kRLead = 7, kRStage = 128 * 128, kRB = 4;
 // the last step issued before step s's loads (sr_last(0): the prologue's)
 constexpr int sr_last(int s) { return s + kRLead - 1; }
 
-template <int OUT, int NKT>
+template <int OUT, int NKT, int RB>
 __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     int nkt_arg, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
     const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
@@ -610,8 +616,9 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     __shared__ __attribute__((aligned(1024))) char b5[kRStage];
     __shared__ __attribute__((aligned(1024))) char b6[kRStage];
     __shared__ __attribute__((aligned(1024))) char b7[kRStage];
-    __shared__ __attribute__((aligned(16))) float scl[kI8TileM];  // the tile's row scales
-    constexpr int nkt = NKT;
+    __shared__ __attribute__((aligned(16))) float scl[kI8TileM];  // the tile's row scales (and the next rows)
+    constexpr int nkt = NKT, kRLoads = RB + 5;
+    static_assert(RB >= 1 && RB <= 4 && kRLoads * kRLead <= 63, "loads in flight exceed the wave's counter");
     (void)nkt_arg;
     const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const int kb = l >> 4, c = l & 15;
@@ -623,7 +630,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
         mt = T / ntn;
         nt = T % ntn;
     }
-    const int64_t mb0 = (int64_t)mt * (kI8TileM / 16);
+    const int64_t mb0 = (int64_t)mt * (4 * RB);  // the tile's first row block
     const int64_t n0 = (int64_t)nt * kI8TileN;
     auto stage = [&](auto uc) -> char* {
         constexpr int u = decltype(uc)::value;
@@ -636,35 +643,44 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
         else if constexpr (u == 6) return b6;
         else return b7;
     };
-    // this wave's row blocks mb0 + 4w + i: element (row block, step) at
-    // (rb * nkt + step) * 64 + lane
-    const v4i* abase = A + (mb0 + 4 * w) * nkt * 64 + l;
-    const v4i* ibase = reinterpret_cast<const v4i*>(I) + (mb0 / 4 + w) * nkt * 64 + l;
-    const int64_t rbs = (int64_t)nkt * 64;
+    // Every load address is a wave-uniform base (scalar registers) plus a
+    // per-lane offset fixed for the whole kernel, so the loads take the
+    // scalar-base form and the loop needs no per-load address arithmetic.
+    // This wave's row blocks mb0 + RB w + i: element (row block, step) at
+    // (rb * nkt + step) * 64 + lane; their positions are group mb0 / RB + w
+    // of idxw.
+    // (the positions are loaded as exactly RB dwords of the lane's 16 bytes:
+    // a dead fourth register of a pending load would be handed to other
+    // values, and writing it makes the compiler drain every load first)
+    typedef int vrb __attribute__((ext_vector_type(RB)));
+    const v4i* aw = A + (mb0 + RB * w) * nkt * 64;
+    const v4i* iw = reinterpret_cast<const v4i*>(I) + (mb0 / RB + w) * nkt * 64;
     // B: the step's 128 X rows, row n = 8 (w + 4i) + l / 8 loaded by this
-    // lane (16-byte chunk (l % 8) ^ xrow_swizzle(n) of the tile's 128 columns)
-    const v4i* bsrc[4];
+    // lane (16-byte chunk (l % 8) ^ xrow_swizzle(n) of the tile's 128
+    // columns): base bw + 128 ldb per step, lane offset boff[i]
+    const int8_t* bw = B + n0 + (int64_t)8 * w * ldb;
+    int boff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int n = 8 * (w + 4 * i) + (l >> 3);
         const int chunk = (l & 7) ^ xrow_swizzle(n);
-        bsrc[i] = reinterpret_cast<const v4i*>(B + (int64_t)n * ldb + n0 + 16 * chunk);
+        boff[i] = (int)((int64_t)(32 * i + (l >> 3)) * ldb) + 16 * chunk;
     }
-    const int64_t b_step = 128 * ldb / 16;  // v4i per k step
-    v4i ar[kRSlots][4];
-    v4i ir[kRSlots];
+    v4i ar[kRSlots][RB];
+    vrb ir[kRSlots];
     // the nine loads of step TS (a compile-time step, below nkt) into slot
     // and stage TS % 8
     auto issue = [&](auto tc) {
         constexpr int ts = decltype(tc)::value, u = ts % kRSlots;
         char* st = stage(std::integral_constant<int, u>{});
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ar[u][i] = abase[i * rbs + ts * 64];
-        ir[u] = ibase[ts * 64];
+        for (int i = 0; i < RB; ++i) ar[u][i] = aw[(i * nkt + ts) * 64 + l];
+        ir[u] = *reinterpret_cast<const vrb*>(iw + ts * 64 + l);
+        const int8_t* bs = bw + (int64_t)ts * 128 * ldb;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(bsrc[i] + (int64_t)ts * b_step, PFR_LDS(st + 8 * (w + 4 * i) * 128), 16,
-                                             0, 0);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const v4i*>(bs + boff[i]),
+                                             PFR_LDS(st + 8 * (w + 4 * i) * 128), 16, 0, 0);
     };
     // B fragment of column block j from a stage (see k_sp24_i8, XROW form)
     const int trk = (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
@@ -678,9 +694,9 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
                 (__attribute__((address_space(3))) v2i*)(bp + 1024 * (r & 1) + 8192 * (r >> 1)));
         f = v8i{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
     };
-    v4i acc[4][8];
+    v4i acc[RB][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     v8i bq[4];
@@ -728,11 +744,11 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
             constexpr int j = decltype(jc)::value;
             fetch_b(bq[(j + 3) % 4], cur, j + 3);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RB; ++i)
                 acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(ar[u][i], bq[j % 4], acc[i][j], ir[u][i], 0, 0);
         });
-        static_for<0, 20>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        static_for<0, 20>([&](auto gc) {
+            if constexpr (decltype(gc)::value < 5 * RB) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         });
         __builtin_amdgcn_sched_barrier(0);
@@ -744,12 +760,12 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
             constexpr int j = decltype(jc)::value;
             fetch_b(bq[(j + 3) % 4], nxt, j - 5);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RB; ++i)
                 acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(ar[u][i], bq[j % 4], acc[i][j], ir[u][i], 0, 0);
         });
         static_for<0, 12>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if constexpr (g < 3 * RB) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
             if constexpr (g < kRLoads * std::max(0, last - first + 1))
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (next loads)
@@ -759,17 +775,17 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);  // the repeated loads have landed
     __builtin_amdgcn_s_barrier();
-    char* tile = (w == 0 ? b0 : (w == 1 ? b2 : (w == 2 ? b4 : b6))) - w * 64 * 128;
-    float wsv[4][4];
+    char* tile = (w == 0 ? b0 : (w == 1 ? b2 : (w == 2 ? b4 : b6))) - w * 16 * RB * 128;
+    float wsv[RB][4];
     if constexpr (OUT != PFR_SP24_OUT_I32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v4f v = *reinterpret_cast<const v4f*>(scl + (w * 4 + i) * 16 + 4 * kb);
+        for (int i = 0; i < RB; ++i) {
+            const v4f v = *reinterpret_cast<const v4f*>(scl + (w * RB + i) * 16 + 4 * kb);
 #pragma unroll
             for (int r = 0; r < 4; ++r) wsv[i][r] = v[r];
         }
     }
-    sp24_i8_epilogue<OUT>(acc, tile, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
+    sp24_i8_epilogue<OUT, RB>(acc, tile, mb0, n0, M, N, wsv, xs, inv_out, out_zp, inrange, Y, ldy, yvec, x_zp, zp_shift,
                           xs_dev, zp_dev, row_sum);
 }
 
@@ -1211,16 +1227,18 @@ __global__ __launch_bounds__(256) void k_sp24_pack_bf16(const uint16_t* __restri
 
 // Row sums of an int8 weight (the zero-point correction), one workgroup per
 // row.
-// idx4[((g * nkt + s) * 64 + l) * 4 + r] = idx[((4g + r) * nkt + s) * 64 + l]
-__global__ __launch_bounds__(256) void k_sp24_idx4(const uint32_t* __restrict__ idx, int64_t ngrp, int64_t nkt,
-                                                   v4i* __restrict__ idx4) {
+// idxw[((g * nkt + s) * 64 + l) * 4 + r] = idx[((kRB g + r) * nkt + s) * 64 + l]
+// for r < kRB and row blocks below nrb, else 0
+__global__ __launch_bounds__(256) void k_sp24_idxw(const uint32_t* __restrict__ idx, int64_t nrb, int64_t ngrp,
+                                                   int64_t nkt, v4i* __restrict__ idxw) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (g, s, l)
     if (e >= ngrp * nkt * 64) return;
     const int64_t g = e / (nkt * 64), sl = e % (nkt * 64);
-    v4i v;
+    v4i v = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = (int)idx[(4 * g + r) * nkt * 64 + sl];
-    idx4[e] = v;
+    for (int r = 0; r < kRB; ++r)
+        if (kRB * g + r < nrb) v[r] = (int)idx[(kRB * g + r) * nkt * 64 + sl];
+    idxw[e] = v;
 }
 
 __global__ __launch_bounds__(256) void k_sp24_row_sum(const int8_t* __restrict__ W, int64_t K,
@@ -1381,13 +1399,15 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     hipLaunchKernelGGL((k_sp24_i8<OUTK, XR>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, B, ldb,    \
                        (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
+    const int64_t rtiles = (W->M + 64 * kRB - 1) / (64 * kRB);  // 192-row tiles
+    const dim3 rgrid((unsigned)(rtiles * ntn));
 #define PFR_SP24_LAUNCH_R(OUTK)                                                                                \
-    hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx4, B, ldb,       \
+    hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32, kRB>), rgrid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idxw, B, ldb, \
                        (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
-    // the register-streamed kernel for the X-row form when its eight-step
-    // ring divides the steps
-    const bool rring = xrow && nkt == 32;
+    // the register-streamed kernel for the X-row form at 32 k steps, when
+    // its 192-row tiles stay inside the packed rows
+    const bool rring = xrow && nkt == 32 && rtiles * 64 * kRB <= W->Mp;
 #define PFR_SP24_LAUNCH(OUTK)                      \
     do {                                           \
         if (rring) PFR_SP24_LAUNCH_R(OUTK);        \
@@ -1531,10 +1551,11 @@ int sp24_pack_any(pfr_ctx* ctx, int64_t M, int64_t K, const void* W, pfr_dtype d
             PFR_HIP(hipMalloc(&w->w_scale, sizeof(float) * (size_t)(M > 0 ? M : 1)));
             if (M) PFR_HIP(hipMemcpy(w->w_scale, scales.data(), sizeof(float) * (size_t)M, hipMemcpyHostToDevice));
             if (dtype == PFR_I8) {
-                const int64_t ngrp = w->Mp / 64, nkt = w->Kp / 128, n = ngrp * nkt * 64;
-                PFR_HIP(hipMalloc(&w->idx4, (size_t)n * 16));
-                hipLaunchKernelGGL(k_sp24_idx4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, w->idx,
-                                   ngrp, nkt, reinterpret_cast<v4i*>(w->idx4));
+                const int64_t nrb = w->Mp / 16, ngrp = (nrb + kRB - 1) / kRB, nkt = w->Kp / 128,
+                              n = ngrp * nkt * 64;
+                PFR_HIP(hipMalloc(&w->idxw, (size_t)n * 16));
+                hipLaunchKernelGGL(k_sp24_idxw, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, w->idx,
+                                   nrb, ngrp, nkt, reinterpret_cast<v4i*>(w->idxw));
                 PFR_HIP(hipGetLastError());
                 PFR_HIP(hipStreamSynchronize(ctx->stream));
             }
