@@ -585,13 +585,16 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
 // Per step s (slot and stage u = s % 8) each wave runs the 8 RB MFMAs of
 // column blocks j = 0..7, reading the B fragment of column block j + 3
 // (the next step's blocks 0..2 for j >= 5) from LDS while block j's MFMAs
-// run, in a ring of four fragment registers.  Before reading the next
-// step's first block it waits for its own loads of step s + 1 (vmcnt: the
-// loads of the steps issued after it may still be in flight) and for its
-// LDS reads, and meets the other waves at the barrier: stage s + 1 is then
-// complete, and every wave has read all of stage s, so the loads of step s
-// + 7 can go to stage (s + 7) % 8 and register slot (s + 7) % 8 (the
-// previous step's).  X is the row-major activation (XROW form of
+// run, in a ring of four fragment registers.  On even steps, before
+// reading the next step's first block, it waits for its own loads of steps
+// s + 1 and s + 2 (vmcnt: the loads of the steps issued after them may
+// still be in flight) and for its LDS reads, and meets the other waves at
+// the barrier: stages s + 1 and s + 2 are then complete, and every wave has
+// read all of stage s.  Every step then loads step s + 7 into stage and
+// register slot (s + 7) % 8, the previous step's: after an even step's
+// barrier that stage has been read by every wave, and an odd step reuses
+// the stage of the even step before it, read before that step's barrier.
+// (A barrier every step cost about a fifth of a streaming step.)  X is the row-major activation (XROW form of
 // k_sp24_i8).  The NKT steps are fully unrolled, so every wait count is a
 // compile-time constant (as a loop the compiler's wait counting loses track
 // of the ring at the back edge and drains all loads there).  The eight
@@ -736,7 +739,11 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     auto step = [&](auto sc) {
         constexpr int S = decltype(sc)::value, u = S % kRSlots, un = (u + 1) % kRSlots;
         constexpr int first = sr_last(S) + 1, last = std::min(sr_last(S + 1), nkt - 1);
-        constexpr int later = std::max(0, std::min(sr_last(S), nkt - 1) - S - 1);  // issued after step S + 1
+        // even steps wait for steps S + 1 and S + 2 (the loads issued after
+        // them may still be in flight) and meet at the barrier; odd steps
+        // read stage S + 1, already waited for, and load without a barrier
+        constexpr bool SYNC = S % 2 == 0;
+        constexpr int later = std::max(0, std::min(sr_last(S), nkt - 1) - S - 2);  // issued after step S + 2
         const char* cur = stage(std::integral_constant<int, u>{});
         const char* nxt = stage(std::integral_constant<int, un>{});
         __builtin_amdgcn_sched_barrier(0);
@@ -752,8 +759,10 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         });
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * later));
-        __builtin_amdgcn_s_barrier();
+        if constexpr (SYNC) {
+            __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * later));
+            __builtin_amdgcn_s_barrier();
+        }
         __builtin_amdgcn_sched_barrier(0);
         static_for<first, last + 1>([&](auto tc) { issue(tc); });
         static_for<5, 8>([&](auto jc) {
