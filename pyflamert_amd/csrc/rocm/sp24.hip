@@ -359,24 +359,53 @@ __device__ __forceinline__ void sp24_i8_epilogue(
             }
         }
     } else {
+        // 4-byte outputs, one row block at a time through the wave's first
+        // 8 KiB of LDS (16 rows x 512 B; the 64-byte chunk j of row 4kb + r
+        // at chunk j ^ kb, so a write's four rows hit four bank groups),
+        // then 16-byte row pieces from distinct registers: stored one element
+        // at a time from one register, each store waited for the one before
+        char* wt = tile + 2048 * RB * w;
+        const bool vec = yvec && (ldy % 4 == 0) && n0 + 128 <= N;
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = (int)(mb0 + w * RB + i) * 16 + 4 * kb + r;
-                if (m >= M) continue;
                 float sab = 1.0f;
-                if constexpr (OUT == PFR_SP24_OUT_F32) sab = wsv[i][r] * xs_eff;
+                if constexpr (OUT == PFR_SP24_OUT_F32) sab = m < M ? wsv[i][r] * xs_eff : 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const int64_t n = n0 + 16 * j + c;
-                    if (n >= N) continue;
                     const int32_t v = exact(acc[i][j][r], rsv[i][r]);
-                    const int64_t o = (int64_t)m * ldy + n;
-                    if constexpr (OUT == PFR_SP24_OUT_I32) static_cast<int32_t*>(Y)[o] = v;
-                    else static_cast<float*>(Y)[o] = (float)v * sab;
+                    uint32_t bits;
+                    if constexpr (OUT == PFR_SP24_OUT_I32) bits = (uint32_t)v;
+                    else bits = __float_as_uint((float)v * sab);
+                    *reinterpret_cast<uint32_t*>(wt + (4 * kb + r) * 512 + 64 * (j ^ kb) + 4 * c) = bits;
                 }
             }
+            __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));  // lgkmcnt(0) only
+            // 16 rows x 32 pieces of 16 B, 8 per lane
+            v4i piece[8];
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const int q16 = l + 64 * h, row = q16 >> 5, pc = q16 & 31;
+                piece[h] = *reinterpret_cast<const v4i*>(wt + row * 512 + 64 * ((pc >> 2) ^ (row >> 2)) + 16 * (pc & 3));
+            }
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const int q16 = l + 64 * h, row = q16 >> 5, pc = q16 & 31;
+                const int64_t m = (mb0 + w * RB + i) * 16 + row, n = n0 + 4 * pc;
+                if (m >= M) continue;
+                uint32_t* yr = static_cast<uint32_t*>(Y) + m * ldy;
+                if (vec) {
+                    *reinterpret_cast<v4i*>(yr + n) = piece[h];
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (n + b < N) yr[n + b] = (uint32_t)piece[h][b];
+                }
+            }
+            // this block's reads have completed before the next block's writes
+            __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (0x3 << 14));
         }
     }
 }
