@@ -85,6 +85,39 @@ def test_i8_register_streamed_forms(ctx):
     assert np.array_equal(Yu.astype(np.int64), q.astype(np.int64) @ (Xu.astype(np.int64) - 131))
 
 
+def test_i8_register_streamed_strided_outputs(ctx):
+    """The register-streamed kernel (K = 4096, N a multiple of 128) with an
+    output row stride that is not a multiple of 16 elements, so its
+    epilogues store element by element: int32, float and requantised int8
+    into the first N columns of wider rows, the padding left untouched."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    M, K, N, pad = 300, 4096, 128, 3
+    q, s = rand_24_int8(rng, M, K, zero_frac=0.1)
+    X = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    say(f"sp24 i8 register-streamed strided outputs M={M} N={N} ldy={N + pad}")
+    W = ctx.sp24_pack(q, s)
+    dX = torch.from_numpy(X).cuda()
+    acc = O.orc_int8_matmul_acc(q, X)
+    R = O.orc_quantized_matmul_rowscale(q, X, s, 0.05)
+    os_, oz = O.orc_dynamic_params(R)
+    want = {"i32": acc, "f32": R, "i8": O.orc_quantize(R, [os_], [oz], O.I8)}
+    for out, dt, fill in (("i32", torch.int32, 7), ("f32", torch.float32, 7.0), ("i8", torch.int8, 7)):
+        dY = torch.full((M, N + pad), fill, dtype=dt, device="cuda")
+        torch.cuda.synchronize()
+        W.gemm_i8_dev(dX.data_ptr(), N, dY.data_ptr(), x_scale=0.05, out=out, out_scale=float(os_),
+                      out_zp=int(oz), ldy=N + pad)
+        torch.cuda.synchronize()
+        Y = dY.cpu().numpy()
+        got, w = Y[:, :N], want[out]
+        if out == "f32":
+            assert np.array_equal(got.view(np.uint32), w.view(np.uint32)), out
+        else:
+            assert np.array_equal(got, w), out
+        assert (Y[:, N:] == fill).all(), out
+
+
 def test_i8_rowscale_float_and_requant(ctx):
     rng = np.random.default_rng(11)
     M, K, N = 96, 512, 80
