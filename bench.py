@@ -650,10 +650,44 @@ def bench_sp24(ctx, args):
         "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
         "shape": [M, K, N],
     }
+    if not args.no_cpu:
+        res["cpu_reference"] = cpu_sp24_reference(q, X)
     log(f"sp24 i8: {res}")
     for W, _, _ in sets:
         W.free()
     return res
+
+
+def cpu_sp24_reference(q, X, rows=256):
+    """The reference's quantization::quantized_matmul with int8 requant
+    (quant_ops.cpp:387-506; int64 accumulation over every k, the 2:4 zeros
+    included) compiled from its sources, one pinned thread, on the first
+    `rows` rows of the 2:4 weight (the reference takes one weight scale:
+    per tensor here, which costs the same) against the full X, median of 3
+    calls after one warm-up, scaled to all 11008 rows."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    if not O.have_ref():
+        return None
+    qs = np.ascontiguousarray(q[:rows])
+    with pinned_core() as pin:
+        O.ref_quantized_matmul(qs, X, 0.01, 0.05, out_params=(0.6, 0, O.I8))
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.ref_quantized_matmul(qs, X, 0.01, 0.05, out_params=(0.6, 0, O.I8))
+            ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    M_, K_ = q.shape
+    full_s = med * M_ / rows
+    return {"value": round(2.0 * M_ * K_ * X.shape[1] / full_s / 1e9, 3), "unit": "GOP/s dense-equivalent",
+            "ms_per_call_scaled": round(full_s * 1e3, 1), "cores": 1, "kind": "reference",
+            "pinned_core": pin.core, "host": host_cpu_info(),
+            "sample": f"quantization::quantized_matmul + int8 requant compiled from the reference sources on "
+                      f"a {rows}-row slice of the {M_}x{K_} weight x X {K_}x{X.shape[1]}, median of 3 calls "
+                      f"({med * 1e3:.0f} ms each) after one warm-up, scaled by {M_}/{rows}"}
 
 
 def host_cpu_info():
