@@ -389,7 +389,50 @@ def bench_masks(ctx, cpu):
     return res
 
 
-def bench_decode_int8(ctx):
+def cpu_decode_reference(data, shapes):
+    """The reference's sparse_matvec (batch 1) and sparse_matmul (batch 8)
+    (sparse_tensor.cpp:473-554) compiled from its sources, one pinned
+    thread, over one layer's seven linears on the dequantised fp32 CSR with
+    int64 indices (the reference's SparseTensor, built once per shape; the
+    calls alone are timed), median of 3 calls per shape after one warm-up,
+    scaled to the 32-layer step."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from pyflamert_amd import workloads
+
+    if not O.have_ref():
+        return None
+    mats = {}
+    for name, (M_, K_, _) in shapes.items():
+        ip, ix, q, sc = data[name]
+        mats[name] = (M_, K_, np.asarray(ip, np.int64), np.asarray(ix, np.int64), workloads.dequant_rows(ip, q, sc))
+    out = {}
+    rng = np.random.default_rng(0)
+    with pinned_core() as pin:
+        for B in (1, 8):
+            xs = {name: rng.standard_normal((K_, B) if B > 1 else K_).astype(np.float32)
+                  for name, (M_, K_, _) in shapes.items()}
+
+            layer_s = 0.0
+            for name, (M_, K_, count) in shapes.items():
+                m_, k_, ip, ix, v = mats[name]
+                if B == 1:
+                    ts, _ = O.ref_time_sparse_matvec(m_, k_, ip, ix, v, xs[name], 3)
+                else:
+                    ts, _ = O.ref_time_sparse_matmul(m_, k_, ip, ix, v, xs[name], 3)
+                layer_s += count * float(np.median(ts))
+            step_s = layer_s * 32
+            out[f"batch{B}"] = {"step_ms": round(step_s * 1e3, 1), "tokens_per_s": round(B / step_s, 3)}
+    out.update({"cores": 1, "kind": "reference", "pinned_core": pin.core,
+                "sample": "pruning::sparse_matvec (batch 1) / sparse_matmul (batch 8) compiled from the reference "
+                          "sources on one layer (q, k, v, o, gate, up, down; dequantised fp32 CSR, int64 indices, "
+                          "the SparseTensor built once per shape), median of 3 calls per shape after a warm-up, "
+                          "scaled by 32 layers"})
+    return out
+
+
+def bench_decode_int8(ctx, cpu=True):
     """Llama-2-7B-shaped decode linear stack: 32 layers x (4 x 4096x4096,
     2 x 11008x4096, 4096x11008), 70 % sparsity with lognormal (sigma 0.5) row
     lengths, int8 weight-only with per-row scales (dequantisation fused),
@@ -435,6 +478,8 @@ def bench_decode_int8(ctx):
             seq.append((tag, K_, ctx.csr_upload(M_ * count, K_, ip, ix, q, row_scales=sc)))
         stacked.append(seq)
     res = {}
+    if cpu:
+        res["cpu_reference"] = cpu_decode_reference(data, shapes)
     for B, mode in ((1, "fast"), (8, "fast"), (1, "strict"), (8, "strict")):
         bufs = {name: (torch.randn((K_, B), dtype=torch.float32, device="cuda"),
                        torch.empty((M_, B), dtype=torch.float32, device="cuda"))
@@ -851,7 +896,7 @@ def main():
         extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
         extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
         extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)
-        extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx)
+        extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx, not args.no_cpu)
         extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
         extra["dynamic_int8_node_11008x4096x512"] = bench_dynamic_int8(ctx)
         extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)

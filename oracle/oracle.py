@@ -91,6 +91,7 @@ def ref_lib():
             "ref_to_sparse_csr": (_INT, [_P, _I64, _I64, _F, _P, _P, _P, _P]),
             "ref_sparse_matmul": (_INT, [_I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P]),
             "ref_time_sparse_matmul": (_INT, [_I64, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P, _P]),
+            "ref_time_sparse_matvec": (_INT, [_I64, _I64, _P, _P, _P, _I64, _P, _INT, _P, _P]),
             "ref_sparse_matvec": (_INT, [_I64, _I64, _P, _P, _P, _I64, _P, _P]),
             "ref_apply_mask": (_INT, [_P, _P, _I64, _P]),
             "ref_magnitude_mask": (_INT, [_P, _I64, _I64, _F, _P]),
@@ -461,6 +462,17 @@ def ref_time_sparse_matmul(m, k, indptr, indices, values, b, reps):
     _ref_check(ref_lib().ref_time_sparse_matmul(m, k, n, _ptr(_c(indptr, np.int64)), _ptr(_c(indices, np.int64)),
                                                 _ptr(_c(values, np.float32)), len(values), _ptr(b), reps,
                                                 _ptr(ns), _ptr(out)))
+    return ns.astype(np.float64) * 1e-9, out
+
+
+def ref_time_sparse_matvec(m, k, indptr, indices, values, x, reps):
+    """Per-call seconds of the reference sparse_matvec (after one warm-up),
+    and its output."""
+    ns = np.zeros(reps, np.int64)
+    out = np.empty(m, np.float32)
+    _ref_check(ref_lib().ref_time_sparse_matvec(m, k, _ptr(_c(indptr, np.int64)), _ptr(_c(indices, np.int64)),
+                                                _ptr(_c(values, np.float32)), len(values), _ptr(_c(x, np.float32)),
+                                                reps, _ptr(ns), _ptr(out)))
     return ns.astype(np.float64) * 1e-9, out
 
 

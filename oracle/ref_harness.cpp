@@ -144,6 +144,26 @@ int ref_time_sparse_matmul(int64_t m, int64_t k, int64_t n, const int64_t* indpt
     });
 }
 
+// The same for the reference's sparse_matvec (x of k floats).
+int ref_time_sparse_matvec(int64_t m, int64_t k, const int64_t* indptr, const int64_t* indices,
+                           const float* values, int64_t nnz, const float* x, int reps, int64_t* ns,
+                           float* out) {
+    return guard([&] {
+        std::vector<int64_t> ip(indptr, indptr + m + 1), ix(indices, indices + nnz);
+        std::vector<float> vv(values, values + nnz);
+        pr::SparseTensor s = pr::SparseTensor::from_csr({m, k}, ip, ix, vv);
+        Tensor xt = make_f32(x, {k});
+        Tensor r = pr::sparse_matvec(s, xt);
+        for (int i = 0; i < reps; ++i) {
+            auto t0 = std::chrono::steady_clock::now();
+            r = pr::sparse_matvec(s, xt);
+            auto t1 = std::chrono::steady_clock::now();
+            ns[i] = std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        }
+        std::memcpy(out, r.data(), r.size_bytes());
+    });
+}
+
 int ref_sparse_matvec(int64_t m, int64_t k, const int64_t* indptr,
                       const int64_t* indices, const float* values, int64_t nnz,
                       const float* x, float* out) {
