@@ -157,7 +157,33 @@ def bench_mlp_session(cpu):
     return res
 
 
-def bench_bert_linears(ctx):
+def cpu_bert_linears_reference(csrs, T):
+    """The reference's sparse_matmul (sparse_tensor.cpp:473-519) compiled from
+    its sources, one pinned thread, for one layer's six linears (W [out, in]
+    CSR with int64 indices times the activation transposed, in x T), median
+    of 3 calls per shape after one warm-up, scaled to 12 layers."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    if not O.have_ref():
+        return None
+    rng = np.random.default_rng(0)
+    layer_s = 0.0
+    with pinned_core() as pin:
+        for (out_f, in_f, count), (ip, ix, v) in csrs:
+            xt = rng.standard_normal((in_f, T)).astype(np.float32)
+            ts, _ = O.ref_time_sparse_matmul(out_f, in_f, ip, ix, v, xt, 3)
+            layer_s += count * float(np.median(ts))
+    fwd = 12 * layer_s
+    return {"per_forward_ms": round(fwd * 1e3, 1), "tokens_per_s": round(T / fwd, 1), "cores": 1,
+            "kind": "reference", "pinned_core": pin.core,
+            "sample": f"pruning::sparse_matmul compiled from the reference sources on one layer's six linears "
+                      f"(CSR with int64 indices x activation^T {T} columns), median of 3 calls per shape after "
+                      f"a warm-up, scaled by 12 layers"}
+
+
+def bench_bert_linears(ctx, cpu=True):
     """BERT-base-shaped encoder's pruned linears: 12 layers x (4 x 768x768,
     768x3072, 3072x768), 80 % uniform-random sparsity, 1024 tokens (batch 8 x
     seq 128), Gemm form with bias (the rocm::Gemm kernel), strict.  Dense
@@ -170,9 +196,10 @@ def bench_bert_linears(ctx):
 
     T = 1024
     shapes = {"qkvo_768x768": (768, 768, 4), "ffn_up_3072x768": (3072, 768, 1), "ffn_down_768x3072": (768, 3072, 1)}
-    res, layer_ms, nnz_layer = {}, 0.0, 0
+    res, layer_ms, nnz_layer, csrs = {}, 0.0, 0, []
     for name, (out_f, in_f, count) in shapes.items():
         ip, ix, v = workloads.csr_uniform(out_f, in_f, 0.2, 0.02, seed=out_f * 7 + in_f)
+        csrs.append(((out_f, in_f, count), (ip, ix, v)))
         Ws = [ctx.csr_upload(out_f, in_f, ip, ix, v) for _ in range(4)]
         A = torch.randn((T, in_f), dtype=torch.float32, device="cuda")
         bias = torch.randn((out_f,), dtype=torch.float32, device="cuda")
@@ -200,6 +227,8 @@ def bench_bert_linears(ctx):
     res["per_forward_ms"] = round(12 * layer_ms, 4)
     res["tokens_per_s"] = round(T / (12 * layer_ms * 1e-3), 1)
     res["gflops"] = round(2.0 * 12 * nnz_layer * T / (12 * layer_ms * 1e-3) / 1e9, 1)
+    if cpu:
+        res["cpu_reference"] = cpu_bert_linears_reference(csrs, T)
     log(f"BERT linears: {res}")
     return res
 
@@ -894,7 +923,7 @@ def main():
         extra["sp24_i8"] = bench_sp24(ctx, args)
         extra["sp24_bf16"] = bench_sp24_bf16(ctx, args)
         extra["mlp_784_512_10_session"] = bench_mlp_session(not args.no_cpu)
-        extra["bert_base_linears_80pct"] = bench_bert_linears(ctx)
+        extra["bert_base_linears_80pct"] = bench_bert_linears(ctx, not args.no_cpu)
         extra["bert_base_ffn_block_80pct"] = bench_bert_ffn_block(ctx)
         extra["llama7b_decode_int8_70pct"] = bench_decode_int8(ctx, not args.no_cpu)
         extra["masks_11008x4096"] = bench_masks(ctx, not args.no_cpu)
