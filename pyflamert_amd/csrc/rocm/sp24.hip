@@ -1444,8 +1444,9 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
                        (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
     // the register-streamed kernel for the X-row form at 32 k steps, when
-    // its 192-row tiles stay inside the packed rows
-    const bool rring = xrow && nkt == 32 && rtiles * 64 * kRB <= W->Mp;
+    // its tiles stay inside the packed rows and its per-lane B offsets (up to
+    // 128 rows of X) fit in 32 bits
+    const bool rring = xrow && nkt == 32 && rtiles * 64 * kRB <= W->Mp && ldb * 128 < INT32_MAX;
 #define PFR_SP24_LAUNCH(OUTK)                      \
     do {                                           \
         if (rring) PFR_SP24_LAUNCH_R(OUTK);        \
