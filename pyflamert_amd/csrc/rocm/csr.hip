@@ -7,6 +7,7 @@
 #include <cstring>
 #include <memory>
 #include <numeric>
+#include <set>
 #include <vector>
 
 #include "common.hpp"
@@ -81,6 +82,73 @@ void sell_order(const std::vector<int32_t>& cnt, int64_t nch, int32_t* b, int64_
     sell_order(cnt, nch, b + h, n - h, depth + 1);
 }
 
+// Slab placement of the sliced-ELL copy.  Slab positions 16g .. 16g + 15 are
+// one workgroup of the 16-wave column-slice launch (wave i on SIMD i % 4, four
+// waves per SIMD), all workgroups of a slice run at once (one per CU), and
+// the waves meet at a barrier after each chunk: a workgroup takes about the
+// sum over chunks of its busiest SIMD's steps, and the launch its slowest
+// workgroup.  The k-d order puts slabs with long runs next to each other, so
+// the first workgroup got the longest ones (on the 4096 x 4096, 10 % weight:
+// 2008 steps against a mean of 1831).  The placement deals them out: slabs,
+// longest total first, go greedily into bins of four (one SIMD's waves), each
+// to the bin among the 64 least loaded whose largest per-chunk load stays
+// smallest; bins, heaviest first, are dealt out to workgroups in snake
+// order; wave i of workgroup g gets slab i / 4 of its group's bin i % 4
+// (1808 steps on that weight; the 8-wave launch's slowest workgroup goes from
+// 1024 to 968 steps, the 4-wave launch's is unchanged).  Measured on that
+// weight at N = 256, the launch went from 40.0-40.2 to 38.6-39.4 us: less
+// than the step counts promise, so the imbalance was a small part of what
+// the launch spends beyond its vector-ALU issue.  The slabs that do not fill
+// a whole group of 16 are the lightest and go last, in k-d order.
+// steps: [nslab * nch] padded steps of slab s in chunk c; returns the slab
+// at each position.
+std::vector<int64_t> sell_place(const std::vector<int64_t>& steps, int64_t nslab, int64_t nch) {
+    std::vector<int64_t> pos((size_t)nslab);
+    std::iota(pos.begin(), pos.end(), 0);
+    if (nslab < 32 || nslab > 65536) return pos;  // one workgroup, or too many to place
+    std::vector<int64_t> tot((size_t)nslab, 0);
+    for (int64_t s = 0; s < nslab; ++s)
+        for (int64_t c = 0; c < nch; ++c) tot[(size_t)s] += steps[(size_t)(s * nch + c)];
+    std::vector<int64_t> by_len(pos);
+    std::stable_sort(by_len.begin(), by_len.end(), [&](int64_t a, int64_t b) { return tot[(size_t)a] > tot[(size_t)b]; });
+    const int64_t nfull = nslab / 16 * 16, nb = nfull / 4, ng = nfull / 16;
+    std::vector<int64_t> load((size_t)(nb * nch), 0), btot((size_t)nb, 0);
+    std::vector<std::vector<int64_t>> bins((size_t)nb);
+    std::set<std::pair<int64_t, int64_t>> open;  // (total load, bin) of bins with room
+    for (int64_t b = 0; b < nb; ++b) open.insert({0, b});
+    for (int64_t k = 0; k < nfull; ++k) {
+        const int64_t s = by_len[(size_t)k];
+        int64_t best = -1, best_mx = 0;
+        int seen = 0;
+        for (auto it = open.begin(); it != open.end() && seen < 64; ++it, ++seen) {
+            const int64_t b = it->second;
+            int64_t mx = 0;
+            for (int64_t c = 0; c < nch; ++c)
+                mx = std::max(mx, load[(size_t)(b * nch + c)] + steps[(size_t)(s * nch + c)]);
+            if (best < 0 || mx < best_mx) best = b, best_mx = mx;
+        }
+        open.erase({btot[(size_t)best], best});
+        for (int64_t c = 0; c < nch; ++c) load[(size_t)(best * nch + c)] += steps[(size_t)(s * nch + c)];
+        btot[(size_t)best] += tot[(size_t)s];
+        bins[(size_t)best].push_back(s);
+        if (bins[(size_t)best].size() < 4) open.insert({btot[(size_t)best], best});
+    }
+    std::vector<int64_t> border((size_t)nb);
+    std::iota(border.begin(), border.end(), 0);
+    std::stable_sort(border.begin(), border.end(), [&](int64_t a, int64_t b) { return btot[(size_t)a] > btot[(size_t)b]; });
+    std::vector<std::vector<int64_t>> grp((size_t)ng);
+    for (int64_t k = 0; k < nb; ++k) {
+        const int64_t rnd = k / ng, p = k % ng;
+        grp[(size_t)(rnd % 2 == 0 ? p : ng - 1 - p)].push_back(border[(size_t)k]);
+    }
+    for (int64_t g = 0; g < ng; ++g)
+        for (int64_t i = 0; i < 16; ++i) pos[(size_t)(16 * g + i)] = bins[(size_t)grp[(size_t)g][(size_t)(i % 4)]][(size_t)(i / 4)];
+    std::vector<int64_t> rest(by_len.begin() + nfull, by_len.end());
+    std::sort(rest.begin(), rest.end());
+    std::copy(rest.begin(), rest.end(), pos.begin() + nfull);
+    return pos;
+}
+
 // ---- Derived copies ---------------------------------------------------------
 // Each derived copy is planned from per-row (per-chunk) nonzero counts alone:
 // row order, slab or group shapes and run offsets.  The upload path counts
@@ -119,20 +187,26 @@ bool plan_sell(int64_t M, int64_t K, const std::vector<int32_t>& cnt, SellPlan* 
     std::vector<int32_t> order((size_t)M);
     std::iota(order.begin(), order.end(), 0);
     sell_order(cnt, nch, order.data(), M, 0);
-    p->off.assign((size_t)(p->nslab * nch + 1), 0);
+    // padded steps of each k-d slab in each chunk
+    std::vector<int64_t> steps((size_t)(p->nslab * nch));
     for (int64_t sl = 0; sl < p->nslab; ++sl)
         for (int64_t c = 0; c < nch; ++c) {
             int32_t mx = 0;
             for (int64_t i = sl * R; i < std::min(M, sl * R + R); ++i)
                 mx = std::max(mx, cnt[(size_t)(order[(size_t)i] * nch + c)]);
-            const int64_t steps = (mx + pfr::kSellStepPad - 1) / pfr::kSellStepPad * pfr::kSellStepPad;
-            p->off[(size_t)(sl * nch + c + 1)] = p->off[(size_t)(sl * nch + c)] + steps / 8 * 64;
+            steps[(size_t)(sl * nch + c)] = (mx + pfr::kSellStepPad - 1) / pfr::kSellStepPad * pfr::kSellStepPad;
         }
-    p->len = p->off.back();
-    if (p->len + pfr::kSellTail > INT32_MAX) return false;
+    const std::vector<int64_t> place = sell_place(steps, p->nslab, nch);
+    p->off.assign((size_t)(p->nslab * nch + 1), 0);
     p->perm.assign((size_t)(p->nslab * R), -1);
-    std::copy(order.begin(), order.end(), p->perm.begin());
-    return true;
+    for (int64_t sl = 0; sl < p->nslab; ++sl) {
+        const int64_t from = place[(size_t)sl];
+        for (int64_t c = 0; c < nch; ++c)
+            p->off[(size_t)(sl * nch + c + 1)] = p->off[(size_t)(sl * nch + c)] + steps[(size_t)(from * nch + c)] / 8 * 64;
+        for (int64_t i = from * R; i < std::min(M, from * R + R); ++i) p->perm[(size_t)(sl * R + i - from * R)] = order[(size_t)i];
+    }
+    p->len = p->off.back();
+    return p->len + pfr::kSellTail <= INT32_MAX;
 }
 
 // Uploads the plan's tables (sell_blk is set by the fill).
@@ -174,8 +248,9 @@ void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vecto
     std::vector<int4> blk((size_t)(p.len + pfr::kSellTail));
     for (auto& b : blk) b = make_int4(pad_off, 0, pad_off, 0);
     std::vector<int32_t> t((size_t)nch);
-    for (int64_t i = 0; i < M; ++i) {
+    for (int64_t i = 0; i < p.nslab * R; ++i) {
         const int32_t row = p.perm[(size_t)i];
+        if (row < 0) continue;  // the lanes of a partial slab past its rows
         const int64_t sl = i / R, r = i % R;
         std::fill(t.begin(), t.end(), 0);
         for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
@@ -632,17 +707,20 @@ __device__ __forceinline__ int32_t first_at_least(const int32_t* __restrict__ co
     return lo;
 }
 
-// Sliced-ELL fill, one wave per sorted position i (row perm[i], slab i / 16,
-// lane i % 16): entry j of chunk c is that chunk's step j - (the row's first
-// entry in c), as build_sell places it.  blk holds the padding pattern.
-__global__ __launch_bounds__(256) void k_sell_fill(int64_t M, const int32_t* __restrict__ perm,
+// Sliced-ELL fill, one wave per slab position i (row perm[i], slab i / 16,
+// lane i % 16; -1 for the lanes of a partial slab past its rows): entry j
+// of chunk c is that chunk's step j - (the row's first entry in c), as
+// build_sell places it.  blk holds the padding pattern.
+__global__ __launch_bounds__(256) void k_sell_fill(int64_t npos, const int32_t* __restrict__ perm,
                                                    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
                                                    const float* __restrict__ val, const int64_t* __restrict__ off,
                                                    int nch, int kc, int4* __restrict__ blk) {
     const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (i >= M) return;
+    if (i >= npos) return;
     const int lane = threadIdx.x & 63;
-    const int32_t row = perm[i], b = rowptr[row], e = rowptr[row + 1];
+    const int32_t row = perm[i];
+    if (row < 0) return;  // a lane of a partial slab past its rows
+    const int32_t b = rowptr[row], e = rowptr[row + 1];
     const int64_t sl = i / pfr::kSellRows, r = i % pfr::kSellRows;
     for (int32_t j = b + lane; j < e; j += 64) {
         const int32_t k = col[j], c = k / kc;
@@ -790,8 +868,9 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
                 fill_dev(w->sell_blk, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
                 set_sell(w, p, s);
                 int64_t* off = dev_alloc_copy(p.off.data(), (int64_t)p.off.size(), s);
-                hipLaunchKernelGGL(k_sell_fill, dim3(waves_grid(M)), dim3(256), 0, s, M, w->sell_perm, w->rowptr,
-                                   w->col, val, off, (int)p.nch, (int)p.kc, w->sell_blk);
+                const int64_t npos = p.nslab * pfr::kSellRows;  // perm's length
+                hipLaunchKernelGGL(k_sell_fill, dim3(waves_grid(npos)), dim3(256), 0, s, npos, w->sell_perm,
+                                   w->rowptr, w->col, val, off, (int)p.nch, (int)p.kc, w->sell_blk);
                 hipError_t e = hipGetLastError();
                 (void)hipStreamSynchronize(s);
                 (void)hipFree(off);

@@ -274,6 +274,28 @@ def test_column_slice_layout_cases(ctx):
     assert np.array_equal(Y[fin].view(np.uint32), R[fin].view(np.uint32))
 
 
+def test_column_slice_placed_slabs(ctx):
+    """Slab placement: 4087 rows (256 slabs, one of them holding 7 rows) are
+    dealt out to workgroups by length, so the partial slab sits inside the
+    slab array.  The copy built from host arrays and the one built from a
+    dense device weight both match the oracle bit for bit through the 16-,
+    8- and 4-wave launches (N = 256, 128, 64)."""
+    import torch
+
+    M, K = 4087, 4096
+    ip, ix, v = workloads.csr_uniform(M, K, 0.1, 0.02, seed=77)
+    dW = torch.from_numpy(workloads.csr_to_dense(M, K, ip, ix, v)).cuda()
+    torch.cuda.synchronize()
+    weights = {"host": ctx.csr_upload(M, K, ip, ix, v), "device": ctx.csr_from_dense_dev(dW.data_ptr(), M, K)}
+    rng = np.random.default_rng(9)
+    for N in (256, 128, 64):
+        X = rng.standard_normal((K, N)).astype(np.float32)
+        R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+        for name, W in weights.items():
+            say(f"placed slabs: {name} N={N}")
+            assert bits_equal(W.spmm(X), R), (name, N)
+
+
 def check_fast(Y, R):
     """Fast-mode bar: NaN exactly where the oracle has it, infinities equal,
     the finite entries normwise within 1e-5 of the oracle's largest."""
