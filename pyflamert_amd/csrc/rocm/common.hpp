@@ -106,6 +106,10 @@ struct DevBuf {
 struct pfr_ctx {
     int device = 0;
     int num_cu = 256;
+    // Fast products with few columns use the merge-path kernels where the
+    // weight has that partition (PFR_CSR_MERGE=0 at init selects the
+    // nnz-balanced kernels instead, for comparison).
+    bool merge = true;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     // scratch[0..1]: staged inputs, scratch[2]: staged output, scratch[3]:
@@ -186,6 +190,30 @@ struct pfr_csr {
     void* bal_val = nullptr;
     uint16_t* bal_col = nullptr;
     int32_t bal_ngroup = 0, bal_nchunk = 0, bal_kcw = 0;
+    // Merge-path partition for the fast kernels that read col16 and val in
+    // place: the M row ends and nnz nonzeros, taken as one sequence in which
+    // row r's end follows its last nonzero, are cut into mp_groups *
+    // kMergeWaves equal shares, one per wave.  mp_wave[q] = {row, nonzero}
+    // is the merge coordinate where wave q starts (rows < row ended, nonzeros
+    // < nonzero taken); mp_wave[Q] = {M, nnz}.  Workgroup p is waves
+    // p * kMergeWaves ...; a row cut by a workgroup boundary is summed by its
+    // contributors' partials: mp_grp[p] = {A, B, A', 0}, where A >= 0 when p
+    // takes the end of a row that started in workgroup A < p, and B >= 0 when
+    // p's last row continues to workgroup B (which takes its end; the row
+    // started in A').  A row cut between two workgroups meets in
+    // mp_xchg[B] (tag << 32 | partial's bits, zero between launches); one
+    // cut by more: mp_carry[2p] holds p's partial of its continuing row,
+    // mp_carry[2p + 1] of the row whose end it takes, and mp_cnt[p] counts
+    // the arrivals of the row p ends (zero between launches).  col16 and val
+    // hold whole records of four entries and then one spare record (padding
+    // entries: value 0, column K).
+    int2* mp_wave = nullptr;
+    int4* mp_wmeta = nullptr;  // [Q] the rows each wave shares within its workgroup (set_merge)
+    int4* mp_grp = nullptr;
+    unsigned long long* mp_xchg = nullptr;
+    float* mp_carry = nullptr;
+    uint32_t* mp_cnt = nullptr;
+    int32_t mp_groups = 0;
     // Stored-entry bitmap (set by pfr_csr_dense_semantics): bit k % 64 of
     // pattern[r * pattern_nw + k / 64] is set when row r stores column k.
     // While it is set, every product through the handle is followed by the
@@ -204,6 +232,9 @@ constexpr int kSellMaxKC = 1024;   // K rows per LDS chunk (1024 x 64 B = 64 KiB
 constexpr int kSellStepPad = 8;    // steps per (slab, chunk) run are a multiple of this (one group)
 constexpr int kSellTail = 512;     // int4 after the last run, read by the unconditional prefetch (8 groups)
 constexpr int kBalChunk = 4096;    // most columns per chunk of the balanced copy
+constexpr int kMergeWaves = 16;    // waves per merge-path workgroup
+constexpr int kMergeMinItems = 256;  // fewest merge items (row ends + nonzeros) per wave
+constexpr int kMergeMaxK = 16383;  // x staged in LDS with its zero slot: (K + 1) * 4 B <= 64 KiB
 }
 
 namespace pfr {

@@ -1,4 +1,6 @@
 // Context, error text and stream handling of the C ABI.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace pfr {
@@ -50,6 +52,8 @@ int pfr_rocm_init(int device, pfr_ctx** out) {
         auto* ctx = new pfr_ctx();
         ctx->device = device;
         ctx->num_cu = prop.multiProcessorCount;
+        const char* mp = std::getenv("PFR_CSR_MERGE");
+        ctx->merge = !(mp && std::string(mp) == "0");
         hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             delete ctx;

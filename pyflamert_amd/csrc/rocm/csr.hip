@@ -32,12 +32,34 @@ T* dev_alloc_copy(const T* host, int64_t count, hipStream_t s) {
     return static_cast<T*>(p);
 }
 
+template <class T>
+T* dev_alloc(int64_t count) {
+    void* p = nullptr;
+    PFR_HIP(hipMalloc(&p, sizeof(T) * (size_t)(count > 0 ? count : 1)));
+    return static_cast<T*>(p);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void k_fill(T* __restrict__ p, int64_t n, T v) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+template <class T>
+void fill_dev(T* p, int64_t n, T v, hipStream_t s) {
+    if (n <= 0) return;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+    PFR_HIP(hipGetLastError());
+}
+
 void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
                     (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0, (void*)w->col16,
                     (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col, (void*)w->bal_meta,
-                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col, (void*)w->pattern})
+                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col, (void*)w->pattern,
+                    (void*)w->mp_wave, (void*)w->mp_wmeta, (void*)w->mp_grp, (void*)w->mp_xchg,
+                    (void*)w->mp_carry, (void*)w->mp_cnt})
         if (p) (void)hipFree(p);
     delete w;
 }
@@ -522,6 +544,152 @@ void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector
     set_bal(w, p, s);  // synchronizes: v and cidx outlive the uploads
 }
 
+// Merge-path partition (layout at pfr_csr::mp_wave) of the CSR with row
+// pointers `rowptr`, after Merrill and Garland, "Merge-based parallel sparse
+// matrix-vector multiplication" (SC 2016): the row ends and the nonzeros are
+// one sequence of M + nnz items (row r's end after its last nonzero), and a
+// point on it, a diagonal d, is the coordinate {rows ended, nonzeros taken}
+// whose sum is d, found by binary search (the number of row ends i taken
+// before nonzero d - i is the first i with rowptr[i + 1] > d - i - 1).
+// Workgroup boundaries are placed at row ends where that costs little: the
+// smallest capacity C for which a greedy fill -- each workgroup ends at the
+// last row end within C items of its start, or at exactly C items when no
+// row ends there -- needs at most one workgroup per CU.  So a row is cut
+// between workgroups only when it is longer than a share, and every
+// workgroup's load stays within a row of C (on the int8 decode weights at
+// 30 % with lognormal rows the heaviest holds 1.007 to 1.041 times the
+// mean).  Within a workgroup the waves take exactly equal shares.  Uploads
+// the tables and zeroes the exchange words and arrival counters.  False (no
+// partition) when the weight has no column copy in uint16 or x does not fit
+// the staged slot.
+bool set_merge(pfr_csr* w, const std::vector<int32_t>& rowptr, hipStream_t s) {
+    const int64_t M = w->M, nnz = w->nnz, T = M + nnz, W = pfr::kMergeWaves;
+    if (w->col16 == nullptr || nnz == 0 || w->K > pfr::kMergeMaxK || nnz > INT32_MAX - 4096) return false;
+    const int64_t cu = w->ctx->num_cu > 0 ? w->ctx->num_cu : 256;
+    const int64_t P0 = std::max<int64_t>(1, std::min<int64_t>(cu, T / (W * pfr::kMergeMinItems)));
+    std::vector<int64_t> ends((size_t)M);  // the diagonal just after row r's end
+    for (int64_t r = 0; r < M; ++r) ends[(size_t)r] = rowptr[(size_t)r + 1] + r + 1;
+    auto greedy = [&](int64_t C, std::vector<int64_t>* D) {
+        int64_t x = 0, n = 0;
+        if (D) D->assign(1, 0);
+        while (x < T) {
+            const auto it = std::upper_bound(ends.begin(), ends.end(), x + C);
+            const int64_t e = it == ends.begin() ? -1 : *(it - 1);  // the last row end within C
+            x = e > x ? e : std::min(x + C, T);
+            ++n;
+            if (D) D->push_back(x);
+        }
+        return n;
+    };
+    int64_t lo = (T + P0 - 1) / P0, hi = T;
+    while (lo < hi) {
+        const int64_t mid = lo + (hi - lo) / 2;
+        if (greedy(mid, nullptr) <= P0) hi = mid;
+        else lo = mid + 1;
+    }
+    std::vector<int64_t> D;
+    const int64_t P = greedy(lo, &D);
+    auto search = [&](int64_t d) {
+        int64_t i0 = std::max<int64_t>(d - nnz, 0), i1 = std::min<int64_t>(d, M);
+        while (i0 < i1) {
+            const int64_t mid = i0 + (i1 - i0) / 2;
+            if (rowptr[(size_t)mid + 1] <= d - mid - 1) i0 = mid + 1;
+            else i1 = mid;
+        }
+        return make_int2((int)i0, (int)(d - i0));
+    };
+    // a workgroup's waves start on whole records (a multiple of four
+    // nonzeros): the point of the path at that nonzero where every row
+    // ending before it has ended, and a row ending exactly there keeps the
+    // side the diagonal gave it
+    const auto e1 = rowptr.begin() + 1;
+    const int64_t Q = P * W;
+    std::vector<int2> wp((size_t)Q + 1);
+    for (int64_t p = 0; p < P; ++p) {
+        const int2 end = search(D[(size_t)p + 1]);
+        wp[(size_t)(p * W)] = search(D[(size_t)p]);
+        for (int64_t t = 1; t < W; ++t) {
+            const int2 c = search(D[(size_t)p] + t * (D[(size_t)p + 1] - D[(size_t)p]) / W);
+            const int2 prev = wp[(size_t)(p * W + t - 1)];
+            const int64_t j = std::max<int64_t>(std::min<int64_t>(((int64_t)c.y + 3) / 4 * 4, end.y), prev.y);
+            const int64_t lt = std::lower_bound(e1, e1 + M, (int32_t)j) - e1;  // rows ending before j
+            const int64_t le = std::upper_bound(e1, e1 + M, (int32_t)j) - e1;  // rows ending at or before j
+            const int64_t i = std::max<int64_t>(std::min<int64_t>(std::max<int64_t>(c.x, lt), le), prev.x);
+            wp[(size_t)(p * W + t)] = make_int2((int)i, (int)j);
+        }
+    }
+    wp[(size_t)Q] = make_int2((int)M, (int)nnz);
+    auto I0 = [&](int64_t p) { return (int64_t)wp[(size_t)(p * W)].x; };
+    auto J0 = [&](int64_t p) { return (int64_t)wp[(size_t)(p * W)].y; };
+    // the workgroup holding nonzero n, searched back from p (n < J0(p + 1))
+    auto holder = [&](int64_t n, int64_t p) {
+        while (p > 0 && J0(p) > n) --p;
+        return p;
+    };
+    std::vector<int4> gp((size_t)P, make_int4(-1, -1, -1, 0));
+    for (int64_t p = 0; p < P; ++p) {
+        const int64_t i0 = I0(p), j0 = J0(p), i1 = I0(p + 1), j1 = J0(p + 1);
+        if (i1 > i0 && rowptr[(size_t)i0] < j0) gp[(size_t)p].x = (int)holder(rowptr[(size_t)i0], p - 1);
+        if (i1 < M && j1 > std::max<int64_t>(rowptr[(size_t)i1], j0)) {
+            int64_t b = p + 1;
+            while (I0(b + 1) <= i1) ++b;  // the workgroup that takes row i1's end (b < P: the last ends at M)
+            gp[(size_t)p].y = (int)b;
+            gp[(size_t)p].z = (int)(rowptr[(size_t)i1] >= j0 ? p : holder(rowptr[(size_t)i1], p - 1));
+        }
+    }
+    // per wave, the rows it shares with other waves of its workgroup: the
+    // row whose end it takes after earlier waves began it ("own") and the
+    // row it leaves unfinished ("give"), each with the wave where the row
+    // starts (-1: before the workgroup), the wave that takes its end (W:
+    // after the workgroup) and how many waves add to it, so the last of them
+    // can finish it: {own start or -2, give start, give end or -1, own count
+    // | give count << 16}
+    std::vector<int4> wm((size_t)Q);
+    for (int64_t p = 0; p < P; ++p) {
+        const int2* c = wp.data() + p * W;  // c[0 .. W]: the workgroup's wave starts and its end
+        auto gives = [&](int64_t t) {
+            return c[t + 1].x < M && c[t + 1].y > std::max<int64_t>(rowptr[(size_t)c[t + 1].x], c[t].y);
+        };
+        auto owns = [&](int64_t t) { return c[t].x < c[t + 1].x && rowptr[(size_t)c[t].x] < c[t].y; };
+        auto start_wave = [&](int64_t n, int64_t t) {
+            while (t > 0 && n < c[t].y) --t;
+            return n < c[t].y ? int64_t(-1) : t;
+        };
+        for (int64_t t = 0; t < W; ++t) {
+            int4 m = make_int4(-2, -1, -1, 0);
+            if (owns(t)) {
+                const int64_t a = start_wave(rowptr[(size_t)c[t].x], t);
+                int64_t n = 1;
+                for (int64_t u = std::max<int64_t>(a, 0); u < t; ++u) n += gives(u);
+                m.x = (int)a;
+                m.w |= (int)n;
+            }
+            if (gives(t)) {
+                const int64_t a = start_wave(rowptr[(size_t)c[t + 1].x], t);
+                int64_t b = t + 1;
+                while (b < W && c[b].x == c[b + 1].x) ++b;  // the next wave that takes a row end
+                int64_t n = b < W;
+                for (int64_t u = std::max<int64_t>(a, 0); u < b; ++u) n += gives(u);
+                m.y = (int)a;
+                m.z = (int)b;
+                m.w |= (int)n << 16;
+            }
+            wm[(size_t)(p * W + t)] = m;
+        }
+    }
+    w->mp_wave = dev_alloc_copy(wp.data(), Q + 1, s);
+    w->mp_wmeta = dev_alloc_copy(wm.data(), Q, s);
+    w->mp_grp = dev_alloc_copy(gp.data(), P, s);
+    w->mp_xchg = dev_alloc<unsigned long long>(P);
+    fill_dev(w->mp_xchg, P, 0ull, s);
+    w->mp_carry = dev_alloc<float>(2 * P);
+    w->mp_cnt = dev_alloc<uint32_t>(P);
+    fill_dev(w->mp_cnt, P, 0u, s);
+    w->mp_groups = (int32_t)P;
+    PFR_HIP(hipStreamSynchronize(s));  // wp and gp outlive the uploads
+    return true;
+}
+
 pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
                const std::vector<int32_t>& col, const void* vals, pfr_dtype vdt,
                const float* row_scales) {
@@ -538,15 +706,28 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
         hipStream_t s = ctx->stream;
         w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
         w->col = dev_alloc_copy(col.data(), w->nnz, s);
+        // col16 and val hold whole records of four and one spare record;
+        // padding entries are value 0 at column K (x's zero slot in the
+        // merge-path kernels, which read whole records and point loads past
+        // a share at the spare one)
+        const int64_t npad = (w->nnz + 3) / 4 * 4 + 4;
         if (K <= 65536 && w->nnz > 0) {
             std::vector<uint16_t> c16(col.begin(), col.end());
-            w->col16 = dev_alloc_copy(c16.data(), w->nnz, s);
+            c16.resize((size_t)npad, (uint16_t)std::min<int64_t>(K, 65535));
+            w->col16 = dev_alloc_copy(c16.data(), npad, s);
             PFR_HIP(hipStreamSynchronize(s));  // c16 goes out of scope
         }
-        if (vdt == PFR_F32)
-            w->val = dev_alloc_copy(static_cast<const float*>(vals), w->nnz, s);
-        else
-            w->val = dev_alloc_copy(static_cast<const int8_t*>(vals), w->nnz, s);
+        if (vdt == PFR_F32) {
+            std::vector<float> v(static_cast<const float*>(vals), static_cast<const float*>(vals) + w->nnz);
+            v.resize((size_t)npad, 0.0f);
+            w->val = dev_alloc_copy(v.data(), npad, s);
+            PFR_HIP(hipStreamSynchronize(s));
+        } else {
+            std::vector<int8_t> v(static_cast<const int8_t*>(vals), static_cast<const int8_t*>(vals) + w->nnz);
+            v.resize((size_t)npad, 0);
+            w->val = dev_alloc_copy(v.data(), npad, s);
+            PFR_HIP(hipStreamSynchronize(s));
+        }
         if (row_scales) w->row_scale = dev_alloc_copy(row_scales, M, s);
         std::vector<int32_t> blocks = spmv_blocks(rowptr, M);
         w->n_spmv_blocks = (int64_t)blocks.size() - 1;
@@ -560,6 +741,7 @@ pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& r
         build_chain(w, rowptr, col, vals, s);
         if (vdt == PFR_F32) build_bal(w, rowptr, col, static_cast<const float*>(vals), s);
         else build_bal(w, rowptr, col, static_cast<const int8_t*>(vals), s);
+        set_merge(w, rowptr, s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {
@@ -582,19 +764,6 @@ struct DevTmp {
 };
 
 constexpr int kMaxCountChunks = 4096;  // sliced-ELL chunks counted in LDS (K <= 4M)
-
-template <class T>
-__global__ __launch_bounds__(256) void k_fill(T* __restrict__ p, int64_t n, T v) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
-}
-
-template <class T>
-void fill_dev(T* p, int64_t n, T v, hipStream_t s) {
-    if (n <= 0) return;
-    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
-    PFR_HIP(hipGetLastError());
-}
 
 // D[c, r] = A[r, c] (* mask[r, c]) for A rows x cols: the op(W) a CSR of
 // W^T is built from, through 32 x 33 LDS tiles (coalesced both ways).
@@ -788,13 +957,6 @@ __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, con
     }
 }
 
-template <class T>
-T* dev_alloc(int64_t count) {
-    void* p = nullptr;
-    PFR_HIP(hipMalloc(&p, sizeof(T) * (size_t)(count > 0 ? count : 1)));
-    return static_cast<T*>(p);
-}
-
 unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
 
 // The CSR handle of D (M x K, row-major, device), with every derived copy
@@ -846,9 +1008,14 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
         w->cols_sorted = true;
         w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
         w->col = dev_alloc<int32_t>(w->nnz);
-        float* val = dev_alloc<float>(w->nnz);
+        const int64_t npad = (w->nnz + 3) / 4 * 4 + 4;  // whole records and a spare one, as build() pads
+        float* val = dev_alloc<float>(npad);
         w->val = val;
-        if (K <= 65536 && w->nnz > 0) w->col16 = dev_alloc<uint16_t>(w->nnz);
+        fill_dev(val + w->nnz, npad - w->nnz, 0.0f, s);
+        if (K <= 65536 && w->nnz > 0) {
+            w->col16 = dev_alloc<uint16_t>(npad);
+            fill_dev(w->col16 + w->nnz, npad - w->nnz, (uint16_t)std::min<int64_t>(K, 65535), s);
+        }
         hipLaunchKernelGGL(k_dense_compact, dim3((unsigned)M), dim3(256), 0, s, D, K, thr, w->rowptr, w->col,
                            w->col16, val);
         PFR_HIP(hipGetLastError());
@@ -925,6 +1092,7 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
                 if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_fill: ") + hipGetErrorString(e));
             }
         }
+        set_merge(w, rowptr, s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
     } catch (...) {

@@ -974,6 +974,319 @@ void launch_bal_fast(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx
                        W->bal_col, W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act);
 }
 
+// The sum of v over the wave's 64 lanes, uniform (returned in an SGPR): DPP
+// adds within quads, half rows and rows, then the row broadcasts carry the
+// row sums into lane 63, which is read out.  One fixed order, so the same
+// bits every time.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<0xB1, 0xF>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E, 0xF>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141, 0xF>(v);  // row_half_mirror
+    v += dpp_f<0x140, 0xF>(v);  // row_mirror: every lane holds its row's sum
+    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Entry k (0..3) of a four-entry record: value (int8 or float) and column.
+template <bool I8>
+__device__ __forceinline__ float rec_val(const typename std::conditional<I8, uint32_t, float4>::type& v, int k) {
+    if constexpr (I8) return (float)(int8_t)((v >> (8 * k)) & 0xFF);
+    else return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ uint32_t rec_col(const uint2& c, int k) {
+    const uint32_t h = k < 2 ? c.x : c.y;
+    return (k & 1) ? (h >> 16) : (h & 0xFFFFu);
+}
+
+// A row cut by workgroup boundaries, finished by whichever of its
+// contributors arrives last, so no workgroup waits for another (A: the
+// workgroup where the row starts, Bw: the one that takes its end; `give`:
+// the caller is not Bw).  Everything goes through device-scope (agent)
+// atomics, which the hardware keeps coherent across the XCDs' L2 caches; an
+// acquire/release fence would instead write back and invalidate the whole L2
+// of the XCD, once per workgroup.
+// - Two contributors (Bw == A + 1, the usual cut): each swaps its tagged
+//   partial into xchg[Bw]; whoever finds the other's there holds both, adds
+//   them in order (A's first) and clears the word.  One round trip.
+// - More: each stores its partial (carry[2p] for A .. Bw - 1, carry[2Bw + 1]
+//   for Bw), waits until the store is complete and counts itself in cnt[Bw];
+//   the last arrival sums carry[2A] + ... + carry[2Bw + 1] in workgroup order
+//   and clears the counter.
+// The sum is the same whatever the arrival order.
+template <bool I8>
+__device__ __forceinline__ void merge_arrive(unsigned long long* __restrict__ xchg, float* __restrict__ carry,
+                                             uint32_t* __restrict__ cnt, int p, bool give, float v, int A, int Bw,
+                                             int row, float scale, float* __restrict__ y, int64_t ldy_r,
+                                             const float* __restrict__ bias, int64_t c_size, float beta, int act) {
+    float s;
+    if (Bw == A + 1) {
+        const unsigned long long mine = (give ? 1ull : 2ull) << 32 | (uint32_t)__float_as_int(v);
+        const unsigned long long old =
+            __hip_atomic_exchange(xchg + Bw, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((old >> 32) == 0) return;  // the other contributor finishes the row
+        const float other = __int_as_float((int)(uint32_t)old);
+        s = give ? v + other : other + v;
+        __hip_atomic_store(xchg + Bw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __hip_atomic_store(carry + (give ? 2 * p : 2 * p + 1), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // every counter zero: the partial has reached its coherent home
+        const uint32_t old = __hip_atomic_fetch_add(cnt + Bw, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old != (uint32_t)(Bw - A)) return;
+        s = __hip_atomic_load(carry + 2 * A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int t = A + 1; t < Bw; ++t)
+            s += __hip_atomic_load(carry + 2 * t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s += __hip_atomic_load(carry + 2 * Bw + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + Bw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (I8) s *= scale;
+    const int64_t f = (int64_t)row * ldy_r;
+    y[f] = bias_add(s, f, bias, c_size, beta, act);
+}
+
+// Fast N = 1 SpMV with merge-path work partitioning (pfr_csr::mp_wave),
+// reading the CSR's own uint16 columns and values, so it needs no copy of
+// the weight.  Every wave takes an equal share of its workgroup's row ends
+// and nonzeros, and workgroups end at row ends wherever a row is shorter
+// than a share, so the launch is balanced however skewed the rows are.  A
+// wave streams the records (four consecutive entries) that hold its share
+// (lane l takes records l, l + 64, ...: coalesced 4-byte int8 or 16-byte
+// float values and 8-byte column loads), U records per lane and batch, two
+// batches in flight; loads past the share read the spare record after the
+// last one, whose entries (like the last record's padding) are value 0 at
+// x's zero slot.  x is staged in LDS once per workgroup.  Per lane, fused multiply-adds into four partial sums of the
+// current segment; where a segment ends inside a batch (a uniform test
+// against the next boundary), the batch's products are split with selects
+// and the wave reduces the finished segment.  The segments are: the entries
+// of the share's first record before the share (dropped; only a share that
+// starts a workgroup, at a row end, begins inside a record), the rows whose
+// ends the share takes, the row that continues past the share, and, when
+// the share ends inside a record, that record's rest (dropped).
+// Lane (e % 64) keeps the e-th finished row's sum, written out 64 rows at a
+// time, so the walk stores nothing to memory.  A row that started in an
+// earlier wave, and the continuing one, are left in LDS, and each wave, when
+// it is done, counts itself in those rows' arrival counters (LDS atomics;
+// the planner gives every shared row its first wave, the wave that takes its
+// end and how many waves add to it): the last to arrive sums the row's
+// partials in wave order and writes it, so no wave waits for another, and a
+// row cut by a workgroup boundary goes on to merge_arrive.  The row scales
+// those writes need are loaded at the start.  An int8 row's sum is scaled
+// once at the end.  The sum is reassociated, so this kernel serves the fast
+// mode only.
+template <bool I8, int U, int XL>
+__global__ __launch_bounds__(64 * pfr::kMergeWaves) void k_spmv_merge(
+    int M, int K, int spare, const int2* __restrict__ wpart, const int4* __restrict__ wmeta,
+    const int4* __restrict__ gpart,
+    const int32_t* __restrict__ rowptr, const void* __restrict__ vals, const uint16_t* __restrict__ cols,
+    const float* __restrict__ rs, const float* __restrict__ x, int ldx, float* __restrict__ y, int64_t ldy_r,
+    const float* __restrict__ bias, int64_t c_size, float beta, int act, float* __restrict__ carry,
+    unsigned long long* __restrict__ xchg, uint32_t* __restrict__ cnt) {
+    constexpr int W = pfr::kMergeWaves, NT = 64 * W, B = 64 * U;  // B: records per wave and batch
+    extern __shared__ float4 dyn[];
+    float* const xs = reinterpret_cast<float*>(dyn);  // x[0 .. K) and zeros to XL * NT (K < XL * NT)
+    __shared__ float hv[W], gv[W];  // each wave's partial of its first row (hv) and of its last (gv)
+    // each wave's first row and that row's scale (entry W: the workgroup's
+    // end), and the arrival counters of the rows the waves share (entry t:
+    // the row wave t ends, W: the one continuing past the workgroup)
+    __shared__ int wi[W + 1];
+    __shared__ float wsc[W + 1];
+    __shared__ uint32_t lcnt[W + 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p = (int)blockIdx.x, q = p * W + wave;
+    const int is = __builtin_amdgcn_readfirstlane(wpart[q].x), js = __builtin_amdgcn_readfirstlane(wpart[q].y);
+    const int ie = __builtin_amdgcn_readfirstlane(wpart[q + 1].x);
+    const int je = __builtin_amdgcn_readfirstlane(wpart[q + 1].y);
+    using ValT = typename std::conditional<I8, uint32_t, float4>::type;
+    const ValT* V = static_cast<const ValT*>(vals);
+    const uint2* Cl = reinterpret_cast<const uint2*>(cols);
+    const int ra = js >> 2, rb = (je + 3) >> 2;  // the records holding entries js .. je - 1
+    const int nb = (rb - ra + B - 1) / B;
+    ValT va[U], vb[U];
+    uint2 ca[U], cb[U];
+    auto load = [&](ValT* v, uint2* c, int b) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int rec = ra + b * B + 64 * u + lane;
+            const int at = rec < rb ? rec : spare;
+            v[u] = V[at];
+            c[u] = Cl[at];
+        }
+        // keep the next batch's loads ahead of the fold of the one before:
+        // scheduled after them, that fold's first use would wait for every
+        // load in flight
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // x's loads first (XL per thread), then the first batch's, so the wait
+    // before x goes to LDS leaves the batch in flight
+    float xt[XL];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xt[i] = x[(int64_t)min(tid + NT * i, K - 1) * ldx];
+    // lane l: rowptr[is + l] (up to ie + 1), so the walk reads its row ends
+    // from registers instead of waiting on memory at each one
+    const int my_rp = rowptr[min(is + lane, ie < M ? ie + 1 : M)];
+    __builtin_amdgcn_sched_barrier(0);
+    load(va, ca, 0);  // unconditional (an empty share reads the spare record): waits after it stay exact
+    const int4 g = gpart[p], wm = wmeta[q];
+    const int rp_is = __builtin_amdgcn_readfirstlane(my_rp);
+    // the scales the write-out needs, loaded now and used after the walk:
+    // lane l's for row is + l, and those of the share's first and last rows
+    float my_sc = 1.0f, sc_is = 1.0f, sc_ie = 1.0f;
+    if constexpr (I8) {
+        my_sc = is + lane < ie ? rs[is + lane] : 1.0f;
+        sc_is = rs[min(is, M - 1)];
+        sc_ie = rs[min(ie, M - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xs[tid + NT * i] = tid + NT * i < K ? xt[i] : 0.0f;
+    if (lane == 0) {
+        gv[wave] = 0.0f;  // a share holding no entry of its last row adds nothing to it
+        hv[wave] = 0.0f;
+        wi[wave] = is;
+        wsc[wave] = sc_is;
+        lcnt[wave] = 0u;
+        if (wave == W - 1) {
+            wi[W] = ie;
+            wsc[W] = sc_ie;
+            lcnt[W] = 0u;
+        }
+    }
+    __syncthreads();
+    const bool head_cut = rp_is < js;  // the first row started in an earlier wave
+    // segment k ends at: js for k < is (the first record's entries before
+    // the share), rowptr[k + 1] for the rows whose ends the share takes, je
+    // for the row that continues (k == ie) when the share ends inside a
+    // record (past a whole record only padding follows, which adds +0), and
+    // never after that
+    auto row_end = [&](int k) {  // rowptr[k + 1], is <= k < ie
+        return k + 1 - is < 64 ? __builtin_amdgcn_readlane(my_rp, k + 1 - is) : rowptr[k + 1];
+    };
+    auto seg_end = [&](int k) { return k < is ? js : k < ie ? row_end(k) : k == ie && (je & 3) ? je : INT_MAX; };
+    int r = (js & 3) ? is - 1 : is;  // the current segment
+    int bnd = seg_end(r), bnd2 = seg_end(r + 1);
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float outv = 0.0f;  // lane e % 64: the sum of finished row is + e
+    auto flush = [&](int base, int n) {  // rows base .. base + n - 1 from lanes 0 .. n - 1
+        const int row = base + lane;
+        if (lane < n && !(row == is && head_cut)) {
+            float v = outv;
+            if constexpr (I8) v *= base == is ? my_sc : rs[row];
+            const int64_t f = (int64_t)row * ldy_r;
+            y[f] = bias_add(v, f, bias, c_size, beta, act);
+        }
+    };
+    // segment r ends: reduce its partials (a) and keep the sum
+    auto emit = [&]() {
+        const float v = wave_sum((a[0] + a[1]) + (a[2] + a[3]));
+        a[0] = a[1] = a[2] = a[3] = 0.0f;
+        if (r >= is && r < ie) {
+            const int e = r - is;
+            if (r == is && head_cut && lane == 0) hv[wave] = v;
+            outv = lane == (e & 63) ? v : outv;
+            if ((e & 63) == 63) flush(r - 63, 64);
+        } else if (r == ie && lane == 0) {
+            gv[wave] = v;
+        }
+        ++r;
+        bnd = bnd2;
+        bnd2 = seg_end(r + 1);
+    };
+    auto fold = [&](const ValT* v, const uint2* c, int b) {
+        const int n0 = 4 * (ra + b * B), n1 = n0 + 4 * B;  // the batch's entries n0 .. n1 - 1
+        if (bnd >= n1) {  // no segment ends in this batch
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) a[k] = __builtin_fmaf(rec_val<I8>(v[u], k), xs[rec_col(c[u], k)], a[k]);
+            return;
+        }
+        // products once, then each segment ending in the batch takes those
+        // before its end
+        float pr[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) pr[u][k] = rec_val<I8>(v[u], k) * xs[rec_col(c[u], k)];
+        do {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const bool pre = n0 + 4 * (64 * u + lane) + k < bnd;
+                    a[k] += pre ? pr[u][k] : 0.0f;
+                    pr[u][k] = pre ? 0.0f : pr[u][k];
+                }
+            emit();
+        } while (bnd < n1);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) a[k] += pr[u][k];
+    };
+    // batch b + 1's loads are issued before batch b is folded (past the last
+    // batch they read the spare record and are never folded)
+    int b = 0;
+    for (; b + 2 <= nb; b += 2) {
+        load(vb, cb, b + 1);
+        fold(va, ca, b);
+        load(va, ca, b + 2);
+        fold(vb, cb, b + 1);
+    }
+    if (b < nb) fold(va, ca, b);
+    while (r <= ie) emit();  // segments ending where the last batch ends (or a share of row ends only)
+    flush(ie - ((ie - is) & 63), (ie - is) & 63);
+    if (lane != 0) return;
+    // count this wave in the rows it shares; the last arrival of a row (from
+    // wave a0, or the workgroup's start when a0 < 0, to the one that takes
+    // its end, b, or past the workgroup when b == W) finishes it
+    auto arrive = [&](int a0, int b, int n) {
+        const uint32_t old = __hip_atomic_fetch_add(lcnt + b, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (old != (uint32_t)(n - 1)) return;
+        const int u1 = a0 < 0 ? 0 : a0;
+        float s = u1 < b ? gv[u1] : hv[b];
+        for (int u = u1 + 1; u < b; ++u) s += gv[u];
+        if (u1 < b && b < W) s += hv[b];
+        const int row = wi[b];
+        if (a0 >= 0 && b < W) {
+            if constexpr (I8) s *= wsc[b];
+            const int64_t f = (int64_t)row * ldy_r;
+            y[f] = bias_add(s, f, bias, c_size, beta, act);
+        } else if (b < W) {  // the row started in an earlier workgroup (g.x)
+            merge_arrive<I8>(xchg, carry, cnt, p, false, s, g.x, p, row, wsc[b], y, ldy_r, bias, c_size, beta, act);
+        } else {  // the row continues past the workgroup, to g.y (it started in g.z)
+            merge_arrive<I8>(xchg, carry, cnt, p, true, s, g.z, g.y, row, wsc[W], y, ldy_r, bias, c_size, beta, act);
+        }
+    };
+    if (wm.x != -2) arrive(wm.x, wave, wm.w & 0xFFFF);
+    if (wm.z != -1) arrive(wm.y, wm.z, wm.w >> 16);
+}
+
+constexpr int kMergeU = 2;  // records per lane and batch
+
+template <bool I8>
+void launch_merge(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, float* Y, int64_t ldy_r,
+                  const float* bias, int64_t c_size, float beta, int act) {
+    constexpr int NT = 64 * pfr::kMergeWaves;
+    const int xl = (int)(W->K / NT + 1);  // x loads per thread, K + 1 <= xl * NT (K <= kMergeMaxK, checked at upload)
+    const int XLs = xl <= 5 ? 5 : xl <= 8 ? 8 : xl <= 12 ? 12 : 16;
+    const size_t lds = (size_t)XLs * NT * 4;
+#define PFR_MERGE(XLV)                                                                                          \
+    hipLaunchKernelGGL((k_spmv_merge<I8, kMergeU, XLV>), dim3((unsigned)W->mp_groups), dim3(NT), lds, ctx->stream, \
+                       (int)W->M, (int)W->K, (int)((W->nnz + 3) / 4), W->mp_wave, W->mp_wmeta, W->mp_grp,       \
+                       W->rowptr, W->val,                                                                         \
+                       W->col16, W->row_scale, X, (int)ldx, Y, ldy_r, bias, c_size, beta, act, W->mp_carry,       \
+                       W->mp_xchg, W->mp_cnt)
+    if (XLs == 5) PFR_MERGE(5);
+    else if (XLs == 8) PFR_MERGE(8);
+    else if (XLs == 12) PFR_MERGE(12);
+    else PFR_MERGE(16);
+#undef PFR_MERGE
+}
+
 // Fast 2 <= N <= 8 over the nnz-balanced copy: a workgroup takes groups b
 // and b + gridDim.x (the copy holds at most two per CU), waves 0..7 the first
 // and 8..15 the second, and walks K chunk by chunk: the chunk's X rows are
@@ -1799,7 +2112,9 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
     hipStream_t s = ctx->stream;
     const void* val = W->val;
     const float* rs = W->row_scale;
-    if (FAST && N == 1 && W->bal_meta != nullptr && ldx < INT32_MAX) {
+    if (FAST && N == 1 && ctx->merge && W->mp_wave != nullptr && ldx < INT32_MAX) {
+        launch_merge<I8>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (FAST && N == 1 && W->bal_meta != nullptr && ldx < INT32_MAX) {
         launch_bal_fast<I8>(ctx, W, X, ldx, Y, ldy_r, bias, c_size, beta, act);
     } else if (FAST && N >= 2 && N <= 8 && W->bal_meta != nullptr) {
         if (N == 8 && ldx % 4 == 0 && aligned16(X))
