@@ -107,6 +107,7 @@ def ref_lib():
             "ref_f32_to_bf16": (None, [_P, _P, _I64]),
             "ref_save_mlp_pfm": (_INT, [C.c_char_p, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
             "ref_run_pfm": (_INT, [C.c_char_p, C.c_char_p, _P, _P, _INT, _P, _I64, _P]),
+            "ref_time_pfm": (_INT, [C.c_char_p, C.c_char_p, _P, _P, _INT, _INT, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -582,6 +583,16 @@ def ref_save_mlp_pfm(path, batch, w1, b1, w2, b2):
     w1, b1, w2, b2 = (_c(t, np.float32) for t in (w1, b1, w2, b2))
     _ref_check(ref_lib().ref_save_mlp_pfm(path.encode(), batch, w1.shape[0], w1.shape[1], w2.shape[1],
                                           _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2)))
+
+
+def ref_time_pfm(path, input_name, x, reps):
+    """Seconds per CPUExecutor::execute call on a graph loaded once."""
+    x = _c(x, np.float32)
+    shape = np.array(x.shape, np.int64)
+    t = np.zeros(reps, np.int64)
+    _ref_check(ref_lib().ref_time_pfm(path.encode(), input_name.encode(), _ptr(x), _ptr(shape), x.ndim, reps,
+                                      _ptr(t)))
+    return t.astype(np.float64) * 1e-9
 
 
 def ref_run_pfm(path, input_name, x, out_elems):

@@ -358,4 +358,23 @@ int ref_run_pfm(const char* path, const char* input_name, const float* x,
     });
 }
 
+// Load a .pfm with the reference loader once, then time `reps` calls of
+// CPUExecutor::execute on it (each call's wall time in ns into times_ns):
+// what a session's run() costs once its graph is loaded.
+int ref_time_pfm(const char* path, const char* input_name, const float* x, const int64_t* shape, int ndim,
+                 int reps, int64_t* times_ns) {
+    return guard([&] {
+        auto g = PyFlameFormat::load(path);
+        std::unordered_map<std::string, Tensor> feed;
+        feed[input_name] = make_f32(x, std::vector<int64_t>(shape, shape + ndim));
+        CPUExecutor ex;
+        for (int i = 0; i < reps; ++i) {
+            const auto t0 = std::chrono::steady_clock::now();
+            auto outs = ex.execute(*g, feed);
+            const auto t1 = std::chrono::steady_clock::now();
+            times_ns[i] = std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        }
+    });
+}
+
 }  // extern "C"

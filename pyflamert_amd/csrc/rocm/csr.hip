@@ -186,12 +186,16 @@ void sell_geom(int64_t K, int64_t* kc, int64_t* nch) {
     *nch = K > 0 ? (K + *kc - 1) / *kc : 0;
 }
 
+constexpr int kMaxCountChunks = 4096;  // sliced-ELL chunks counted in LDS by the device build (K <= 4M)
+
 // The sliced-ELL copy exists for float32 weights whose count table stays
-// small (else the row kernels serve).
+// small and whose chunks the device build can count in LDS (else the row
+// kernels serve), the same limit for the host and the device build, so
+// every product through either handle runs the same kernel.
 bool sell_wanted(int64_t M, int64_t K, int64_t nnz) {
     int64_t kc, nch;
     sell_geom(K, &kc, &nch);
-    return M > 0 && K > 0 && nnz > 0 && M * nch <= (int64_t(1) << 26);
+    return M > 0 && K > 0 && nnz > 0 && M * nch <= (int64_t(1) << 26) && nch <= kMaxCountChunks;
 }
 
 struct SellPlan {
@@ -763,7 +767,6 @@ struct DevTmp {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
-constexpr int kMaxCountChunks = 4096;  // sliced-ELL chunks counted in LDS (K <= 4M)
 
 // D[c, r] = A[r, c] (* mask[r, c]) for A rows x cols: the op(W) a CSR of
 // W^T is built from, through 32 x 33 LDS tiles (coalesced both ways).

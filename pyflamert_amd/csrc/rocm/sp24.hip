@@ -1437,7 +1437,7 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     hipLaunchKernelGGL((k_sp24_i8<OUTK, XR>), grid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idx, B, ldb,    \
                        (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
-    const int64_t rtiles = (W->M + 64 * kRB - 1) / (64 * kRB);  // 192-row tiles
+    const int64_t rtiles = (W->M + 64 * kRB - 1) / (64 * kRB);  // 256-row tiles (64 * kRB rows)
     const dim3 rgrid((unsigned)(rtiles * ntn));
 #define PFR_SP24_LAUNCH_R(OUTK)                                                                                \
     hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32, kRB>), rgrid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idxw, B, ldb, \

@@ -1,9 +1,12 @@
 """HIP graph capture of the product launches: a decode-like sequence of
-CSR products (fast and strict, batch 1 and 8, int8 and fp32 weights), a
-Gemm with bias and Relu, and a 2:4 int8 GEMM, captured once on a capture
-stream and replayed several times with eager work and synchronisations in
-between; every replay must give the eager results bit for bit (the same
-kernels on the same data).  None of these launches records a memset or an
+CSR products (fast and strict, batch 1 and 8, int8 and fp32 weights; the
+fast batch-1 products run the merge-path kernel, whose arrival counters the
+last arrival clears inside the kernel), a Gemm with bias and Relu through
+the allocation-free entry (its op(A)^T staged in the fixed per-device
+workspace), and a 2:4 int8 GEMM, captured once on a capture stream and
+replayed several times with eager work and synchronisations in between;
+every replay must give the eager results bit for bit (the same kernels on
+the same data).  None of these launches records a memset or an
 allocation."""
 import sys
 
@@ -61,7 +64,7 @@ def test_graph_replay_matches_eager(ctx):
         Wf.spmm_dev(x1.data_ptr(), 1, outs["f_1"].data_ptr(), mode="fast")
         Wf.spmm_dev(x8.data_ptr(), 8, outs["f_8"].data_ptr(), mode="strict")
         ctx.gemm_csr_dev(A.data_ptr(), 64, 3000, BT, outs["gemm"].data_ptr(), 1.0, 1.0, bias.data_ptr(), 700,
-                         relu=True)
+                         relu=True, noalloc=True)
         S.gemm_i8_dev(xq.data_ptr(), 256, outs["sp24"].data_ptr(), out="i32")
 
     main = torch.cuda.current_stream().cuda_stream

@@ -171,8 +171,13 @@ def test_i8_golden(ctx, golden):
 
 def test_i8_full_size_properties(ctx):
     """W 11008 x 4096 (2:4, per-row int8), X 4096 x 512 int8 (scale 0.05):
-    exact row sums and column sums of the int32 accumulators, plus 192 rows
-    checked against the oracle (accumulators and requantised int8)."""
+    every int32 accumulator against the exact product (a float64 BLAS product
+    of the int8 operands is exact here: every partial sum is below
+    4096 * 128^2 < 2^53), the float output of every row, (float)acc *
+    RN(s_row * 0.05) as quantized_matmul computes it (quant_ops.cpp:435,
+    :456-466), and every requantised int8 output against orc_quantize
+    (quant_ops.cpp:15-127); plus the exact row and column sums and 192 rows
+    against the oracle's own loops."""
     M, K, N = 11008, 4096, 512
     say("sp24 full size: generating")
     q, s = workloads.sp24_int8_weight(M, K, seed=3)
@@ -187,11 +192,20 @@ def test_i8_full_size_properties(ctx):
     rows.sort()
     acc = O.orc_int8_matmul_acc(q[rows], X)
     assert np.array_equal(Y[rows], acc)
-    say("sp24 full size: requant")
-    F = O.orc_quantized_matmul_rowscale(q[rows], X, s[rows], 0.05)
-    os_, _ = O.orc_dynamic_params(F)
+    say("sp24 full size: every accumulator against the float64 product")
+    exact = q.astype(np.float64) @ X.astype(np.float64)
+    assert np.array_equal(Y.astype(np.float64), exact)
+    del exact
+    say("sp24 full size: float output, every row")
+    F_ref = (Y.astype(np.float32) * (s * np.float32(0.05)).astype(np.float32)[:, None]).astype(np.float32)
+    assert np.array_equal(O.orc_quantized_matmul_rowscale(q[rows], X, s[rows], 0.05).view(np.uint32),
+                          F_ref[rows].view(np.uint32))
+    Fg = W.gemm_i8(X, x_scale=0.05, out="f32")
+    assert np.array_equal(Fg.view(np.uint32), F_ref.view(np.uint32))
+    say("sp24 full size: requantised int8, every row")
+    os_, _ = O.orc_dynamic_params(F_ref)
     Q = W.gemm_i8(X, x_scale=0.05, out="i8", out_scale=float(os_), out_zp=0)
-    assert np.array_equal(Q[rows], O.orc_quantize(F, [os_], [0], O.I8))
+    assert np.array_equal(Q, O.orc_quantize(F_ref, [os_], [0], O.I8))
 
 
 NEG_CARRY = np.float32(np.array([0xBF80C000], np.uint32).view(np.float32)[0])  # bf16 from_float: -inf

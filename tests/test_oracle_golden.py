@@ -143,6 +143,31 @@ def test_qmatmul_golden(golden):
     assert same(O.orc_quantized_matmul_rowscale(g["sp_wq"], g["sp_xq"], rows, 0.05), g["sp_yf"])
 
 
+def test_quantized_matmul_rowscale_distinct_scales():
+    """The per-row form with a different scale on every row: each output is
+    (float)acc * RN(s_row * x_scale) (quant_ops.cpp:435, :456-466), with acc
+    the exact integer accumulator.  A wrong row index for the scale (say row
+    0's on every row, or the transposed operand) fails this: every row's
+    scale is distinct and the accumulators are checked exactly."""
+    rng = np.random.default_rng(31)
+    M, K, N = 37, 300, 23
+    a = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    b = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    s = (rng.random(M) * 0.02 + 1e-3).astype(np.float32)
+    assert len(np.unique(s)) == M
+    acc = a.astype(np.int64) @ b.astype(np.int64)  # exact
+    scale = (s * np.float32(0.05)).astype(np.float32)  # one float32 rounding per row
+    ref = (acc.astype(np.float32) * scale[:, None]).astype(np.float32)
+    got = O.orc_quantized_matmul_rowscale(a, b, s, 0.05)
+    assert same(got, ref)
+    # rows are not interchangeable: swapping two scales changes those rows only
+    s2 = s.copy()
+    s2[[3, 4]] = s2[[4, 3]]
+    got2 = O.orc_quantized_matmul_rowscale(a, b, s2, 0.05)
+    diff = np.nonzero((got2 != got).any(axis=1))[0]
+    assert set(diff) <= {3, 4} and len(diff) > 0
+
+
 def test_bf16_golden(golden):
     g = golden("bf16.npz")
     assert np.array_equal(O.orc_f32_to_bf16(g["x"]), g["bf16"])

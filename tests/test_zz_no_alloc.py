@@ -66,6 +66,45 @@ def test_noalloc_gemm_matches_allocating_entry():
     ctx.close()
 
 
+def test_noalloc_gemm_allocates_nothing():
+    """On a fresh context whose grow-only buffers are still empty, the first
+    call is the allocation-free entry in a form that stages op(A)^T
+    (transA = 0, 1024 x 768: 3 MiB): device free memory is the same before
+    and after it.  Were the staging to go through the context's grow-only
+    buffer instead of the fixed workspace, this call would allocate it.  A
+    warm-up call on another context loads the kernels first."""
+    import torch
+
+    from pyflamert_amd import rocm
+
+    rng = np.random.default_rng(32)
+    K, Nf, Mb = 768, 3072, 1024
+    w = (rng.standard_normal((Nf, K)) * 0.02).astype(np.float32)
+    w[rng.random(w.shape) < 0.8] = 0
+    A = rng.standard_normal((Mb, K)).astype(np.float32)
+    dA = torch.from_numpy(A).cuda()
+    dY = torch.empty((Mb, Nf), dtype=torch.float32, device="cuda")
+    dY2 = torch.empty((Mb, Nf), dtype=torch.float32, device="cuda")
+    warm = rocm.Context(0)
+    BTw = warm.csr_from_dense(w)
+    warm.gemm_csr_dev(dA.data_ptr(), Mb, K, BTw, dY2.data_ptr(), noalloc=True)
+    warm.synchronize()
+    ctx = rocm.Context(0)
+    BT = ctx.csr_from_dense(w)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    say(f"no-alloc Gemm on a fresh context, Mb={Mb} K={K}: device free memory {free0}")
+    ctx.gemm_csr_dev(dA.data_ptr(), Mb, K, BT, dY.data_ptr(), noalloc=True)
+    ctx.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
+    assert bits_equal(dY.cpu().numpy(), dY2.cpu().numpy())
+    for W_, c in ((BT, ctx), (BTw, warm)):
+        W_.free()
+        c.close()
+
+
 def test_noalloc_gemm_rejects_oversize():
     """K * Mb above the workspace is an argument error raised on the host,
     before any kernel is enqueued (the buffers here hold only what a valid
