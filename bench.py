@@ -453,7 +453,7 @@ def cpu_decode_reference(data, shapes):
     return out
 
 
-def bench_decode_int8(ctx, cpu=True):
+def bench_decode_int8(ctx, cpu=True, modes=("fast", "strict"), reps=20):
     """Llama-2-7B-shaped decode linear stack: 32 layers x (4 x 4096x4096,
     2 x 11008x4096, 4096x11008), 70 % sparsity with lognormal (sigma 0.5) row
     lengths, int8 weight-only with per-row scales (dequantisation fused),
@@ -501,7 +501,7 @@ def bench_decode_int8(ctx, cpu=True):
     res = {}
     if cpu:
         res["cpu_reference"] = cpu_decode_reference(data, shapes)
-    for B, mode in ((1, "fast"), (8, "fast"), (1, "strict"), (8, "strict")):
+    for B, mode in [(B, m) for m in ("fast", "strict") if m in modes for B in (1, 8)]:
         bufs = {name: (torch.randn((K_, B), dtype=torch.float32, device="cuda"),
                        torch.empty((M_, B), dtype=torch.float32, device="cuda"))
                 for name, (M_, K_, _) in shapes.items()}
@@ -517,7 +517,6 @@ def bench_decode_int8(ctx, cpu=True):
             step()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
         a.record()
         for _ in range(reps):
             step()
@@ -870,6 +869,11 @@ def main():
     ap.add_argument("--only-sp24", action="store_true", help="time only the 2:4 int8 GEMM (profiler runs)")
     ap.add_argument("--only-sp24-bf16", action="store_true", help="time only the 2:4 bf16 GEMM (profiler runs)")
     ap.add_argument("--only-decode", action="store_true", help="time only the decode linear stack")
+    ap.add_argument("--decode-modes", default="fast,strict",
+                    help="math modes of the decode stack (comma list; profiler runs use fast)")
+    ap.add_argument("--decode-reps", type=int, default=20, help="timed steps of the decode stack per form")
+    ap.add_argument("--only-n", default="",
+                    help="time only these column counts of the 4096 x 4096 SpMM (comma list; profiler runs)")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
                     help="run a copy-like kernel of MIB MiB for counter calibration and exit")
     args = ap.parse_args()
@@ -895,7 +899,8 @@ def main():
         ctx.close()
         return
     if args.only_decode:
-        print(json.dumps({"llama7b_decode_int8_70pct": bench_decode_int8(ctx)}), flush=True)
+        print(json.dumps({"llama7b_decode_int8_70pct": bench_decode_int8(
+            ctx, not args.no_cpu, modes=args.decode_modes.split(","), reps=args.decode_reps)}), flush=True)
         ctx.close()
         return
     if args.only_sp24_bf16:
@@ -909,7 +914,8 @@ def main():
     Xh = workloads.dense_normal((K, N_MAIN), 1.0, seed=2024)
 
     extra = {}
-    if not args.only_main:
+    only_n = [int(v) for v in args.only_n.split(",") if v]
+    if not args.only_main and not only_n:
         # the other workloads first: the headline is timed on a GPU that has
         # been busy (clocks up), with its own warm-up on top
         extra["sp24_i8"] = bench_sp24(ctx, args)
@@ -923,7 +929,7 @@ def main():
         extra["N256_host_entry"] = time_host_entry(ctx, ip, ix, v, Xh)
 
     results = {}
-    for N in ((N_MAIN,) if args.only_main else (64, 1, N_MAIN)):
+    for N in (only_n or ((N_MAIN,) if args.only_main else (64, 1, N_MAIN))):
         sets = []
         for s in range(N_SETS):
             W = ctx.csr_upload(M, K, ip, ix, v)
@@ -932,7 +938,7 @@ def main():
             sets.append((W, dX, dY))
         torch.cuda.synchronize()
         steps = args.steps if N == N_MAIN else max(200, args.steps // 4)
-        if N == N_MAIN and args.mode == "strict" and not args.only_main:
+        if N == N_MAIN and args.mode == "strict" and not args.only_main and not only_n:
             # the fused multiply-add form of the same product (within 1e-5
             # normwise of the strict result, the fp32 tolerance)
             msf = time_gpu(sets, N, max(200, steps // 4), args.warmup, "fast")
@@ -952,7 +958,7 @@ def main():
             "bound": "fp32 compute" if N == N_MAIN else "hbm",
         }
         log(f"N={N}: {ms * 1e3:.2f} us/launch  {extra[f'N{N}']}")
-        if N == N_MAIN and args.mode == "strict" and not args.only_main:
+        if N == N_MAIN and args.mode == "strict" and not args.only_main and not only_n:
             err = float(np.abs(Yf - Y0).max() / np.abs(Y0).max())
             extra[f"N{N}_fast"] = {
                 "ms_per_launch": round(msf, 5),
@@ -967,6 +973,10 @@ def main():
         del sets
         torch.cuda.empty_cache()
 
+    if N_MAIN not in results:  # a profiler run of other column counts
+        print(json.dumps({"spmm_4096x4096": extra, "mode": args.mode}), flush=True)
+        ctx.close()
+        return
     ms, Y0, steps = results[N_MAIN]
     byts = csr_bytes(nnz, M, K, N_MAIN)
     flops = 2.0 * nnz * N_MAIN
