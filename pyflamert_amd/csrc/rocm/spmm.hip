@@ -1287,6 +1287,8 @@ void launch_merge(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, f
 #undef PFR_MERGE
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 // Fast 2 <= N <= 8 over the nnz-balanced copy: a workgroup takes groups b
 // and b + gridDim.x (the copy holds at most two per CU), waves 0..7 the first
 // and 8..15 the second, and walks K chunk by chunk: the chunk's X rows are
@@ -2024,7 +2026,6 @@ __global__ __launch_bounds__((sell_threads<XVEC, W, XT>())) void k_spmm_sell(
     }
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int next_pow2(int n) {
     int p = 1;

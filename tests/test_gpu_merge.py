@@ -97,9 +97,13 @@ KINDS = ["empty_runs", "one_long_row", "full_rows", "tiny", "short_rows", "recor
          "lognormal"]
 
 
+@pytest.mark.parametrize("N", [1, 2, 3, 8])
 @pytest.mark.parametrize("int8", [False, True])
 @pytest.mark.parametrize("kind", KINDS)
-def test_merge_spmv_edge_shapes(ctx, kind, int8):
+def test_merge_spmv_edge_shapes(ctx, kind, int8, N):
+    """N = 1: the merge-path kernel; N = 2, 3, 8: the fast kernels for few
+    columns over the same weights (nnz-balanced or row kernels), on the same
+    skewed shapes."""
     rng = np.random.default_rng(2 * KINDS.index(kind) + int(int8))
     M, K, lens = shape_case(kind, rng)
     ip, ix, v = csr_from_lengths(lens, K, rng)
@@ -111,8 +115,8 @@ def test_merge_spmv_edge_shapes(ctx, kind, int8):
     else:
         W = ctx.csr_upload(M, K, ip, ix, v)
         vals = v
-    x = rng.standard_normal(K).astype(np.float32)
-    say(f"merge spmv {kind} int8={int8} M={M} K={K} nnz={len(ix)}")
+    x = rng.standard_normal((K, N) if N > 1 else K).astype(np.float32)
+    say(f"merge spmv {kind} int8={int8} M={M} K={K} nnz={len(ix)} N={N}")
     Y = W.spmm(x, mode="fast")
     R = O.orc_csr_spmm(M, K, ip, ix, vals, x)
     assert close_normwise(Y, R), kind
@@ -124,8 +128,8 @@ def test_merge_spmv_edge_shapes(ctx, kind, int8):
     # NaN and -inf in x propagate to the rows that use them, cut or not
     xb = x.copy()
     if len(ix):
-        xb[ix[len(ix) // 2]] = np.nan
-        xb[ix[-1]] = -np.inf
+        xb[ix[len(ix) // 2], ...] = np.nan
+        xb[ix[-1], ...] = -np.inf
     Y = W.spmm(xb, mode="fast")
     R = O.orc_csr_spmm(M, K, ip, ix, vals, xb)
     assert close_normwise(Y, R), (kind, "non-finite x")
