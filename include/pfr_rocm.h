@@ -146,6 +146,20 @@ int pfr_csr_from_dense_dev(pfr_ctx* ctx, const float* dense, int64_t rows,
  * finite activations results are unchanged.  Idempotent. */
 int pfr_csr_dense_semantics(pfr_csr* w);
 int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz);
+/* Device bytes the handle holds: the CSR itself (row pointers, columns as
+ * uint16 when K <= 65536 and int32 otherwise, values, row scales), the
+ * row-block table, the merge-path partition and every derived copy built so
+ * far.  The sliced-ELL copy (float32 weights, N >= 16), the row-chain copy
+ * (strict, N <= 8) and the nnz-balanced copy (fast, N <= 8) are built by the
+ * first product through the handle that would use one: that call plans on
+ * the host, allocates, fills on the device and synchronizes the handle's
+ * stream.  While that stream is being captured into a graph, and in
+ * pfr_gemm_csr_act_noalloc_dev, nothing is built and a product without its
+ * copy runs a kernel that reads the CSR in place (same results in strict
+ * mode, the fast mode's own rounding otherwise), so run each kind of
+ * product once before capture.  No counterpart in the reference (its
+ * weights are host memory); for footprint reports. */
+int pfr_csr_device_bytes(const pfr_csr* w, int64_t* bytes);
 int pfr_csr_free(pfr_csr* w);
 
 /* ---- CSR products --------------------------------------------------------- */
@@ -196,7 +210,11 @@ int pfr_gemm_csr_act_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K,
 /* Allocation-free form of pfr_gemm_csr_act_dev.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments, results and errors, except that the copy of
+ * hipMalloc).  Same arguments, results and errors, except that it builds
+ * none of the handle's derived copies (see pfr_csr_device_bytes): a product
+ * whose copy the handle does not hold yet runs a kernel that reads the CSR
+ * in place (bit-identical in strict mode, the fast mode's own rounding
+ * otherwise), and that the copy of
  * op(A)^T that the product reads (made when transA == 0 or alpha != 1) is
  * staged in a fixed per-device workspace of 4,194,304 floats (16 MiB)
  * instead of the context's grow-only buffer; K * Mb beyond that is

@@ -61,6 +61,7 @@ SIGNATURES = {
     "pfr_apply_mask": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_apply_mask_dev": (_INT, [_P, _P, _P, _I64, _P]),
     "pfr_csr_info": (_INT, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64)]),
+    "pfr_csr_device_bytes": (_INT, [_P, C.POINTER(_I64)]),
     "pfr_csr_free": (_INT, [_P]),
     "pfr_spmm_csr": (_INT, [_P, _P, _P, _I64, _P, _INT]),
     "pfr_spmm_csr_dev": (_INT, [_P, _P, _P, _I64, _I64, _P, _I64, _INT]),

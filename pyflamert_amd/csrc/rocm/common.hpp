@@ -4,9 +4,12 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "pfr_rocm.h"
 
@@ -123,9 +126,12 @@ struct pfr_csr {
     pfr_ctx* ctx = nullptr;
     int64_t M = 0, K = 0, nnz = 0;
     int32_t* rowptr = nullptr;  // [M+1]
-    int32_t* col = nullptr;     // [nnz], ascending within a row
-    uint16_t* col16 = nullptr;  // [nnz] the same columns as uint16 when K <= 65536 (fast vector kernel)
-    void* val = nullptr;        // [nnz] float or int8
+    // The columns in storage order, in one of two widths: col16 when K <=
+    // 65536 (col is then null), else col.  col16 and val are padded to whole
+    // records of four and one spare record (value 0, column K); see mp_wave.
+    int32_t* col = nullptr;     // [nnz] when K > 65536
+    uint16_t* col16 = nullptr;  // [nnz padded] when K <= 65536
+    void* val = nullptr;        // [nnz padded] float or int8
     pfr_dtype vdt = PFR_F32;
     float* row_scale = nullptr;  // [M] for int8 values
     // Row blocks for the vector (N == 1) kernel: each block is a run of
@@ -221,6 +227,17 @@ struct pfr_csr {
     // or NaN activation meets a weight the CSR does not store (a zero).
     uint64_t* pattern = nullptr;
     int64_t pattern_nw = 0;
+    // The sliced-ELL, row-chain and balanced copies are built on the first
+    // product that would use them (pfr::csr_build_copies): `pending` holds
+    // the pfr::kCopy* bits of those still to build, and the host keeps what
+    // their plans need -- the row pointers and the per-row counts of each
+    // copy's column chunks (M x a few integers; empty when that copy is not
+    // wanted).  Freed when nothing is pending.
+    std::atomic<uint32_t> pending{0};
+    std::mutex lazy_mu;
+    std::vector<int32_t> h_rowptr, h_sell_cnt, h_bal_cnt;
+    // Device bytes the handle holds (every array above).
+    int64_t dev_bytes = 0;
 };
 
 namespace pfr {
@@ -240,6 +257,13 @@ constexpr int kMergeMaxK = 16383;  // x staged in LDS with its zero slot: (K + 1
 namespace pfr {
 // Makes ctx's device current (cheap when it already is).
 void bind(pfr_ctx* ctx);
+// Derived copies of a CSR weight, built on first use.
+constexpr uint32_t kCopySell = 1, kCopyChain = 2, kCopyBal = 4;
+// Builds the copies among `which` that w still has pending, on w's context
+// stream (allocates, plans on the host and fills on the device, then
+// synchronizes).  A copy whose plan does not fit is dropped from pending and
+// its products keep the kernels that read the CSR in place.
+void csr_build_copies(pfr_csr* w, uint32_t which);
 // out[i] = w[i] * mask[i] on stream s (apply_mask); out may alias w.
 void apply_mask_dev(hipStream_t s, const float* w, const float* mask, int64_t n, float* out);
 // Records, once per device, the workspace address of the allocation-free

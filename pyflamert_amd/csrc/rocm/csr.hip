@@ -1,7 +1,8 @@
 // Device-resident CSR weights: upload from the reference's SparseTensor
 // arrays or from a dense zero-filled pruned weight, with the range checks the
-// reference leaves out, the row-block table used by the vector kernel and the
-// sliced-ELL copy used by the column-slice kernel.
+// reference leaves out, and the derived copies the product kernels read (the
+// row-block table and merge-path partition at build, the sliced-ELL,
+// row-chain and balanced copies on first use).
 #include <algorithm>
 #include <climits>
 #include <cstring>
@@ -50,6 +51,21 @@ void fill_dev(T* p, int64_t n, T v, hipStream_t s) {
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
     PFR_HIP(hipGetLastError());
+}
+
+// Allocations a handle keeps, counted in its dev_bytes.
+template <class T>
+T* walloc(pfr_csr* w, int64_t count) {
+    T* p = dev_alloc<T>(count);
+    w->dev_bytes += (int64_t)sizeof(T) * (count > 0 ? count : 1);
+    return p;
+}
+
+template <class T>
+T* walloc_copy(pfr_csr* w, const T* host, int64_t count, hipStream_t s) {
+    T* p = dev_alloc_copy(host, count, s);
+    w->dev_bytes += (int64_t)sizeof(T) * (count > 0 ? count : 1);
+    return p;
 }
 
 void free_csr(pfr_csr* w) {
@@ -174,10 +190,11 @@ std::vector<int64_t> sell_place(const std::vector<int64_t>& steps, int64_t nslab
 // ---- Derived copies ---------------------------------------------------------
 // Each derived copy is planned from per-row (per-chunk) nonzero counts alone:
 // row order, slab or group shapes and run offsets.  The upload path counts
-// on the host and fills on the host; the build from a dense device weight
-// counts on the device, plans on the host from the counts it copies back
-// (M x a few integers) and fills on the device, so the nonzeros never leave
-// the GPU and both paths give the same layout.
+// on the host, the build from a dense device weight on the device (copying
+// back M x a few integers); either keeps the counts, and the first product
+// that would use a copy plans it on the host and fills it on the device from
+// the resident CSR, so both paths give the same layout and a weight holds
+// only the copies its products use.
 
 // Chunking of the sliced-ELL copy: chunks of whole 16-row LDS loads (the
 // staging of a chunk never reaches the zero row that follows it).
@@ -241,56 +258,13 @@ void set_sell(pfr_csr* w, const SellPlan& p, hipStream_t s) {
     for (int64_t sl = 0; sl < p.nslab; ++sl)
         for (int64_t c = 0; c <= p.nch; ++c)  // c == nch: end of the slab's last run
             soff[(size_t)(sl * (p.nch + 1) + c)] = (int32_t)p.off[(size_t)(sl * p.nch + c)];
-    w->sell_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
-    w->sell_soff = dev_alloc_copy(soff.data(), (int64_t)soff.size(), s);
+    w->sell_perm = walloc_copy(w, p.perm.data(), (int64_t)p.perm.size(), s);
+    w->sell_soff = walloc_copy(w, soff.data(), (int64_t)soff.size(), s);
     w->sell_nslab = (int32_t)p.nslab;
     w->sell_nch = (int32_t)p.nch;
     w->sell_kc = (int32_t)p.kc;
     w->sell_len = p.len;
     PFR_HIP(hipStreamSynchronize(s));  // soff goes out of scope
-}
-
-// Sliced-ELL copy (layout described at pfr_csr::sell_blk).  Each row keeps
-// its storage order inside a chunk and chunks are visited in order, so the
-// copy needs the chunk index to be non-decreasing along every row (always
-// true for one chunk, and for ascending columns).  Rows are ordered by
-// sell_order.
-void build_sell(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
-                const float* vals, hipStream_t s) {
-    const int64_t M = w->M, K = w->K;
-    if (!sell_wanted(M, K, w->nnz)) return;
-    int64_t kc, nch;
-    sell_geom(K, &kc, &nch);
-    for (int64_t r = 0; r < M; ++r)
-        for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
-            if (col[j] / kc < col[j - 1] / kc) return;
-    std::vector<int32_t> cnt((size_t)(M * nch), 0);
-    for (int64_t r = 0; r < M; ++r)
-        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cnt[(size_t)(r * nch + col[j] / kc)];
-    SellPlan p;
-    if (!plan_sell(M, K, cnt, &p)) return;
-    const int64_t R = pfr::kSellRows;
-    const int32_t pad_off = (int32_t)(kc * 64);
-    std::vector<int4> blk((size_t)(p.len + pfr::kSellTail));
-    for (auto& b : blk) b = make_int4(pad_off, 0, pad_off, 0);
-    std::vector<int32_t> t((size_t)nch);
-    for (int64_t i = 0; i < p.nslab * R; ++i) {
-        const int32_t row = p.perm[(size_t)i];
-        if (row < 0) continue;  // the lanes of a partial slab past its rows
-        const int64_t sl = i / R, r = i % R;
-        std::fill(t.begin(), t.end(), 0);
-        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
-            const int64_t c = col[j] / kc;
-            const int32_t step = t[(size_t)c]++;
-            int4& b = blk[(size_t)(p.off[(size_t)(sl * nch + c)] + (step / 8) * 64 + 4 * r + (step % 8) / 2)];
-            int32_t bits;
-            std::memcpy(&bits, &vals[j], 4);
-            const int32_t o = (int32_t)((col[j] - c * kc) * 64);
-            if (step % 2 == 0) { b.x = o; b.y = bits; } else { b.z = o; b.w = bits; }
-        }
-    }
-    w->sell_blk = dev_alloc_copy(blk.data(), (int64_t)blk.size(), s);
-    set_sell(w, p, s);  // synchronizes: blk outlives the upload
 }
 
 // Rows sorted by count, longest first, ties by row index (the row order of
@@ -345,58 +319,14 @@ bool plan_chain(const pfr_csr* w, const std::vector<int32_t>& len, ChainPlan* p)
 
 // Uploads the plan's tables (chain_val / chain_col are set by the fill).
 void set_chain(pfr_csr* w, const ChainPlan& p, hipStream_t s) {
-    w->chain_len = dev_alloc_copy(p.len.data(), (int64_t)p.len.size(), s);
-    w->chain_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
-    w->chain_q0 = dev_alloc_copy(p.q0.data(), (int64_t)p.q0.size(), s);
+    w->chain_len = walloc_copy(w, p.len.data(), (int64_t)p.len.size(), s);
+    w->chain_perm = walloc_copy(w, p.perm.data(), (int64_t)p.perm.size(), s);
+    w->chain_q0 = walloc_copy(w, p.q0.data(), (int64_t)p.q0.size(), s);
     w->chain_rows = (int32_t)p.R;
     w->chain_nslab = (int32_t)p.nslab;
     w->chain_xlds = p.xlds;
     w->chain_c16 = p.c16;
     PFR_HIP(hipStreamSynchronize(s));
-}
-
-// Row-chain copy (layout described at pfr_csr::chain_q0), filled on the host.
-template <class V, class C>
-void fill_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
-                const ChainPlan& p, hipStream_t s) {
-    const int64_t R = p.R, nrec = (int64_t)p.q0.back() * R;
-    // staged-x form: byte offsets into the LDS copy of x, padding at its zero
-    // slot K; otherwise column indices, padding at column 0.  One spare quad
-    // row of padding after the last slab: the kernels' clamped loads may
-    // touch it.
-    const int64_t mul = p.xlds ? 4 : 1;
-    std::vector<V> v((size_t)((nrec + R) * 4), V(0));
-    std::vector<C> c((size_t)((nrec + R) * 4), C(p.xlds ? w->K * 4 : 0));
-    for (int64_t i = 0; i < w->M; ++i) {
-        const int32_t row = p.perm[(size_t)i];
-        const int64_t sl = i / R, lane = i % R;
-        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
-            const int64_t step = j - rowptr[row];
-            const size_t at = (size_t)((((int64_t)p.q0[(size_t)sl] + step / 4) * R + lane) * 4 + step % 4);
-            v[at] = vals[j];
-            c[at] = (C)(col[j] * mul);
-        }
-    }
-    w->chain_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
-    w->chain_col = dev_alloc_copy(c.data(), (int64_t)c.size(), s);
-    set_chain(w, p, s);  // synchronizes: v and c outlive the uploads
-}
-
-void build_chain(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col,
-                 const void* vals, hipStream_t s) {
-    const int64_t M = w->M;
-    if (M == 0 || w->nnz == 0) return;
-    std::vector<int32_t> len((size_t)M);
-    for (int64_t r = 0; r < M; ++r) len[(size_t)r] = rowptr[r + 1] - rowptr[r];
-    ChainPlan p;
-    if (!plan_chain(w, len, &p)) return;  // keep the block kernels
-    if (w->vdt == PFR_F32) {
-        if (p.c16) fill_chain<float, uint16_t>(w, rowptr, col, static_cast<const float*>(vals), p, s);
-        else fill_chain<float, int32_t>(w, rowptr, col, static_cast<const float*>(vals), p, s);
-    } else {
-        if (p.c16) fill_chain<int8_t, uint16_t>(w, rowptr, col, static_cast<const int8_t*>(vals), p, s);
-        else fill_chain<int8_t, int32_t>(w, rowptr, col, static_cast<const int8_t*>(vals), p, s);
-    }
 }
 
 // Chunking of the balanced copy: C chunks of kcw columns; false when the
@@ -496,56 +426,13 @@ bool plan_bal(const pfr_csr* w, const std::vector<int32_t>& len, const std::vect
 
 // Uploads the plan's tables (bal_val / bal_col are set by the fill).
 void set_bal(pfr_csr* w, const BalPlan& p, hipStream_t s) {
-    w->bal_meta = dev_alloc_copy(p.meta.data(), p.G, s);
-    w->bal_cmeta = dev_alloc_copy(p.cmeta.data(), p.G * p.C, s);
-    w->bal_perm = dev_alloc_copy(p.perm.data(), (int64_t)p.perm.size(), s);
+    w->bal_meta = walloc_copy(w, p.meta.data(), p.G, s);
+    w->bal_cmeta = walloc_copy(w, p.cmeta.data(), p.G * p.C, s);
+    w->bal_perm = walloc_copy(w, p.perm.data(), (int64_t)p.perm.size(), s);
     w->bal_ngroup = (int32_t)p.G;
     w->bal_nchunk = (int32_t)p.C;
     w->bal_kcw = (int32_t)p.kcw;
     PFR_HIP(hipStreamSynchronize(s));
-}
-
-// nnz-balanced copy, filled on the host.
-template <class V>
-void build_bal(pfr_csr* w, const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, const V* vals,
-               hipStream_t s) {
-    const int64_t M = w->M;
-    int64_t C, kcw;
-    if (M == 0 || w->nnz == 0 || !bal_geom(w->K, &C, &kcw)) return;
-    std::vector<int32_t> len((size_t)M), cntc((size_t)(M * C), 0);
-    for (int64_t r = 0; r < M; ++r) {
-        len[(size_t)r] = rowptr[r + 1] - rowptr[r];
-        for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cntc[(size_t)(r * C + col[j] / kcw)];
-    }
-    BalPlan p;
-    if (!plan_bal(w, len, cntc, &p)) return;
-    // one spare record per lane after the last group
-    std::vector<V> v((size_t)((p.nrec + 64) * 4), V(0));
-    std::vector<uint16_t> cidx((size_t)((p.nrec + 64) * 4), (uint16_t)(4 * kcw));  // chunk 0's zero
-    for (int64_t g = 0; g < p.G; ++g) {
-        const int64_t R = int64_t(1) << p.meta[(size_t)g].x;
-        for (int64_t c = 0; c < C; ++c) {
-            const int2 cm = p.cmeta[(size_t)(g * C + c)];
-            for (int64_t e = (int64_t)cm.x * 4; e < ((int64_t)cm.x + R * cm.y) * 4; ++e)
-                cidx[(size_t)e] = (uint16_t)(4 * (c * (kcw + 1) + kcw));  // padding: this chunk's zero
-        }
-    }
-    std::vector<int32_t> k_in((size_t)C);
-    for (int64_t i = 0; i < M; ++i) {
-        const int64_t g = p.gpos[(size_t)i];
-        const int64_t R = int64_t(1) << p.meta[(size_t)g].x, lane = i - p.meta[(size_t)g].y;
-        const int32_t row = p.perm[(size_t)i];
-        std::fill(k_in.begin(), k_in.end(), 0);
-        for (int32_t j = rowptr[row]; j < rowptr[row + 1]; ++j) {
-            const int64_t c = col[j] / kcw, k = k_in[(size_t)c]++;
-            const size_t at = (size_t)(((p.cmeta[(size_t)(g * C + c)].x + (k / 4) * R + lane) * 4) + k % 4);
-            v[at] = vals[j];
-            cidx[at] = (uint16_t)(4 * (c * (kcw + 1) + col[j] - c * kcw));
-        }
-    }
-    w->bal_val = dev_alloc_copy(v.data(), (int64_t)v.size(), s);
-    w->bal_col = dev_alloc_copy(cidx.data(), (int64_t)cidx.size(), s);
-    set_bal(w, p, s);  // synchronizes: v and cidx outlive the uploads
 }
 
 // Merge-path partition (layout at pfr_csr::mp_wave) of the CSR with row
@@ -681,79 +568,18 @@ bool set_merge(pfr_csr* w, const std::vector<int32_t>& rowptr, hipStream_t s) {
             wm[(size_t)(p * W + t)] = m;
         }
     }
-    w->mp_wave = dev_alloc_copy(wp.data(), Q + 1, s);
-    w->mp_wmeta = dev_alloc_copy(wm.data(), Q, s);
-    w->mp_grp = dev_alloc_copy(gp.data(), P, s);
-    w->mp_xchg = dev_alloc<unsigned long long>(P);
+    w->mp_wave = walloc_copy(w, wp.data(), Q + 1, s);
+    w->mp_wmeta = walloc_copy(w, wm.data(), Q, s);
+    w->mp_grp = walloc_copy(w, gp.data(), P, s);
+    w->mp_xchg = walloc<unsigned long long>(w, P);
     fill_dev(w->mp_xchg, P, 0ull, s);
-    w->mp_carry = dev_alloc<float>(2 * P);
-    w->mp_cnt = dev_alloc<uint32_t>(P);
+    w->mp_carry = walloc<float>(w, 2 * P);
+    w->mp_cnt = walloc<uint32_t>(w, P);
     fill_dev(w->mp_cnt, P, 0u, s);
     w->mp_groups = (int32_t)P;
     PFR_HIP(hipStreamSynchronize(s));  // wp and gp outlive the uploads
     return true;
 }
-
-pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
-               const std::vector<int32_t>& col, const void* vals, pfr_dtype vdt,
-               const float* row_scales) {
-    auto* w = new pfr_csr();
-    try {
-        w->ctx = ctx;
-        w->M = M;
-        w->K = K;
-        w->nnz = rowptr[M];
-        w->vdt = vdt;
-        int32_t mx = 0;
-        for (int64_t r = 0; r < M; ++r) mx = std::max(mx, rowptr[r + 1] - rowptr[r]);
-        w->max_row_nnz = mx;
-        hipStream_t s = ctx->stream;
-        w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
-        w->col = dev_alloc_copy(col.data(), w->nnz, s);
-        // col16 and val hold whole records of four and one spare record;
-        // padding entries are value 0 at column K (x's zero slot in the
-        // merge-path kernels, which read whole records and point loads past
-        // a share at the spare one)
-        const int64_t npad = (w->nnz + 3) / 4 * 4 + 4;
-        if (K <= 65536 && w->nnz > 0) {
-            std::vector<uint16_t> c16(col.begin(), col.end());
-            c16.resize((size_t)npad, (uint16_t)std::min<int64_t>(K, 65535));
-            w->col16 = dev_alloc_copy(c16.data(), npad, s);
-            PFR_HIP(hipStreamSynchronize(s));  // c16 goes out of scope
-        }
-        if (vdt == PFR_F32) {
-            std::vector<float> v(static_cast<const float*>(vals), static_cast<const float*>(vals) + w->nnz);
-            v.resize((size_t)npad, 0.0f);
-            w->val = dev_alloc_copy(v.data(), npad, s);
-            PFR_HIP(hipStreamSynchronize(s));
-        } else {
-            std::vector<int8_t> v(static_cast<const int8_t*>(vals), static_cast<const int8_t*>(vals) + w->nnz);
-            v.resize((size_t)npad, 0);
-            w->val = dev_alloc_copy(v.data(), npad, s);
-            PFR_HIP(hipStreamSynchronize(s));
-        }
-        if (row_scales) w->row_scale = dev_alloc_copy(row_scales, M, s);
-        std::vector<int32_t> blocks = spmv_blocks(rowptr, M);
-        w->n_spmv_blocks = (int64_t)blocks.size() - 1;
-        w->spmv_blocks = dev_alloc_copy(blocks.data(), (int64_t)blocks.size(), s);
-        bool sorted = true;
-        for (int64_t r = 0; r < M && sorted; ++r)
-            for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
-                if (col[j] <= col[j - 1]) { sorted = false; break; }
-        w->cols_sorted = sorted;
-        if (vdt == PFR_F32) build_sell(w, rowptr, col, static_cast<const float*>(vals), s);
-        build_chain(w, rowptr, col, vals, s);
-        if (vdt == PFR_F32) build_bal(w, rowptr, col, static_cast<const float*>(vals), s);
-        else build_bal(w, rowptr, col, static_cast<const int8_t*>(vals), s);
-        set_merge(w, rowptr, s);
-        PFR_HIP(hipStreamSynchronize(s));
-        return w;
-    } catch (...) {
-        free_csr(w);
-        throw;
-    }
-}
-
 
 // ---- Build from a dense device weight ----------------------------------------
 
@@ -836,8 +662,8 @@ __global__ __launch_bounds__(256) void k_dense_count(const float* __restrict__ D
 }
 
 // One workgroup per row of D: the kept entries in ascending column order at
-// rowptr[r] onward (the order to_sparse emits), as int32 (and, when col16 is
-// given, uint16) columns and float values.
+// rowptr[r] onward (the order to_sparse emits), as float values and the
+// columns as int32 (col) or uint16 (col16), whichever is given.
 __global__ __launch_bounds__(256) void k_dense_compact(const float* __restrict__ D, int64_t K, float thr,
                                                        const int32_t* __restrict__ rowptr, int32_t* __restrict__ col,
                                                        uint16_t* __restrict__ col16, float* __restrict__ val) {
@@ -860,8 +686,8 @@ __global__ __launch_bounds__(256) void k_dense_compact(const float* __restrict__
         }
         if (f) {
             const int j = off + (int)__popcll(m & ((uint64_t(1) << lane) - 1));
-            col[j] = (int32_t)k;
             val[j] = v;
+            if (col) col[j] = (int32_t)k;
             if (col16) col16[j] = (uint16_t)k;
         }
         base += total;
@@ -869,11 +695,14 @@ __global__ __launch_bounds__(256) void k_dense_compact(const float* __restrict__
     }
 }
 
-// First index in [lo, hi) of the ascending columns col[] that is >= t.
-__device__ __forceinline__ int32_t first_at_least(const int32_t* __restrict__ col, int32_t lo, int32_t hi, int32_t t) {
+// First index in [lo, hi) whose column is >= t, where t starts a chunk of
+// columns and the chunk index (column / chunk width) does not decrease over
+// [lo, hi) (ascending columns are one such case).
+template <class CI>
+__device__ __forceinline__ int32_t first_at_least(const CI* __restrict__ col, int32_t lo, int32_t hi, int32_t t) {
     while (lo < hi) {
         const int32_t mid = lo + (hi - lo) / 2;
-        if (col[mid] < t) lo = mid + 1;
+        if ((int32_t)col[mid] < t) lo = mid + 1;
         else hi = mid;
     }
     return lo;
@@ -881,10 +710,12 @@ __device__ __forceinline__ int32_t first_at_least(const int32_t* __restrict__ co
 
 // Sliced-ELL fill, one wave per slab position i (row perm[i], slab i / 16,
 // lane i % 16; -1 for the lanes of a partial slab past its rows): entry j
-// of chunk c is that chunk's step j - (the row's first entry in c), as
-// build_sell places it.  blk holds the padding pattern.
+// of chunk c is that chunk's step j - (the row's first entry in c); step t
+// of slab lane r in chunk c is int4 t / 8 * 64 + 4 r + t % 8 / 2 of the
+// (slab, chunk) run, its half t % 2.  blk holds the padding pattern.
+template <class CI>
 __global__ __launch_bounds__(256) void k_sell_fill(int64_t npos, const int32_t* __restrict__ perm,
-                                                   const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+                                                   const int32_t* __restrict__ rowptr, const CI* __restrict__ col,
                                                    const float* __restrict__ val, const int64_t* __restrict__ off,
                                                    int nch, int kc, int4* __restrict__ blk) {
     const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -895,7 +726,7 @@ __global__ __launch_bounds__(256) void k_sell_fill(int64_t npos, const int32_t* 
     const int32_t b = rowptr[row], e = rowptr[row + 1];
     const int64_t sl = i / pfr::kSellRows, r = i % pfr::kSellRows;
     for (int32_t j = b + lane; j < e; j += 64) {
-        const int32_t k = col[j], c = k / kc;
+        const int32_t k = (int32_t)col[j], c = k / kc;
         const int32_t step = j - first_at_least(col, b, j, c * kc);
         int32_t* q = reinterpret_cast<int32_t*>(blk + off[sl * nch + c] + (step / 8) * 64 + 4 * r + (step % 8) / 2) +
                      (step % 2) * 2;
@@ -905,12 +736,14 @@ __global__ __launch_bounds__(256) void k_sell_fill(int64_t npos, const int32_t* 
 }
 
 // Row-chain fill, one wave per sorted position i (row perm[i], slab i / R,
-// lane i % R), as fill_chain places the entries; v and c hold the padding.
-template <class C>
+// lane i % R): step t of the row goes to entry t % 4 of quad row
+// q0[slab] + t / 4, lane i % R, with its column times mul (4: byte offsets
+// into staged x); v and c hold the padding.
+template <class CI, class V, class CO>
 __global__ __launch_bounds__(256) void k_chain_fill(int64_t M, int R, const int32_t* __restrict__ perm,
                                                     const int32_t* __restrict__ q0, const int32_t* __restrict__ rowptr,
-                                                    const int32_t* __restrict__ col, const float* __restrict__ val,
-                                                    int mul, float* __restrict__ v, C* __restrict__ c) {
+                                                    const CI* __restrict__ col, const V* __restrict__ val,
+                                                    int mul, V* __restrict__ v, CO* __restrict__ c) {
     const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= M) return;
     const int lane = threadIdx.x & 63;
@@ -920,7 +753,7 @@ __global__ __launch_bounds__(256) void k_chain_fill(int64_t M, int R, const int3
         const int64_t step = j - b;
         const int64_t at = ((q + step / 4) * R + ln) * 4 + step % 4;
         v[at] = val[j];
-        c[at] = (C)(col[j] * mul);
+        c[at] = (CO)((int32_t)col[j] * mul);
     }
 }
 
@@ -938,12 +771,15 @@ __global__ __launch_bounds__(256) void k_bal_pad(int C, int kcw, const int4* __r
 
 // Balanced fill, one wave per sorted position i (group gpos[i], lane i minus
 // the group's first position): entry j is entry k of its row in chunk c, k
-// counted from the row's first entry in c, placed as build_bal places it.
+// counted from the row's first entry in c, goes to entry k % 4 of record
+// cmeta[g, c].x + k / 4 * R + lane with the byte offset of its column in
+// the staged chunk.
+template <class CI, class V>
 __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, const int4* __restrict__ meta,
                                                   const int2* __restrict__ cmeta, const int32_t* __restrict__ perm,
                                                   const int32_t* __restrict__ gpos, const int32_t* __restrict__ rowptr,
-                                                  const int32_t* __restrict__ col, const float* __restrict__ val,
-                                                  float* __restrict__ v, uint16_t* __restrict__ cidx) {
+                                                  const CI* __restrict__ col, const V* __restrict__ val,
+                                                  V* __restrict__ v, uint16_t* __restrict__ cidx) {
     const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= M) return;
     const int lane = threadIdx.x & 63;
@@ -952,7 +788,7 @@ __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, con
     const int64_t R = int64_t(1) << m.x, ln = i - m.y;
     const int32_t row = perm[i], b = rowptr[row], e = rowptr[row + 1];
     for (int32_t j = b + lane; j < e; j += 64) {
-        const int32_t kk = col[j], c = kk / kcw;
+        const int32_t kk = (int32_t)col[j], c = kk / kcw;
         const int64_t k = j - first_at_least(col, b, j, c * kcw);
         const int64_t at = ((cmeta[g * C + c].x + (k / 4) * R + ln) * 4) + k % 4;
         v[at] = val[j];
@@ -962,26 +798,245 @@ __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, con
 
 unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
 
-// The CSR handle of D (M x K, row-major, device), with every derived copy
-// the upload path would build, from counts copied back to the host and
-// fills on the device.
 // Stored-entry bitmap: one wave per row sets the bit of every stored column.
+template <class CI>
 __global__ __launch_bounds__(256) void k_pattern(int64_t M, const int32_t* __restrict__ rowptr,
-                                                 const int32_t* __restrict__ col, int64_t nw,
+                                                 const CI* __restrict__ col, int64_t nw,
                                                  unsigned long long* __restrict__ bm) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= M) return;
     for (int32_t j = rowptr[r] + (int32_t)(threadIdx.x & 63); j < rowptr[r + 1]; j += 64) {
-        const int32_t k = col[j];
+        const int32_t k = (int32_t)col[j];
         atomicOr(&bm[r * nw + k / 64], 1ull << (k % 64));
     }
 }
 
+// ---- Copies built on first use ----------------------------------------------
+
+// Each row's chunk index (column / width) does not decrease along it, which
+// the chunked copies' fills rely on (always true for ascending columns).
+bool chunks_ascend(const std::vector<int32_t>& rowptr, const std::vector<int32_t>& col, int64_t M, int64_t width) {
+    for (int64_t r = 0; r < M; ++r)
+        for (int32_t j = rowptr[(size_t)r] + 1; j < rowptr[(size_t)r + 1]; ++j)
+            if (col[(size_t)j] / width < col[(size_t)j - 1] / width) return false;
+    return true;
+}
+
+// Keeps what the copies' plans need on the host and marks the copies
+// pending: the row-chain copy always, the sliced-ELL and balanced copies
+// where their per-row chunk counts are given.
+void set_lazy(pfr_csr* w, const std::vector<int32_t>& rowptr, std::vector<int32_t> sell_cnt,
+              std::vector<int32_t> bal_cnt) {
+    uint32_t bits = 0;
+    if (w->M > 0 && w->nnz > 0) {
+        bits = pfr::kCopyChain | (sell_cnt.empty() ? 0u : pfr::kCopySell) | (bal_cnt.empty() ? 0u : pfr::kCopyBal);
+        w->h_rowptr = rowptr;
+        w->h_sell_cnt = std::move(sell_cnt);
+        w->h_bal_cnt = std::move(bal_cnt);
+    }
+    w->pending.store(bits, std::memory_order_release);
+}
+
+std::vector<int32_t> row_lengths(const pfr_csr* w) {
+    std::vector<int32_t> len((size_t)w->M);
+    for (int64_t r = 0; r < w->M; ++r) len[(size_t)r] = w->h_rowptr[(size_t)r + 1] - w->h_rowptr[(size_t)r];
+    return len;
+}
+
+// Sliced-ELL copy (float32 values), planned from the kept chunk counts.
+template <class CI>
+void fill_sell(pfr_csr* w, const CI* col, hipStream_t s) {
+    SellPlan p;
+    if (!plan_sell(w->M, w->K, w->h_sell_cnt, &p)) return;
+    w->sell_blk = walloc<int4>(w, p.len + pfr::kSellTail);
+    const int32_t pad = (int32_t)(p.kc * 64);
+    fill_dev(w->sell_blk, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
+    set_sell(w, p, s);
+    int64_t* off = dev_alloc_copy(p.off.data(), (int64_t)p.off.size(), s);
+    const int64_t npos = p.nslab * pfr::kSellRows;  // perm's length
+    hipLaunchKernelGGL(k_sell_fill<CI>, dim3(waves_grid(npos)), dim3(256), 0, s, npos, w->sell_perm, w->rowptr, col,
+                       static_cast<const float*>(w->val), off, (int)p.nch, (int)p.kc, w->sell_blk);
+    const hipError_t e = hipGetLastError();
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(off);
+    if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_sell_fill: ") + hipGetErrorString(e));
+}
+
+// Row-chain copy; V is the value type (float or int8).
+template <class CI, class V>
+void fill_chain(pfr_csr* w, const CI* col, hipStream_t s) {
+    ChainPlan p;
+    if (!plan_chain(w, row_lengths(w), &p)) return;  // the block kernels serve
+    // one spare quad row of padding after the last slab: the kernels'
+    // clamped loads may touch it
+    const int64_t n = ((int64_t)p.q0.back() * p.R + p.R) * 4;
+    V* v = walloc<V>(w, n);
+    w->chain_val = v;
+    fill_dev(v, n, V(0), s);
+    set_chain(w, p, s);
+    // staged-x form: byte offsets into the LDS copy of x, padding at its
+    // zero slot K; otherwise column indices, padding at column 0
+    const int mul = p.xlds ? 4 : 1;
+    const auto* val = static_cast<const V*>(w->val);
+    if (p.c16) {
+        auto* c = walloc<uint16_t>(w, n);
+        w->chain_col = c;
+        fill_dev(c, n, (uint16_t)(p.xlds ? w->K * 4 : 0), s);
+        hipLaunchKernelGGL((k_chain_fill<CI, V, uint16_t>), dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, (int)p.R,
+                           w->chain_perm, w->chain_q0, w->rowptr, col, val, mul, v, c);
+    } else {
+        auto* c = walloc<int32_t>(w, n);
+        w->chain_col = c;
+        fill_dev(c, n, (int32_t)(p.xlds ? w->K * 4 : 0), s);
+        hipLaunchKernelGGL((k_chain_fill<CI, V, int32_t>), dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, (int)p.R,
+                           w->chain_perm, w->chain_q0, w->rowptr, col, val, mul, v, c);
+    }
+    PFR_HIP(hipGetLastError());
+    PFR_HIP(hipStreamSynchronize(s));
+}
+
+// nnz-balanced copy, planned from the kept chunk counts.
+template <class CI, class V>
+void fill_bal(pfr_csr* w, const CI* col, hipStream_t s) {
+    BalPlan p;
+    if (!plan_bal(w, row_lengths(w), w->h_bal_cnt, &p)) return;
+    const int64_t n = (p.nrec + 64) * 4;  // one spare record per lane after the last group
+    V* v = walloc<V>(w, n);
+    w->bal_val = v;
+    w->bal_col = walloc<uint16_t>(w, n);
+    fill_dev(v, n, V(0), s);
+    fill_dev(w->bal_col, n, (uint16_t)(4 * p.kcw), s);  // chunk 0's zero
+    set_bal(w, p, s);
+    int32_t* gpos = dev_alloc_copy(p.gpos.data(), (int64_t)p.gpos.size(), s);
+    hipLaunchKernelGGL(k_bal_pad, dim3((unsigned)p.G), dim3(256), 0, s, (int)p.C, (int)p.kcw, w->bal_meta,
+                       w->bal_cmeta, w->bal_col);
+    hipLaunchKernelGGL((k_bal_fill<CI, V>), dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, (int)p.C, (int)p.kcw,
+                       w->bal_meta, w->bal_cmeta, w->bal_perm, gpos, w->rowptr, col, static_cast<const V*>(w->val),
+                       v, w->bal_col);
+    const hipError_t e = hipGetLastError();
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(gpos);
+    if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_fill: ") + hipGetErrorString(e));
+}
+
+template <class CI>
+void build_copy(pfr_csr* w, uint32_t bit, const CI* col, hipStream_t s) {
+    const bool i8 = w->vdt == PFR_I8;
+    if (bit == pfr::kCopySell) fill_sell(w, col, s);  // pending for float32 weights only
+    else if (bit == pfr::kCopyChain) i8 ? fill_chain<CI, int8_t>(w, col, s) : fill_chain<CI, float>(w, col, s);
+    else i8 ? fill_bal<CI, int8_t>(w, col, s) : fill_bal<CI, float>(w, col, s);
+}
+
+template <class P>
+void free_null(P*& p) {
+    if (p) (void)hipFree((void*)p);
+    p = nullptr;
+}
+
+// Frees a copy left part-built by a failed build.
+void drop_copy(pfr_csr* w, uint32_t bit) {
+    if (bit == pfr::kCopySell) {
+        free_null(w->sell_perm), free_null(w->sell_soff), free_null(w->sell_blk);
+        w->sell_nslab = w->sell_nch = w->sell_kc = 0;
+        w->sell_len = 0;
+    } else if (bit == pfr::kCopyChain) {
+        free_null(w->chain_q0), free_null(w->chain_len), free_null(w->chain_perm);
+        free_null(w->chain_val), free_null(w->chain_col);
+        w->chain_nslab = 0;
+    } else {
+        free_null(w->bal_meta), free_null(w->bal_cmeta), free_null(w->bal_perm);
+        free_null(w->bal_val), free_null(w->bal_col);
+        w->bal_ngroup = w->bal_nchunk = w->bal_kcw = 0;
+    }
+}
+
+// ---- Builds ------------------------------------------------------------------
+
+// The handle of a host CSR: row pointers, columns (uint16 when K <= 65536),
+// values and row scales on the device, the row-block table and the
+// merge-path partition; the other copies are built on first use.
+pfr_csr* build(pfr_ctx* ctx, int64_t M, int64_t K, const std::vector<int32_t>& rowptr,
+               const std::vector<int32_t>& col, const void* vals, pfr_dtype vdt,
+               const float* row_scales) {
+    auto* w = new pfr_csr();
+    try {
+        w->ctx = ctx;
+        w->M = M;
+        w->K = K;
+        w->nnz = rowptr[M];
+        w->vdt = vdt;
+        int32_t mx = 0;
+        for (int64_t r = 0; r < M; ++r) mx = std::max(mx, rowptr[r + 1] - rowptr[r]);
+        w->max_row_nnz = mx;
+        hipStream_t s = ctx->stream;
+        w->rowptr = walloc_copy(w, rowptr.data(), M + 1, s);
+        // col16 and val hold whole records of four and one spare record;
+        // padding entries are value 0 at column K (x's zero slot in the
+        // merge-path kernels, which read whole records and point loads past
+        // a share at the spare one)
+        const int64_t npad = (w->nnz + 3) / 4 * 4 + 4;
+        if (K > 65536) {
+            w->col = walloc_copy(w, col.data(), w->nnz, s);
+        } else {  // allocated (padding only) also without entries: kernels may load a row's first record
+            std::vector<uint16_t> c16(col.begin(), col.end());
+            c16.resize((size_t)npad, (uint16_t)std::min<int64_t>(K, 65535));
+            w->col16 = walloc_copy(w, c16.data(), npad, s);
+            PFR_HIP(hipStreamSynchronize(s));  // c16 goes out of scope
+        }
+        if (vdt == PFR_F32) {
+            std::vector<float> v(static_cast<const float*>(vals), static_cast<const float*>(vals) + w->nnz);
+            v.resize((size_t)npad, 0.0f);
+            w->val = walloc_copy(w, v.data(), npad, s);
+            PFR_HIP(hipStreamSynchronize(s));
+        } else {
+            std::vector<int8_t> v(static_cast<const int8_t*>(vals), static_cast<const int8_t*>(vals) + w->nnz);
+            v.resize((size_t)npad, 0);
+            w->val = walloc_copy(w, v.data(), npad, s);
+            PFR_HIP(hipStreamSynchronize(s));
+        }
+        if (row_scales) w->row_scale = walloc_copy(w, row_scales, M, s);
+        std::vector<int32_t> blocks = spmv_blocks(rowptr, M);
+        w->n_spmv_blocks = (int64_t)blocks.size() - 1;
+        w->spmv_blocks = walloc_copy(w, blocks.data(), (int64_t)blocks.size(), s);
+        bool sorted = true;
+        for (int64_t r = 0; r < M && sorted; ++r)
+            for (int32_t j = rowptr[r] + 1; j < rowptr[r + 1]; ++j)
+                if (col[j] <= col[j - 1]) { sorted = false; break; }
+        w->cols_sorted = sorted;
+        // per-row chunk counts for the plans of the copies built on first use
+        int64_t kc, nchs, nchb = 0, kcw = 1;
+        sell_geom(K, &kc, &nchs);
+        std::vector<int32_t> cs, cb;
+        if (vdt == PFR_F32 && sell_wanted(M, K, w->nnz) && chunks_ascend(rowptr, col, M, kc)) {
+            cs.assign((size_t)(M * nchs), 0);
+            for (int64_t r = 0; r < M; ++r)
+                for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cs[(size_t)(r * nchs + col[j] / kc)];
+        }
+        if (w->nnz > 0 && bal_geom(K, &nchb, &kcw) && chunks_ascend(rowptr, col, M, kcw)) {
+            cb.assign((size_t)(M * nchb), 0);
+            for (int64_t r = 0; r < M; ++r)
+                for (int32_t j = rowptr[r]; j < rowptr[r + 1]; ++j) ++cb[(size_t)(r * nchb + col[j] / kcw)];
+        }
+        set_lazy(w, rowptr, std::move(cs), std::move(cb));
+        set_merge(w, rowptr, s);
+        PFR_HIP(hipStreamSynchronize(s));
+        return w;
+    } catch (...) {
+        (void)hipStreamSynchronize(ctx->stream);
+        free_csr(w);
+        throw;
+    }
+}
+
+// The handle of D (M x K, row-major, device), as build() makes it from the
+// same entries: counts on the device, copied back (M x a few integers) for
+// the row pointers and the copies' plans, then the entries compacted on the
+// device, so the nonzeros never leave the GPU.
 pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, float thr) {
     hipStream_t s = ctx->stream;
     int64_t kc, nchs;
     sell_geom(K, &kc, &nchs);
-    if (!sell_wanted(M, K, 1) || nchs > kMaxCountChunks) nchs = 0;
+    if (!sell_wanted(M, K, 1)) nchs = 0;
     int64_t nchb = 0, kcw = 1;
     if (!bal_geom(K, &nchb, &kcw)) nchb = 0, kcw = 1;
     const int64_t stride = 1 + nchs + nchb;
@@ -1009,14 +1064,15 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
         w->vdt = PFR_F32;
         w->max_row_nnz = M ? *std::max_element(len.begin(), len.end()) : 0;
         w->cols_sorted = true;
-        w->rowptr = dev_alloc_copy(rowptr.data(), M + 1, s);
-        w->col = dev_alloc<int32_t>(w->nnz);
+        w->rowptr = walloc_copy(w, rowptr.data(), M + 1, s);
         const int64_t npad = (w->nnz + 3) / 4 * 4 + 4;  // whole records and a spare one, as build() pads
-        float* val = dev_alloc<float>(npad);
+        float* val = walloc<float>(w, npad);
         w->val = val;
         fill_dev(val + w->nnz, npad - w->nnz, 0.0f, s);
-        if (K <= 65536 && w->nnz > 0) {
-            w->col16 = dev_alloc<uint16_t>(npad);
+        if (K > 65536) {
+            w->col = walloc<int32_t>(w, w->nnz);
+        } else {
+            w->col16 = walloc<uint16_t>(w, npad);
             fill_dev(w->col16 + w->nnz, npad - w->nnz, (uint16_t)std::min<int64_t>(K, 65535), s);
         }
         hipLaunchKernelGGL(k_dense_compact, dim3((unsigned)M), dim3(256), 0, s, D, K, thr, w->rowptr, w->col,
@@ -1024,77 +1080,21 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
         PFR_HIP(hipGetLastError());
         std::vector<int32_t> blocks = spmv_blocks(rowptr, M);
         w->n_spmv_blocks = (int64_t)blocks.size() - 1;
-        w->spmv_blocks = dev_alloc_copy(blocks.data(), (int64_t)blocks.size(), s);
+        w->spmv_blocks = walloc_copy(w, blocks.data(), (int64_t)blocks.size(), s);
         PFR_HIP(hipStreamSynchronize(s));  // blocks goes out of scope
         if (w->nnz == 0) return w;
+        std::vector<int32_t> cs, cb;
         if (nchs > 0 && sell_wanted(M, K, w->nnz)) {
-            std::vector<int32_t> cs((size_t)(M * nchs));
+            cs.resize((size_t)(M * nchs));
             for (int64_t r = 0; r < M; ++r)
                 std::copy(cnt.begin() + r * stride + 1, cnt.begin() + r * stride + 1 + nchs, cs.begin() + r * nchs);
-            SellPlan p;
-            if (plan_sell(M, K, cs, &p)) {
-                w->sell_blk = dev_alloc<int4>(p.len + pfr::kSellTail);
-                const int32_t pad = (int32_t)(p.kc * 64);
-                fill_dev(w->sell_blk, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
-                set_sell(w, p, s);
-                int64_t* off = dev_alloc_copy(p.off.data(), (int64_t)p.off.size(), s);
-                const int64_t npos = p.nslab * pfr::kSellRows;  // perm's length
-                hipLaunchKernelGGL(k_sell_fill, dim3(waves_grid(npos)), dim3(256), 0, s, npos, w->sell_perm,
-                                   w->rowptr, w->col, val, off, (int)p.nch, (int)p.kc, w->sell_blk);
-                hipError_t e = hipGetLastError();
-                (void)hipStreamSynchronize(s);
-                (void)hipFree(off);
-                if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_sell_fill: ") + hipGetErrorString(e));
-            }
-        }
-        ChainPlan cp;
-        if (plan_chain(w, len, &cp)) {
-            const int64_t n = ((int64_t)cp.q0.back() * cp.R + cp.R) * 4;
-            float* v = dev_alloc<float>(n);
-            w->chain_val = v;
-            fill_dev(v, n, 0.0f, s);
-            set_chain(w, cp, s);
-            const int mul = cp.xlds ? 4 : 1;
-            if (cp.c16) {
-                auto* c = dev_alloc<uint16_t>(n);
-                w->chain_col = c;
-                fill_dev(c, n, (uint16_t)(cp.xlds ? K * 4 : 0), s);
-                hipLaunchKernelGGL(k_chain_fill<uint16_t>, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)cp.R,
-                                   w->chain_perm, w->chain_q0, w->rowptr, w->col, val, mul, v, c);
-            } else {
-                auto* c = dev_alloc<int32_t>(n);
-                w->chain_col = c;
-                fill_dev(c, n, (int32_t)(cp.xlds ? K * 4 : 0), s);
-                hipLaunchKernelGGL(k_chain_fill<int32_t>, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)cp.R,
-                                   w->chain_perm, w->chain_q0, w->rowptr, w->col, val, mul, v, c);
-            }
-            PFR_HIP(hipGetLastError());
         }
         if (nchb > 0) {
-            std::vector<int32_t> cb((size_t)(M * nchb));
+            cb.resize((size_t)(M * nchb));
             for (int64_t r = 0; r < M; ++r)
                 std::copy(cnt.begin() + r * stride + 1 + nchs, cnt.begin() + (r + 1) * stride, cb.begin() + r * nchb);
-            BalPlan bp;
-            if (plan_bal(w, len, cb, &bp)) {
-                const int64_t n = (bp.nrec + 64) * 4;
-                float* v = dev_alloc<float>(n);
-                w->bal_val = v;
-                w->bal_col = dev_alloc<uint16_t>(n);
-                fill_dev(v, n, 0.0f, s);
-                fill_dev(w->bal_col, n, (uint16_t)(4 * bp.kcw), s);  // chunk 0's zero
-                set_bal(w, bp, s);
-                int32_t* gpos = dev_alloc_copy(bp.gpos.data(), (int64_t)bp.gpos.size(), s);
-                hipLaunchKernelGGL(k_bal_pad, dim3((unsigned)bp.G), dim3(256), 0, s, (int)bp.C, (int)bp.kcw,
-                                   w->bal_meta, w->bal_cmeta, w->bal_col);
-                hipLaunchKernelGGL(k_bal_fill, dim3(waves_grid(M)), dim3(256), 0, s, M, (int)bp.C, (int)bp.kcw,
-                                   w->bal_meta, w->bal_cmeta, w->bal_perm, gpos, w->rowptr, w->col, val, v,
-                                   w->bal_col);
-                hipError_t e = hipGetLastError();
-                (void)hipStreamSynchronize(s);
-                (void)hipFree(gpos);
-                if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_fill: ") + hipGetErrorString(e));
-            }
         }
+        set_lazy(w, rowptr, std::move(cs), std::move(cb));
         set_merge(w, rowptr, s);
         PFR_HIP(hipStreamSynchronize(s));
         return w;
@@ -1107,7 +1107,44 @@ pfr_csr* build_dense_dev(pfr_ctx* ctx, const float* D, int64_t M, int64_t K, flo
 
 }  // namespace
 
+namespace pfr {
+
+void csr_build_copies(pfr_csr* w, uint32_t which) {
+    if ((w->pending.load(std::memory_order_acquire) & which) == 0) return;
+    std::lock_guard<std::mutex> lock(w->lazy_mu);
+    which &= w->pending.load(std::memory_order_acquire);
+    if (which == 0) return;
+    hipStream_t s = w->ctx->stream;
+    // nothing is allocated or synchronized while the stream is captured:
+    // the product reads the CSR in place and the copy waits for an eager one
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    PFR_HIP(hipStreamIsCapturing(s, &st));
+    if (st != hipStreamCaptureStatusNone) return;
+    for (const uint32_t bit : {kCopySell, kCopyChain, kCopyBal}) {
+        if ((which & bit) == 0) continue;
+        const int64_t before = w->dev_bytes;
+        try {
+            if (w->col16) build_copy(w, bit, w->col16, s);
+            else build_copy(w, bit, w->col, s);
+        } catch (...) {
+            (void)hipStreamSynchronize(s);
+            drop_copy(w, bit);
+            w->dev_bytes = before;
+            throw;  // still pending: the next product tries again
+        }
+        w->pending.fetch_and(~bit, std::memory_order_release);
+    }
+    if (w->pending.load(std::memory_order_acquire) == 0) {
+        std::vector<int32_t>().swap(w->h_rowptr);
+        std::vector<int32_t>().swap(w->h_sell_cnt);
+        std::vector<int32_t>().swap(w->h_bal_cnt);
+    }
+}
+
+}  // namespace pfr
+
 extern "C" {
+
 
 extern "C++" {
 namespace {
@@ -1253,8 +1290,12 @@ int pfr_csr_dense_semantics(pfr_csr* w) {
         try {
             fill_dev(bm, w->M * nw, 0ull, s);
             if (w->nnz > 0) {
-                hipLaunchKernelGGL(k_pattern, dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, w->rowptr, w->col, nw,
-                                   bm);
+                if (w->col16)
+                    hipLaunchKernelGGL(k_pattern<uint16_t>, dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, w->rowptr,
+                                       w->col16, nw, bm);
+                else
+                    hipLaunchKernelGGL(k_pattern<int32_t>, dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, w->rowptr,
+                                       w->col, nw, bm);
                 PFR_HIP(hipGetLastError());
             }
             PFR_HIP(hipStreamSynchronize(s));
@@ -1265,6 +1306,7 @@ int pfr_csr_dense_semantics(pfr_csr* w) {
         }
         w->pattern = reinterpret_cast<uint64_t*>(bm);
         w->pattern_nw = nw;
+        w->dev_bytes += (int64_t)sizeof(unsigned long long) * w->M * nw;
     });
 }
 
@@ -1274,6 +1316,13 @@ int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz) {
         if (M) *M = w->M;
         if (K) *K = w->K;
         if (nnz) *nnz = w->nnz;
+    });
+}
+
+int pfr_csr_device_bytes(const pfr_csr* w, int64_t* bytes) {
+    return pfr::guarded([&] {
+        pfr::require(w != nullptr && bytes != nullptr, "null CSR handle or output");
+        *bytes = w->dev_bytes;
     });
 }
 

@@ -58,9 +58,9 @@ __device__ __forceinline__ float wval(const void* __restrict__ val, const float*
 
 // One wave per CSR row, lanes across the N columns (4 per lane when VEC).
 // Output element (row, c) goes to Y[row * ldy_r + c * ldy_c].
-template <bool FAST, bool VEC, bool I8>
+template <bool FAST, bool VEC, bool I8, class C>
 __global__ __launch_bounds__(256) void k_spmm_rows(
-    int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+    int M, int N, const int32_t* __restrict__ rowptr, const C* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
     int64_t c_size, float beta, int act) {
@@ -118,9 +118,9 @@ __global__ __launch_bounds__(256) void k_spmm_rows(
 }
 
 // NP lanes per row (NP = next power of two >= N, N < 64), 64 / NP rows per wave.
-template <int NP, bool FAST, bool I8>
+template <int NP, bool FAST, bool I8, class C>
 __global__ __launch_bounds__(256) void k_spmm_small(
-    int M, int N, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ col,
+    int M, int N, const int32_t* __restrict__ rowptr, const C* __restrict__ col,
     const void* __restrict__ val, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
     float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias,
     int64_t c_size, float beta, int act) {
@@ -144,10 +144,10 @@ __global__ __launch_bounds__(256) void k_spmm_small(
 // either the products RN(w * x[col]) (float values) or x[col] and the int8
 // value (int8 values: the product needs the row's scale); then lane g of
 // wave 0 folds row r0 + g in storage order.  Longer blocks go in chunks.
-template <bool I8>
+template <bool I8, class C>
 __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
     const int32_t* __restrict__ blocks, const int32_t* __restrict__ rowptr,
-    const int32_t* __restrict__ col, const void* __restrict__ val, const float* __restrict__ rs,
+    const C* __restrict__ col, const void* __restrict__ val, const float* __restrict__ rs,
     const float* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy_r,
     const float* __restrict__ bias, int64_t c_size, float beta, int act) {
     __shared__ float P[kSpmvCap];
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kSpmvThreads) void k_spmv_wg(
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int j = base + tid + i * kSpmvThreads;
-            cl[i] = j < cend ? col[j] : 0;
+            cl[i] = j < cend ? (int)col[j] : 0;
             if constexpr (I8) q[i] = j < cend ? static_cast<const int8_t*>(val)[j] : 0;
             else w[i] = j < cend ? static_cast<const float*>(val)[j] : 0.0f;
         }
@@ -2105,6 +2105,51 @@ void launch_sell(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t
 #undef PFR_SELLX
 }
 
+// The kernels that read the CSR in place, columns of type C: the block
+// SpMV, the small-N kernel and the row kernel.
+template <bool FAST, bool I8, class C>
+void launch_inplace(pfr_ctx* ctx, const pfr_csr* W, const C* col, const float* X, int64_t N, int64_t ldx, float* Y,
+                    int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
+    const int M = (int)W->M;
+    hipStream_t s = ctx->stream;
+    const void* val = W->val;
+    const float* rs = W->row_scale;
+    if (N == 1) {
+        hipLaunchKernelGGL((k_spmv_wg<I8, C>), dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
+                           W->spmv_blocks, W->rowptr, col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta, act);
+    } else if (N < 64) {
+        const int np = next_pow2((int)N);
+        const int rows_per_block = kWaves * (64 / np);
+        const unsigned grid = (unsigned)((M + rows_per_block - 1) / rows_per_block);
+#define PFR_SMALL(NPV)                                                                                \
+    case NPV:                                                                                         \
+        hipLaunchKernelGGL((k_spmm_small<NPV, FAST, I8, C>), dim3(grid), dim3(256), 0, s, M, (int)N,  \
+                           W->rowptr, col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);  \
+        break;
+        switch (np) {
+            PFR_SMALL(2)
+            PFR_SMALL(4)
+            PFR_SMALL(8)
+            PFR_SMALL(16)
+            PFR_SMALL(32)
+            PFR_SMALL(64)
+            default:
+                throw pfr::Error(PFR_ERR_UNSUPPORTED, "unexpected column count");
+        }
+#undef PFR_SMALL
+    } else {
+        const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
+        const bool vec = (N % 4 == 0) && (ldx % 4 == 0) && ldy_c == 1 && (ldy_r % 4 == 0) &&
+                         aligned16(X) && aligned16(Y);
+        if (vec)
+            hipLaunchKernelGGL((k_spmm_rows<FAST, true, I8, C>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
+                               col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        else
+            hipLaunchKernelGGL((k_spmm_rows<FAST, false, I8, C>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
+                               col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+    }
+}
+
 // Row, small-N and vector kernels for one value type.
 template <bool FAST, bool I8>
 void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
@@ -2169,39 +2214,10 @@ void launch_csr_kernels(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t 
             hipLaunchKernelGGL((k_spmv_chain<I8, false>), grid, block, 0, s, W->chain_q0, W->chain_len,
                                W->chain_perm, W->chain_val, W->chain_col, rs, X, (int)ldx, Y, ldy_r, bias, c_size,
                                beta, act);
-    } else if (N == 1) {
-        hipLaunchKernelGGL(k_spmv_wg<I8>, dim3((unsigned)W->n_spmv_blocks), dim3(kSpmvThreads), 0, s,
-                           W->spmv_blocks, W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, bias, c_size, beta, act);
-    } else if (N < 64) {
-        const int np = next_pow2((int)N);
-        const int rows_per_block = kWaves * (64 / np);
-        const unsigned grid = (unsigned)((M + rows_per_block - 1) / rows_per_block);
-#define PFR_SMALL(NPV)                                                                                \
-    case NPV:                                                                                         \
-        hipLaunchKernelGGL((k_spmm_small<NPV, FAST, I8>), dim3(grid), dim3(256), 0, s, M, (int)N,   \
-                           W->rowptr, W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act); \
-        break;
-        switch (np) {
-            PFR_SMALL(2)
-            PFR_SMALL(4)
-            PFR_SMALL(8)
-            PFR_SMALL(16)
-            PFR_SMALL(32)
-            PFR_SMALL(64)
-            default:
-                throw pfr::Error(PFR_ERR_UNSUPPORTED, "unexpected column count");
-        }
-#undef PFR_SMALL
+    } else if (W->col16 != nullptr) {
+        launch_inplace<FAST, I8>(ctx, W, W->col16, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     } else {
-        const unsigned grid = (unsigned)((M + kWaves - 1) / kWaves);
-        const bool vec = (N % 4 == 0) && (ldx % 4 == 0) && ldy_c == 1 && (ldy_r % 4 == 0) &&
-                         aligned16(X) && aligned16(Y);
-        if (vec)
-            hipLaunchKernelGGL((k_spmm_rows<FAST, true, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
-                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
-        else
-            hipLaunchKernelGGL((k_spmm_rows<FAST, false, I8>), dim3(grid), dim3(256), 0, s, M, (int)N, W->rowptr,
-                               W->col, val, rs, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
+        launch_inplace<FAST, I8>(ctx, W, W->col, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
     }
 }
 
@@ -2303,6 +2319,16 @@ void check_act(int act) {
     pfr::require(act == PFR_ACT_NONE || act == PFR_ACT_RELU || act == PFR_ACT_GELU, "unknown activation");
 }
 
+// Builds the derived copy that a product of N columns in this mode runs on,
+// when the handle still has it pending (its first such product).
+void ensure_copies(const pfr_ctx* ctx, const pfr_csr* W, int64_t N, bool fast) {
+    uint32_t need = 0;
+    if (W->vdt == PFR_F32 && N >= kSellMinN) need |= pfr::kCopySell;
+    if (fast && ((N >= 2 && N <= 8) || (N == 1 && !(ctx->merge && W->mp_wave != nullptr)))) need |= pfr::kCopyBal;
+    if (!fast && N <= 8) need |= pfr::kCopyChain;
+    if ((W->pending.load(std::memory_order_acquire) & need) != 0) pfr::csr_build_copies(const_cast<pfr_csr*>(W), need);
+}
+
 void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t ldx, float* Y,
               int64_t ldy, int mode, int act = PFR_ACT_NONE) {
     check_csr(W);
@@ -2311,6 +2337,7 @@ void spmm_dev(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int64_t
     pfr::require(mode == PFR_MODE_STRICT || mode == PFR_MODE_FAST, "unknown mode");
     pfr::require((X && Y) || W->M * N == 0, "null X/Y");
     check_act(act);
+    if (W->M > 0 && N > 0) ensure_copies(ctx, W, N, mode == PFR_MODE_FAST);
     launch_spmm(ctx, W, X, N, ldx, Y, ldy, 1, nullptr, 0, 0.0f, mode == PFR_MODE_FAST, act);
 }
 
@@ -2328,6 +2355,7 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     const int64_t Nf = BT->M;
     if (Mb == 0 || Nf == 0) return;
     pfr::require(A != nullptr && Y != nullptr, "null A/Y");
+    if (ws == nullptr) ensure_copies(ctx, BT, Mb, mode == PFR_MODE_FAST);  // the allocation-free entry builds none
     if (C == nullptr || c_size <= 0) {
         C = nullptr;
         c_size = 0;

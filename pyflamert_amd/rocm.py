@@ -291,6 +291,13 @@ class CsrWeight:
         check(self.ctx._lib.pfr_csr_dense_semantics(self.handle))
         return self
 
+    def device_bytes(self):
+        """pfr_csr_device_bytes: device memory the handle holds now (the CSR,
+        its tables and the derived copies its products have built)."""
+        b = C.c_int64()
+        check(self.ctx._lib.pfr_csr_device_bytes(self.handle, C.byref(b)))
+        return b.value
+
     def free(self):
         if self.handle:
             check(self.ctx._lib.pfr_csr_free(self.handle))

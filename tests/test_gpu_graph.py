@@ -7,7 +7,8 @@ workspace), and a 2:4 int8 GEMM, captured once on a capture stream and
 replayed several times with eager work and synchronisations in between;
 every replay must give the eager results bit for bit (the same kernels on
 the same data).  None of these launches records a memset or an
-allocation."""
+allocation; the eager run before the capture builds the weights' derived
+copies, so the captured products run on them."""
 import sys
 
 import numpy as np
@@ -69,6 +70,10 @@ def test_graph_replay_matches_eager(ctx):
 
     main = torch.cuda.current_stream().cuda_stream
     ctx.set_stream(main)
+    # the allocating entry builds the Gemm weight's sliced-ELL copy, which the
+    # allocation-free entry then reads (it builds no copy itself)
+    ctx.gemm_csr_dev(A.data_ptr(), 64, 3000, BT, outs["gemm"].data_ptr(), 1.0, 1.0, bias.data_ptr(), 700,
+                     relu=True)
     run()
     torch.cuda.synchronize()
     eager = {k: v.clone() for k, v in outs.items()}
