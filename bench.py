@@ -60,6 +60,8 @@ def time_gpu(sets, N, steps, warmup, mode):
     stream (torch's current stream), bracketed by HIP events."""
     import torch
 
+    for W, dX, dY in sets:  # each weight's first product of this kind builds its derived copy
+        W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode)
     for i in range(warmup):
         W, dX, dY = sets[i % len(sets)]
         W.spmm_dev(dX.data_ptr(), N, dY.data_ptr(), mode=mode)
@@ -501,6 +503,14 @@ def bench_decode_int8(ctx, cpu=True, modes=("fast", "strict"), reps=20):
     res = {}
     if cpu:
         res["cpu_reference"] = cpu_decode_reference(data, shapes)
+    total_nnz = NL * sum(count * len(data[name][2]) for name, (_, _, count) in shapes.items())
+
+    def bytes_per_nnz():  # device bytes the layer weights hold, per nonzero
+        return round(sum(W.device_bytes() for seq in layers for _, W in seq) / total_nnz, 4)
+
+    # grows as the first product of each kind builds its derived copy
+    footprint = {"after_upload": bytes_per_nnz()}
+    res["device_bytes_per_nnz"] = footprint
     for B, mode in [(B, m) for m in ("fast", "strict") if m in modes for B in (1, 8)]:
         bufs = {name: (torch.randn((K_, B), dtype=torch.float32, device="cuda"),
                        torch.empty((M_, B), dtype=torch.float32, device="cuda"))
@@ -571,7 +581,8 @@ def bench_decode_int8(ctx, cpu=True, modes=("fast", "strict"), reps=20):
                         "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                         "gflops": round(flops / (ms * 1e-3) / 1e9, 1)}
         res[f"batch{B}_{mode}"] = out
-        log(f"decode int8 batch {B} {mode}: {out}")
+        footprint[f"after_batch{B}_{mode}"] = bytes_per_nnz()
+        log(f"decode int8 batch {B} {mode}: {out}; weights hold {footprint[f'after_batch{B}_{mode}']} B/nnz")
     for seq in layers:
         for _, W in seq:
             W.free()

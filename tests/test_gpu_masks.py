@@ -83,6 +83,21 @@ def test_nm_ratios_and_partial_groups(ctx, total):
         assert same(ctx.nm_mask(w, n, m), O.orc_nm_mask(w, n, m)), (total, n, m)
 
 
+def test_nm24_every_tie_pattern(ctx):
+    """The closed-form 2:4 kernel on every group of four drawn from nine
+    values (signed zeros, +-1, +-2, +-inf, NaN): 6561 groups, every pattern
+    of ties the comparator |a| > |b| can meet, against the oracle's heap
+    select and, where it is built, the reference's compute_mask."""
+    vals = np.array([0.0, -0.0, 1.0, -1.0, 2.0, -2.0, np.inf, -np.inf, np.nan], np.float32)
+    grid = np.stack(np.meshgrid(*([np.arange(len(vals))] * 4), indexing="ij"), -1).reshape(-1, 4)
+    w = np.ascontiguousarray(vals[grid].ravel())
+    say(f"2:4 mask, every tie pattern: {w.size // 4} groups")
+    got = ctx.nm_mask(w, 2, 4)
+    assert same(got, O.orc_nm_mask(w, 2, 4))
+    if O.have_ref():
+        assert same(got, O.ref_nm_mask(w, 2, 4))
+
+
 @pytest.mark.parametrize("frac,s", [(0.01, 0.5), (0.01, 0.995), (0.2, 0.9), (0.3, 0.05)])
 def test_magnitude_nan_weights(ctx, frac, s):
     """A NaN weight is never kept and counts among the zeros (the

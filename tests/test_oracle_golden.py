@@ -351,6 +351,19 @@ def test_oracle_matches_reference_random():
         assert same(O.orc_nm_mask(w, n, m), O.ref_nm_mask(w, n, m))
 
 
+@pytest.mark.skipif(not O.have_ref(), reason="compiled reference not present")
+def test_nm_mask_every_tie_pattern_against_reference():
+    """Every group of four drawn from nine values (signed zeros, +-1, +-2,
+    +-inf, NaN) through the compiled reference's compute_mask and the
+    oracle's heap select: the same mask bit for bit, for 2:4 and for 1:4
+    and 3:4 on the same groups."""
+    vals = np.array([0.0, -0.0, 1.0, -1.0, 2.0, -2.0, np.inf, -np.inf, np.nan], np.float32)
+    grid = np.stack(np.meshgrid(*([np.arange(len(vals))] * 4), indexing="ij"), -1).reshape(-1, 4)
+    w = np.ascontiguousarray(vals[grid].ravel())
+    for n in (1, 2, 3):
+        assert same(O.orc_nm_mask(w, n, 4), O.ref_nm_mask(w, n, 4)), n
+
+
 def test_neighbours_golden(golden):
     """Gelu, LayerNormalization and Add restated against the reference ops'
     outputs, bit for bit (same libm tanhf as the reference build)."""
