@@ -79,6 +79,49 @@ def test_spmm_fast_normwise(ctx, cfg_weight, N):
     assert np.abs(Y - R).max() <= 1e-5 * np.abs(R).max()
 
 
+@pytest.mark.parametrize("M,K,N,dens", [(4096, 4096, 16, 0.1), (4096, 4096, 32, 0.1), (4096, 4096, 64, 0.1),
+                                        (1500, 3000, 48, 0.2), (700, 5000, 64, 0.05), (33, 2100, 20, 0.5)])
+def test_fast_chunk_split(ctx, M, K, N, dens):
+    """Fast mode at few columns with K in several chunks (the column-slice
+    kernel's chunked walk, several slabs per workgroup, a partial last
+    slab).  Within 1e-5 normwise of the oracle and within the forward error bound
+    of any summation order, with an odd number of chunks (K = 3000, 5000,
+    2100); repeated calls give the same bits; bias and Relu through the
+    Gemm form's epilogue against the strict result."""
+    from bounds import gamma_bound_ok
+
+    ip, ix, v = workloads.csr_uniform(M, K, dens, 0.02, seed=M + K + N)
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    X = workloads.dense_normal((K, N), 1.0, seed=N)
+    say(f"fast chunk split M={M} K={K} N={N}")
+    Y = W.spmm(X, mode="fast")
+    R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+    assert np.abs(Y - R).max() <= 1e-5 * np.abs(R).max()
+    ok, worst = gamma_bound_ok(Y, M, K, ip, ix, v, X)
+    assert ok, worst
+    Y2 = W.spmm(X, mode="fast")
+    assert bits_equal(Y2, Y)
+    W.free()
+    # Gemm form: Y = relu(A . B + bias), B = W^T, A = X^T (Mb = N rows)
+    B = np.zeros((K, M), np.float32)
+    rows = np.repeat(np.arange(M), np.diff(ip))
+    B[ix, rows] = v
+    BT = ctx.csr_from_dense(B, transpose=True)
+    import torch
+
+    dA = torch.from_numpy(np.ascontiguousarray(X.T)).cuda()
+    dC = torch.from_numpy(workloads.dense_normal((M,), 0.1, seed=3)).cuda()
+    out = {}
+    for mode in ("fast", "strict"):
+        dY = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        ctx.gemm_csr_dev(dA.data_ptr(), N, K, BT, dY.data_ptr(), 1.0, 1.0, dC.data_ptr(), M, mode=mode, relu=True)
+        ctx.synchronize()
+        out[mode] = dY.cpu().numpy()
+    assert np.abs(out["fast"] - out["strict"]).max() <= 1e-5 * max(np.abs(out["strict"]).max(), 1e-30)
+    assert (out["fast"] >= 0).all()
+    BT.free()
+
+
 def test_golden_csr(ctx, golden):
     g = golden("csr.npz")
     M, K = g["W"].shape
