@@ -531,8 +531,13 @@ void launch_chain_x(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx,
 // (row, column) pair is its own in-order chain, one lane each,
 // so NC / 4 waves fold (NC = 2, 4 or 8, N <= NC) while four producer waves
 // load the values and offsets two chunks ahead, gather the x rows from global
-// memory (16-byte loads when x rows are aligned and N == NC >= 4) and write
-// RN(w * x[col, n]) for every column.  Steps past a row's count (and quad
+// memory one chunk ahead (16-byte loads when x rows are aligned and N == NC
+// >= 4) and write RN(w * x[col, n]) for every column.  The gathers are what
+// bounds it: on the 4096 x 4096 int8 decode weight at batch 8 a timing-only
+// copy without them takes 27.9 us, against 59.9 us when each chunk gathered
+// its own x rows and 52.0 us gathering them a chunk ahead.  (x staged in LDS
+// instead, 128 KiB at K = 4096, leaves room for 8-quad-row product chunks
+// only, and the per-chunk barriers made that 68 us.)  Steps past a row's count (and quad
 // rows past the slab) give +0; their gather addresses are clamped into x.
 // LDS: 2 x 32 quad rows x NC x 16 rows x 16 B of products.
 constexpr int kChainNR = 16;  // rows per workgroup of this kernel
@@ -630,9 +635,10 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
             return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
         }
     };
-    auto chunk = [&](int i, const ValT* vc, const uint2* cc, ValT* vn, uint2* cn) {
-        load(min(i + 2, nch - 1), vn, cn);
-        float xg[T][4][NC];
+    // the x rows of a chunk's records, gathered one chunk ahead of their use
+    // (their latency then overlaps a chunk's products instead of adding to it)
+    using XG = float[T][4][NC];
+    auto gather = [&](const uint2* cc, XG& xg) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -654,6 +660,12 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
                     for (int q = 0; q < NC; ++q) xg[t][e][q] = xr[min(q, N - 1)];
                 }
             }
+    };
+    // chunk i: values and columns two chunks ahead, x one chunk ahead, then
+    // chunk i's products from its values (vc) and the x gathered last chunk
+    auto chunk = [&](int i, const ValT* vc, ValT* vn, uint2* cn, const uint2* cnext, XG& xg, XG& xnext) {
+        load(min(i + 2, nch - 1), vn, cn);
+        gather(cnext, xnext);
         float4* b = ((i & 1) ? buf1 : buf0);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -679,15 +691,17 @@ __global__ __launch_bounds__(64 * (chain_n_folders<NC>() + kChainNP)) void k_spm
         }
         __syncthreads();
     };
+    XG xa, xb;
     load(0, v0, c0);
     load(min(1, nch - 1), v1, c1);
+    gather(c0, xa);
     for (int i = 0; i < iters; i += 6) {
-        chunk(i, v0, c0, v2, c2);
-        chunk(i + 1, v1, c1, v0, c0);
-        chunk(i + 2, v2, c2, v1, c1);
-        chunk(i + 3, v0, c0, v2, c2);
-        chunk(i + 4, v1, c1, v0, c0);
-        chunk(i + 5, v2, c2, v1, c1);
+        chunk(i, v0, v2, c2, c1, xa, xb);
+        chunk(i + 1, v1, v0, c0, c2, xb, xa);
+        chunk(i + 2, v2, v1, c1, c0, xa, xb);
+        chunk(i + 3, v0, v2, c2, c1, xb, xa);
+        chunk(i + 4, v1, v0, c0, c2, xa, xb);
+        chunk(i + 5, v2, v1, c1, c0, xb, xa);
     }
 }
 
