@@ -594,24 +594,26 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
                           xs_dev, zp_dev, row_sum);
 }
 
-// int8 2:4 GEMM with the weight streamed into registers.  Tiles of 64 RB
-// x 128 outputs, four waves (one per SIMD), wave w owning RB row blocks
-// (rows 16 RB w .. 16 RB w + 16 RB - 1) and all 128 columns, with
+// int8 2:4 GEMM with the weight streamed into registers.  Tiles of 256 x
+// 128 outputs, 16 / RB waves, wave w owning RB row blocks (rows 16 RB w ..
+// 16 RB w + 16 RB - 1) and all 128 columns, with
 // k_sp24_i8's MFMA order; each wave loads its own row blocks' packed values
-// and positions straight from global memory into a ring of eight register
-// slots (one per k step; the packed order is the MFMA's lane order, so one
-// 16-byte load per row block and step, and one for the row blocks'
-// positions from the regrouped idxw), and only X goes through LDS, in eight
-// 16 KiB stages filled by direct-to-LDS loads.  Against k_sp24_i8 this
-// takes the weight out of LDS (40 KiB of writes and reads per step at RB =
-// 4) and keeps seven steps of loads in flight per wave instead of three,
-// which the weight, streamed from HBM, needs to cover its latency: RB + 5
-// loads per step, so seven steps stay within the 63 vector-memory
-// instructions a wave can have outstanding.  RB = 4 (256-row tiles) is
-// used: RB = 3 (192-row tiles, 232 tiles for 11008 x 512 instead of 172,
-// 31 KiB loaded per CU and step instead of 36) measured slower, 29.4
-// against 28.2 us, as every tile also streams all of X.
-// Per step s (slot and stage u = s % 8) each wave runs the 8 RB MFMAs of
+// and positions straight from global memory into a ring of register slots
+// (one per k step: eight at RB = 4, six at RB = 2; the packed order is the
+// MFMA's lane order, so one 16-byte load per row block and step, and one for
+// the row blocks' positions from the regrouped idxw), and only X goes
+// through LDS, in 16 KiB stages filled by direct-to-LDS loads (RB loads per
+// wave and step).  Against k_sp24_i8 this takes the weight out of LDS (40
+// KiB of writes and reads per step) and keeps SLOTS - 1 steps of loads in
+// flight per wave instead of three, which the weight, streamed from HBM,
+// needs to cover its latency: 2 RB + 1 loads per step, within the 63
+// vector-memory instructions a wave can have outstanding.  RB = 2 (eight
+// waves, two per SIMD: one wave's memory stalls leave the SIMD's MFMA unit
+// to the other) is launched: 26.8 against 27.4 us for RB = 4 (four waves of
+// 64 rows), bit-identical.  192-row tiles (RB = 3, 232 tiles for 11008 x 512
+// instead of 172) measured slower, 29.4 against 28.2 us, as every tile also
+// streams all of X.
+// Per step s (slot and stage u = s % SLOTS) each wave runs the 8 RB MFMAs of
 // column blocks j = 0..7, reading the B fragment of column block j + 3
 // (the next step's blocks 0..2 for j >= 5) from LDS while block j's MFMAs
 // run, in a ring of four fragment registers.  On even steps, before
@@ -619,8 +621,8 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
 // s + 1 and s + 2 (vmcnt: the loads of the steps issued after them may
 // still be in flight) and for its LDS reads, and meets the other waves at
 // the barrier: stages s + 1 and s + 2 are then complete, and every wave has
-// read all of stage s.  Every step then loads step s + 7 into stage and
-// register slot (s + 7) % 8, the previous step's: after an even step's
+// read all of stage s.  Every step then loads step s + SLOTS - 1 into stage
+// and register slot (s - 1) % SLOTS, the previous step's: after an even step's
 // barrier that stage has been read by every wave, and an odd step reuses
 // the stage of the even step before it, read before that step's barrier.
 // (A barrier every step cost about a fifth of a streaming step.)  X is the row-major activation (XROW form of
@@ -629,12 +631,17 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8(
 // of the ring at the back edge and drains all loads there).  The eight
 // stages are separate arrays so the compiler's wait counting sees that a
 // stage load never writes the stages being read.
-constexpr int kRSlots = 8, kRLead = 7, kRStage = 128 * 128, kRB = 4;
-// the last step issued before step s's loads (sr_last(0): the prologue's)
-constexpr int sr_last(int s) { return s + kRLead - 1; }
+constexpr int kRSlots = 8, kRStage = 128 * 128, kRB = 4;
+// the launched form: RB = 2, eight waves (two per SIMD, each with half the
+// registers, so a ring of six slots)
+constexpr int kRB8 = 2, kRSlots8 = 6;
+// the last step issued before step s's loads (sr_last<LEAD>(0): the
+// prologue's), LEAD steps ahead
+template <int LEAD>
+constexpr int sr_last(int s) { return s + LEAD - 1; }
 
 template <int OUT, int NKT, int RB>
-__global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
+__global__ __launch_bounds__(64 * (16 / RB), 1) void k_sp24_i8r(
     int nkt_arg, const v4i* __restrict__ A, const uint32_t* __restrict__ I,
     const int8_t* __restrict__ B, int64_t ldb, int M, int N, const float* __restrict__ ws, float xs,
     float inv_out, int32_t out_zp, int inrange, void* __restrict__ Y, int64_t ldy, int yvec, int ntn,
@@ -648,9 +655,12 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     __shared__ __attribute__((aligned(1024))) char b5[kRStage];
     __shared__ __attribute__((aligned(1024))) char b6[kRStage];
     __shared__ __attribute__((aligned(1024))) char b7[kRStage];
-    __shared__ __attribute__((aligned(16))) float scl[kI8TileM];  // the tile's row scales (and the next rows)
-    constexpr int nkt = NKT, kRLoads = RB + 5;
-    static_assert(RB >= 1 && RB <= 4 && kRLoads * kRLead <= 63, "loads in flight exceed the wave's counter");
+    // NW waves of RB row blocks each: 16 row blocks (256 rows) per tile
+    constexpr int NW = 16 / RB;
+    __shared__ __attribute__((aligned(16))) float scl[64 * NW];  // the tile's row scales (and the next rows)
+    constexpr int nkt = NKT, kRLoads = 2 * RB + 1;
+    constexpr int SLOTS = RB == 4 ? kRSlots : kRSlots8, LEAD = SLOTS - 1;
+    static_assert((RB == 2 || RB == 4) && kRLoads * LEAD <= 63, "loads in flight exceed the wave's counter");
     (void)nkt_arg;
     const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
     const int kb = l >> 4, c = l & 15;
@@ -662,7 +672,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
         mt = T / ntn;
         nt = T % ntn;
     }
-    const int64_t mb0 = (int64_t)mt * (4 * RB);  // the tile's first row block
+    const int64_t mb0 = (int64_t)mt * (NW * RB);  // the tile's first row block
     const int64_t n0 = (int64_t)nt * kI8TileN;
     auto stage = [&](auto uc) -> char* {
         constexpr int u = decltype(uc)::value;
@@ -679,40 +689,42 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     // per-lane offset fixed for the whole kernel, so the loads take the
     // scalar-base form and the loop needs no per-load address arithmetic.
     // This wave's row blocks mb0 + RB w + i: element (row block, step) at
-    // (rb * nkt + step) * 64 + lane; their positions are group mb0 / RB + w
-    // of idxw.
+    // (rb * nkt + step) * 64 + lane; their positions are elements
+    // (RB w) % 4 .. of group (mb0 + RB w) / 4 of idxw (four row blocks per
+    // group).
     // (the positions are loaded as exactly RB dwords of the lane's 16 bytes:
     // a dead fourth register of a pending load would be handed to other
     // values, and writing it makes the compiler drain every load first)
     typedef int vrb __attribute__((ext_vector_type(RB)));
     const v4i* aw = A + (mb0 + RB * w) * nkt * 64;
-    const v4i* iw = reinterpret_cast<const v4i*>(I) + (mb0 / RB + w) * nkt * 64;
-    // B: the step's 128 X rows, row n = 8 (w + 4i) + l / 8 loaded by this
+    const uint32_t* iw = I + ((mb0 + RB * w) / 4 * nkt * 64) * 4 + (RB * w) % 4;
+    // B: the step's 128 X rows, row n = 8 (w + NW i) + l / 8 loaded by this
     // lane (16-byte chunk (l % 8) ^ xrow_swizzle(n) of the tile's 128
-    // columns): base bw + 128 ldb per step, lane offset boff[i]
+    // columns), RB loads per wave: base bw + 128 ldb per step, lane offset
+    // boff[i]
     const int8_t* bw = B + n0 + (int64_t)8 * w * ldb;
-    int boff[4];
+    int boff[RB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int n = 8 * (w + 4 * i) + (l >> 3);
+    for (int i = 0; i < RB; ++i) {
+        const int n = 8 * (w + NW * i) + (l >> 3);
         const int chunk = (l & 7) ^ xrow_swizzle(n);
-        boff[i] = (int)((int64_t)(32 * i + (l >> 3)) * ldb) + 16 * chunk;
+        boff[i] = (int)((int64_t)(8 * NW * i + (l >> 3)) * ldb) + 16 * chunk;
     }
-    v4i ar[kRSlots][RB];
-    vrb ir[kRSlots];
+    v4i ar[SLOTS][RB];
+    vrb ir[SLOTS];
     // the nine loads of step TS (a compile-time step, below nkt) into slot
     // and stage TS % 8
     auto issue = [&](auto tc) {
-        constexpr int ts = decltype(tc)::value, u = ts % kRSlots;
+        constexpr int ts = decltype(tc)::value, u = ts % SLOTS;
         char* st = stage(std::integral_constant<int, u>{});
 #pragma unroll
         for (int i = 0; i < RB; ++i) ar[u][i] = aw[(i * nkt + ts) * 64 + l];
-        ir[u] = *reinterpret_cast<const vrb*>(iw + ts * 64 + l);
+        ir[u] = *reinterpret_cast<const vrb*>(iw + (ts * 64 + l) * 4);
         const int8_t* bs = bw + (int64_t)ts * 128 * ldb;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RB; ++i)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const v4i*>(bs + boff[i]),
-                                             PFR_LDS(st + 8 * (w + 4 * i) * 128), 16, 0, 0);
+                                             PFR_LDS(st + 8 * (w + NW * i) * 128), 16, 0, 0);
     };
     // B fragment of column block j from a stage (see k_sp24_i8, XROW form)
     const int trk = (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
@@ -755,24 +767,24 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
         issue(tc);
         __builtin_amdgcn_sched_barrier(0);
     };
-    static_assert(nkt > sr_last(0), "the prologue issues seven steps");
+    static_assert(nkt > sr_last<LEAD>(0), "the prologue issues seven steps");
     prologue_issue(std::integral_constant<int, 0>{});
     __builtin_amdgcn_s_barrier();
-    static_for<1, sr_last(0) + 1>([&](auto tc) { prologue_issue(tc); });
-    __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * sr_last(0)));
+    static_for<1, sr_last<LEAD>(0) + 1>([&](auto tc) { prologue_issue(tc); });
+    __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * sr_last<LEAD>(0)));
     __builtin_amdgcn_s_barrier();
     fetch_b(bq[0], b0, 0);
     fetch_b(bq[1], b0, 1);
     fetch_b(bq[2], b0, 2);
     // step S (compile-time)
     auto step = [&](auto sc) {
-        constexpr int S = decltype(sc)::value, u = S % kRSlots, un = (u + 1) % kRSlots;
-        constexpr int first = sr_last(S) + 1, last = std::min(sr_last(S + 1), nkt - 1);
+        constexpr int S = decltype(sc)::value, u = S % SLOTS, un = (u + 1) % SLOTS;
+        constexpr int first = sr_last<LEAD>(S) + 1, last = std::min(sr_last<LEAD>(S + 1), nkt - 1);
         // even steps wait for steps S + 1 and S + 2 (the loads issued after
         // them may still be in flight) and meet at the barrier; odd steps
         // read stage S + 1, already waited for, and load without a barrier
         constexpr bool SYNC = S % 2 == 0;
-        constexpr int later = std::max(0, std::min(sr_last(S), nkt - 1) - S - 2);  // issued after step S + 2
+        constexpr int later = std::max(0, std::min(sr_last<LEAD>(S), nkt - 1) - S - 2);  // issued after step S + 2
         const char* cur = stage(std::integral_constant<int, u>{});
         const char* nxt = stage(std::integral_constant<int, un>{});
         __builtin_amdgcn_sched_barrier(0);
@@ -813,7 +825,15 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_i8r(
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);  // the repeated loads have landed
     __builtin_amdgcn_s_barrier();
-    char* tile = (w == 0 ? b0 : (w == 1 ? b2 : (w == 2 ? b4 : b6))) - w * 16 * RB * 128;
+    // wave w's epilogue rows go to a stage of its own (every second one for
+    // four waves)
+    char* own;
+    if constexpr (NW == 4) {
+        own = w == 0 ? b0 : (w == 1 ? b2 : (w == 2 ? b4 : b6));
+    } else {
+        own = w == 0 ? b0 : w == 1 ? b1 : w == 2 ? b2 : w == 3 ? b3 : w == 4 ? b4 : w == 5 ? b5 : w == 6 ? b6 : b7;
+    }
+    char* tile = own - w * 16 * RB * 128;
     float wsv[RB][4];
     if constexpr (OUT != PFR_SP24_OUT_I32) {
 #pragma unroll
@@ -1439,10 +1459,10 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
                        x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
     const int64_t rtiles = (W->M + 64 * kRB - 1) / (64 * kRB);  // 256-row tiles (64 * kRB rows)
     const dim3 rgrid((unsigned)(rtiles * ntn));
-#define PFR_SP24_LAUNCH_R(OUTK)                                                                                \
-    hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32, kRB>), rgrid, dim3(kI8Threads), 0, ctx->stream, nkt, A, W->idxw, B, ldb, \
-                       (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, x_zp,   \
-                       x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
+#define PFR_SP24_LAUNCH_R(OUTK)                                                                                 \
+    hipLaunchKernelGGL((k_sp24_i8r<OUTK, 32, kRB8>), rgrid, dim3(64 * 16 / kRB8), 0, ctx->stream, nkt, A, W->idxw, \
+                       B, ldb, (int)W->M, (int)N, W->w_scale, x_scale, inv_out, out_zp, inrange, Y, ldy, yvec, ntn, \
+                       x_zp, x_u8 ? 128 : 0, xs_dev, zp_dev, W->row_sum)
     // the register-streamed kernel for the X-row form at 32 k steps, when
     // its tiles stay inside the packed rows and its per-lane B offsets (up to
     // 128 rows of X) fit in 32 bits
