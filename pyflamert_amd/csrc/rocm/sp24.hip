@@ -801,7 +801,10 @@ __global__ __launch_bounds__(64 * (16 / RB), 1) void k_sp24_i8r(
         });
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (SYNC) {
-            __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * later));
+            // vmcnt only: the stage reuse needs this wave's loads and every
+            // wave at the barrier, not its fragment reads of stage s, which
+            // keep flowing through the barrier (lgkmcnt left alone)
+            __builtin_amdgcn_s_waitcnt(vm_wait(kRLoads * later) | (0xF << 8));
             __builtin_amdgcn_s_barrier();
         }
         __builtin_amdgcn_sched_barrier(0);
