@@ -32,21 +32,18 @@ constexpr int kRedBlocks = 1024;  // partial min/max pairs
 struct DqlState {
     float part_min[kRedBlocks];
     float part_max[kRedBlocks];
-    float inv_scale;
-    int32_t zp;
 };
 
-__global__ __launch_bounds__(kRedThreads) void k_dql_minmax(const float* __restrict__ x, int64_t n,
-                                                             DqlState* __restrict__ st) {
-    __shared__ float smin[kRedThreads], smax[kRedThreads];
-    float mn = FLT_MAX, mx = -FLT_MAX;
-    for (int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kRedThreads) {
-        const float v = x[i];
-        if (isfinite(v)) {
-            mn = v < mn ? v : mn;
-            mx = mx < v ? v : mx;
-        }
+// min and max over the finite values of `v`
+__device__ __forceinline__ void dql_take(float v, float& mn, float& mx) {
+    if (isfinite(v)) {
+        mn = v < mn ? v : mn;
+        mx = mx < v ? v : mx;
     }
+}
+
+// min and max over a block's threads' values (all threads call it)
+__device__ __forceinline__ void dql_block_reduce(float& mn, float& mx, float* smin, float* smax) {
     smin[threadIdx.x] = mn;
     smax[threadIdx.x] = mx;
     __syncthreads();
@@ -58,19 +55,55 @@ __global__ __launch_bounds__(kRedThreads) void k_dql_minmax(const float* __restr
         }
         __syncthreads();
     }
+    mn = smin[0];
+    mx = smax[0];
+}
+
+// Pass 1 of DynamicQuantizeLinear: each block's min and max over the finite
+// values (float4 loads when x is 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kRedThreads) void k_dql_minmax(const float* __restrict__ x, int64_t n,
+                                                             DqlState* __restrict__ st) {
+    __shared__ float smin[kRedThreads], smax[kRedThreads];
+    float mn = FLT_MAX, mx = -FLT_MAX;
+    const int64_t stride = (int64_t)gridDim.x * kRedThreads;
+    int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x;
+    if constexpr (VEC) {
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        const int64_t n4 = n / 4;
+        for (; i < n4; i += stride) {
+            const float4 v = x4[i];
+            dql_take(v.x, mn, mx);
+            dql_take(v.y, mn, mx);
+            dql_take(v.z, mn, mx);
+            dql_take(v.w, mn, mx);
+        }
+        i = 4 * n4 + (int64_t)blockIdx.x * kRedThreads + threadIdx.x;  // the last n % 4
+    }
+    for (; i < n; i += stride) dql_take(x[i], mn, mx);
+    dql_block_reduce(mn, mx, smin, smax);
     if (threadIdx.x == 0) {
-        st->part_min[blockIdx.x] = smin[0];
-        st->part_max[blockIdx.x] = smax[0];
+        st->part_min[blockIdx.x] = mn;
+        st->part_max[blockIdx.x] = mx;
     }
 }
 
-// One block: the parameters, written to the op's scale and zero-point
-// outputs and kept (inverse scale, zero point) for the quantize kernel.
-// status (optional): 0, or 1 when the scale is not finite (the error
-// QuantParams::per_tensor raises).
-__global__ __launch_bounds__(kRedThreads) void k_dql_params(int nparts, DqlState* __restrict__ st,
-                                                             float* __restrict__ scale_out,
-                                                             uint8_t* __restrict__ zp_out, int32_t* status) {
+__device__ __forceinline__ uint32_t dql_q(float v, float inv, int32_t zp) {
+    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(v * inv)) + (uint32_t)zp);
+    return (uint32_t)(q < 0 ? 0 : (q > 255 ? 255 : q));
+}
+
+// Pass 2: every block reduces the nparts partials to the parameters (block 0
+// also writes them to the op's scale and zero-point outputs and the status),
+// then quantizes its share of x: four values per thread (one float4 in, four
+// bytes out) when x and y allow it.  nparts == 0 (an empty tensor) gives
+// scale 1 and zero point 0.  status (optional): 0, or 1 when the scale is
+// not finite (the error QuantParams::per_tensor raises).
+template <bool VEC>
+__global__ __launch_bounds__(kRedThreads) void k_dql_quant(const float* __restrict__ x, int64_t n, int nparts,
+                                                           const DqlState* __restrict__ st, uint8_t* __restrict__ y,
+                                                           float* __restrict__ scale_out, uint8_t* __restrict__ zp_out,
+                                                           int32_t* status) {
     __shared__ float smin[kRedThreads], smax[kRedThreads];
     float mn = FLT_MAX, mx = -FLT_MAX;
     for (int i = threadIdx.x; i < nparts; i += kRedThreads) {
@@ -78,43 +111,33 @@ __global__ __launch_bounds__(kRedThreads) void k_dql_params(int nparts, DqlState
         mn = a < mn ? a : mn;
         mx = mx < b ? b : mx;
     }
-    smin[threadIdx.x] = mn;
-    smax[threadIdx.x] = mx;
-    __syncthreads();
-    for (int off = kRedThreads / 2; off > 0; off >>= 1) {
-        if (threadIdx.x < off) {
-            const float a = smin[threadIdx.x + off], b = smax[threadIdx.x + off];
-            smin[threadIdx.x] = a < smin[threadIdx.x] ? a : smin[threadIdx.x];
-            smax[threadIdx.x] = smax[threadIdx.x] < b ? b : smax[threadIdx.x];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x != 0) return;
-    const float min_val = smin[0], max_val = smax[0];
+    dql_block_reduce(mn, mx, smin, smax);
     float scale = 1.0f;
     int32_t zp = 0;
-    if (nparts > 0 && !(min_val > max_val) && !(fabsf(max_val - min_val) < 1e-8f)) {
-        scale = (max_val - min_val) / 255.0f;
-        zp = (int32_t)(0u - (uint32_t)pfr::f2i_trunc_x86(roundf(min_val / scale)));  // x86 wraps
+    if (nparts > 0 && !(mn > mx) && !(fabsf(mx - mn) < 1e-8f)) {
+        scale = (mx - mn) / 255.0f;
+        zp = (int32_t)(0u - (uint32_t)pfr::f2i_trunc_x86(roundf(mn / scale)));  // x86 wraps
         zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
         if (scale < 1e-10f) scale = 1e-10f;
     }
-    if (status) *status = (scale > 0.0f && isfinite(scale)) ? 0 : 1;
-    st->inv_scale = 1.0f / scale;
-    st->zp = zp;
-    *scale_out = scale;
-    *zp_out = (uint8_t)zp;
-}
-
-__global__ __launch_bounds__(256) void k_dql_quant(const float* __restrict__ x, int64_t n,
-                                                   const DqlState* __restrict__ st, uint8_t* __restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const float inv = st->inv_scale;
-    const int32_t zp = st->zp;
-    int32_t q = (int32_t)((uint32_t)pfr::f2i_trunc_x86(roundf(x[i] * inv)) + (uint32_t)zp);
-    q = q < 0 ? 0 : (q > 255 ? 255 : q);
-    y[i] = (uint8_t)q;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (status) *status = (scale > 0.0f && isfinite(scale)) ? 0 : 1;
+        *scale_out = scale;
+        *zp_out = (uint8_t)zp;
+    }
+    const float inv = 1.0f / scale;
+    const int64_t stride = (int64_t)gridDim.x * kRedThreads;
+    int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x;
+    if constexpr (VEC) {
+        const int64_t n4 = n / 4;
+        for (; i < n4; i += stride) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            reinterpret_cast<uint32_t*>(y)[i] =
+                dql_q(v.x, inv, zp) | dql_q(v.y, inv, zp) << 8 | dql_q(v.z, inv, zp) << 16 | dql_q(v.w, inv, zp) << 24;
+        }
+        i = 4 * n4 + (int64_t)blockIdx.x * kRedThreads + threadIdx.x;
+    }
+    for (; i < n; i += stride) y[i] = (uint8_t)dql_q(x[i], inv, zp);
 }
 
 // Per-tensor quantize (quantize_tensor, quant_ops.cpp:15-57): inv = 1 /
@@ -184,11 +207,22 @@ void dql_dev(pfr_ctx* ctx, const float* x, int64_t n, uint8_t* y, float* scale, 
     pfr::require(scale && zp, "null scale/zero-point output");
     pfr::require(n == 0 || (x && y), "null x/y");
     DqlState* st = static_cast<DqlState*>(ctx->scratch[4].ensure(sizeof(DqlState)));
-    const int nparts = n == 0 ? 0 : (int)std::min<int64_t>(kRedBlocks, (n + kRedThreads - 1) / kRedThreads);
     hipStream_t q = ctx->stream;
-    if (nparts) hipLaunchKernelGGL(k_dql_minmax, dim3(nparts), dim3(kRedThreads), 0, q, x, n, st);
-    hipLaunchKernelGGL(k_dql_params, dim3(1), dim3(kRedThreads), 0, q, nparts, st, scale, zp, status);
-    if (n) hipLaunchKernelGGL(k_dql_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, q, x, n, st, y);
+    const bool vx = n > 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool vy = vx && (reinterpret_cast<uintptr_t>(y) & 3) == 0;
+    const int64_t per = vx ? 4 * kRedThreads : kRedThreads;  // elements per block and pass
+    const int nparts = n == 0 ? 0 : (int)std::min<int64_t>(kRedBlocks, (n + per - 1) / per);
+    if (nparts) {
+        if (vx) hipLaunchKernelGGL(k_dql_minmax<true>, dim3(nparts), dim3(kRedThreads), 0, q, x, n, st);
+        else hipLaunchKernelGGL(k_dql_minmax<false>, dim3(nparts), dim3(kRedThreads), 0, q, x, n, st);
+    }
+    // the quantize pass: about a block per CU-slot, each reducing the
+    // partials (nparts x 8 B from L2) before its share of x
+    const int qb = (int)std::max<int64_t>(1, std::min<int64_t>(512, (n + 4 * kRedThreads - 1) / (4 * kRedThreads)));
+    if (vy)
+        hipLaunchKernelGGL(k_dql_quant<true>, dim3(qb), dim3(kRedThreads), 0, q, x, n, nparts, st, y, scale, zp, status);
+    else
+        hipLaunchKernelGGL(k_dql_quant<false>, dim3(qb), dim3(kRedThreads), 0, q, x, n, nparts, st, y, scale, zp, status);
     PFR_HIP(hipGetLastError());
 }
 

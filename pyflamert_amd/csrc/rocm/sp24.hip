@@ -1048,12 +1048,28 @@ __global__ __launch_bounds__(kI8Threads, 1) void k_sp24_bf16p(int nkt, const v4i
         }
 }
 
-// x - 128 as int8 for uint8 x (rows of n bytes, ld apart, to a compact copy)
+// x - 128 as int8 for uint8 x (K rows of N bytes, ldx apart, to a compact
+// copy): VEC (N and ldx multiples of 16, X 16-byte aligned) flips 16 bytes
+// per thread, otherwise one byte per thread, blockIdx.y striding the rows.
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_flip_sign(const uint8_t* __restrict__ X, int64_t K, int64_t N,
                                                    int64_t ldx, uint8_t* __restrict__ Y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= K * N) return;
-    Y[i] = X[(i / N) * ldx + i % N] ^ 0x80u;
+    if constexpr (VEC) {
+        const int64_t cpr = N / 16, total = K * cpr;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+            const int64_t r = i / cpr, c = i - r * cpr;
+            uint4 v = *reinterpret_cast<const uint4*>(X + r * ldx + 16 * c);
+            v.x ^= 0x80808080u;
+            v.y ^= 0x80808080u;
+            v.z ^= 0x80808080u;
+            v.w ^= 0x80808080u;
+            *reinterpret_cast<uint4*>(Y + r * N + 16 * c) = v;
+        }
+    } else {
+        const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        if (n >= N) return;
+        for (int64_t r = blockIdx.y; r < K; r += gridDim.y) Y[r * N + n] = X[r * ldx + n] ^ 0x80u;
+    }
 }
 
 // ---- host -----------------------------------------------------------------
@@ -1426,8 +1442,13 @@ void gemm_i8_dev(pfr_ctx* ctx, const pfr_sp24* W, const int8_t* X, int64_t N, in
     if (x_u8) {
         // the signed MFMA takes x - 128; the zero-point correction adds the 128 back
         uint8_t* xs8 = static_cast<uint8_t*>(ctx->scratch[1].ensure((size_t)(W->K * N) + 16));
-        hipLaunchKernelGGL(k_flip_sign, dim3((unsigned)((W->K * N + 255) / 256)), dim3(256), 0, ctx->stream,
-                           reinterpret_cast<const uint8_t*>(X), W->K, N, ldx, xs8);
+        if (N % 16 == 0 && ldx % 16 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0)
+            hipLaunchKernelGGL(k_flip_sign<true>,
+                               dim3((unsigned)std::min<int64_t>(4096, (W->K * (N / 16) + 255) / 256)), dim3(256), 0,
+                               ctx->stream, reinterpret_cast<const uint8_t*>(X), W->K, N, ldx, xs8);
+        else
+            hipLaunchKernelGGL(k_flip_sign<false>, dim3((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(W->K, 1024)),
+                               dim3(256), 0, ctx->stream, reinterpret_cast<const uint8_t*>(X), W->K, N, ldx, xs8);
         PFR_HIP(hipGetLastError());
         X = reinterpret_cast<const int8_t*>(xs8);
         ldx = N;
