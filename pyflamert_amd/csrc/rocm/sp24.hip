@@ -216,6 +216,17 @@ constexpr int kLdsA = 16 * 64 * 16, kLdsI = 16 * 64 * 4, kLdsB = 128 * 128;
 constexpr int kStage = kLdsA + kLdsI + kLdsB;  // 36 KiB
 
 #define PFR_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// word 3 of a raw buffer resource on CDNA (32-bit data format, no swizzle)
+constexpr int kBufWord3 = 0x00020000;
+
+// 16 bytes per lane from base + off (base wave-uniform) to LDS dst + 16 lane,
+// as a buffer load: the compiler counts a global direct-to-LDS load as a
+// flat access that may finish out of order and then turns every later wait
+// on the LDS counter into a wait for all LDS reads while one is in flight.
+__device__ __forceinline__ void lds_copy16(const void* base, int off, __attribute__((address_space(3))) void* dst) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kBufWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, off, 0, 0, 0);
+}
 
 // B source: XROW = false reads XT (Np x Kp, the transposed activation),
 // XROW = true reads the row-major activation X itself (K % 512 == 0,
@@ -722,9 +733,7 @@ __global__ __launch_bounds__(64 * (16 / RB), 1) void k_sp24_i8r(
         ir[u] = *reinterpret_cast<const vrb*>(iw + (ts * 64 + l) * 4);
         const int8_t* bs = bw + (int64_t)ts * 128 * ldb;
 #pragma unroll
-        for (int i = 0; i < RB; ++i)
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const v4i*>(bs + boff[i]),
-                                             PFR_LDS(st + 8 * (w + NW * i) * 128), 16, 0, 0);
+        for (int i = 0; i < RB; ++i) lds_copy16(bs, boff[i], PFR_LDS(st + 8 * (w + NW * i) * 128));
     };
     // B fragment of column block j from a stage (see k_sp24_i8, XROW form)
     const int trk = (16 * kb + (c >> 1)) * 128 + 8 * (c & 1);
