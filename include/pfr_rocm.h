@@ -17,8 +17,11 @@
  *                    sparse_matmul (math.cpp:268-438, sparse_tensor.cpp:473-554):
  *                    each output is the ascending-k sequence of separately
  *                    rounded products and sums, bias added last.
- *   PFR_MODE_FAST    same order with fused multiply-add (one rounding per
- *                    term); close to, not equal to, the reference.
+ *   PFR_MODE_FAST    fused multiply-add (one rounding per term) in an order
+ *                    the kernel chooses (wave-parallel partial sums; the
+ *                    column-slice kernel also takes a row's terms in an order
+ *                    that spreads its LDS reads over the banks); close to,
+ *                    not equal to, the reference.
  *   int8 paths       int32 accumulators and requantised int8 bit-exact to
  *                    quantized_matmul + quantize_tensor (quant_ops.cpp:387-506,
  *                    :15-127).
@@ -149,8 +152,10 @@ int pfr_csr_info(const pfr_csr* w, int64_t* M, int64_t* K, int64_t* nnz);
 /* Device bytes the handle holds: the CSR itself (row pointers, columns as
  * uint16 when K <= 65536 and int32 otherwise, values, row scales), the
  * row-block table, the merge-path partition and every derived copy built so
- * far.  The sliced-ELL copy (float32 weights, N >= 16), the row-chain copy
- * (strict, N <= 8) and the nnz-balanced copy (fast, N <= 8) are built by the
+ * far.  The sliced-ELL copy (float32 weights, N >= 16; one in storage order
+ * for the strict mode, one reordered for the fast mode, sharing their slab
+ * tables), the row-chain copy (strict, N <= 8) and the nnz-balanced copy
+ * (fast, N <= 8) are built by the
  * first product through the handle that would use one: that call plans on
  * the host, allocates, fills on the device and synchronizes the handle's
  * stream.  While that stream is being captured into a graph, and in

@@ -154,6 +154,14 @@ struct pfr_csr {
     int32_t* sell_perm = nullptr;  // [sell_nslab * kSellRows] row of each slab lane, -1 none
     int32_t* sell_soff = nullptr;  // [sell_nslab * (sell_nch + 1)]
     int4* sell_blk = nullptr;      // [sell_len + kSellTail]
+    // The same runs for the fast mode (reassociated sums), each row's steps
+    // of a chunk reordered so that at every step the four slab rows whose
+    // 16-byte X reads the LDS serves together ({0, 3, 5, 6}, {1, 2, 4, 7},
+    // {8, 11, 13, 14}, {9, 10, 12, 15}) take X rows in different bank
+    // quarters (column % 4) where their counts allow; null until a fast
+    // product builds it.  Either copy may exist without the other; the
+    // tables above serve both.
+    int4* sell_blk_fast = nullptr;  // [sell_len + kSellTail]
     int32_t sell_nslab = 0, sell_nch = 0, sell_kc = 0;
     int64_t sell_len = 0;
     // Row-chain copy for the in-order vector kernels (few columns, strict):
@@ -258,7 +266,7 @@ namespace pfr {
 // Makes ctx's device current (cheap when it already is).
 void bind(pfr_ctx* ctx);
 // Derived copies of a CSR weight, built on first use.
-constexpr uint32_t kCopySell = 1, kCopyChain = 2, kCopyBal = 4;
+constexpr uint32_t kCopySell = 1, kCopyChain = 2, kCopyBal = 4, kCopySellFast = 8;
 // Builds the copies among `which` that w still has pending, on w's context
 // stream (allocates, plans on the host and fills on the device, then
 // synchronizes).  A copy whose plan does not fit is dropped from pending and

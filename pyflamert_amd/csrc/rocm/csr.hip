@@ -71,7 +71,8 @@ T* walloc_copy(pfr_csr* w, const T* host, int64_t count, hipStream_t s) {
 void free_csr(pfr_csr* w) {
     if (!w) return;
     for (void* p : {(void*)w->rowptr, (void*)w->col, w->val, (void*)w->row_scale, (void*)w->spmv_blocks,
-                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->chain_q0, (void*)w->col16,
+                    (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->sell_blk_fast,
+                    (void*)w->chain_q0, (void*)w->col16,
                     (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col, (void*)w->bal_meta,
                     (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col, (void*)w->pattern,
                     (void*)w->mp_wave, (void*)w->mp_wmeta, (void*)w->mp_grp, (void*)w->mp_xchg,
@@ -751,6 +752,104 @@ __global__ __launch_bounds__(256) void k_sell_fill(int64_t npos, const int32_t* 
     }
 }
 
+// The 24 orders of the four column classes mod 4, two bits per row of a group.
+__constant__ uint8_t kClassPerms[24] = {0xE4, 0xB4, 0xD8, 0x78, 0x9C, 0x6C, 0xE1, 0xB1, 0xC9, 0x39, 0x8D, 0x2D,
+                                        0xD2, 0x72, 0xC6, 0x36, 0x4E, 0x1E, 0x93, 0x63, 0x87, 0x27, 0x4B, 0x1B};
+// Slab rows (r & 7) of each LDS read group: lanes 4r .. 4r + 3 of the rows
+// with r >> 3 == h and an even (group 2h) or odd (2h + 1) number of bits set
+// in r & 7 are served together.
+__constant__ uint8_t kReadGroupRows[2][4] = {{0, 3, 5, 6}, {1, 2, 4, 7}};
+
+// Fast-mode sliced-ELL fill (pfr_csr::sell_blk_fast), one thread per
+// (slab, LDS read group, chunk): the layout of k_sell_fill, but each row of
+// the group takes its chunk's entries in an order of its own.  A column's X
+// row in the chunk's LDS copy starts 64 (column % kc) bytes in, so its 16
+// banks are one quarter of the 64, column % 4.  A step's 16-byte reads
+// (lane 4r + q: bytes 16q .. 16q + 15 of slab row r's X row) are served four
+// slab rows at a time, the rows {0, 3, 5, 6}, {1, 2, 4, 7}, {8, 11, 13, 14}
+// and {9, 10, 12, 15} (measured: a probe of 16-byte reads runs at about 230
+// B per clock per CU when each of these groups' rows take distinct
+// quarters, whatever else repeats, and at 132 when the consecutive rows
+// 4g .. 4g + 3 do instead).  So at each step the group's rows that still
+// have entries get, over the 24 orders of the quarters, the assignment with
+// the most rows on a quarter of their own (a row past its entries reads the
+// zero row, quarter 0, which the others then avoid), ties going to the
+// rows' fullest quarters; a row left without a quarter of its own takes its
+// fullest one.  Every row still takes one entry per step, so the runs keep
+// their lengths and padding; only the order of a row's terms changes, which
+// the fast mode's reassociated sums allow.
+template <class CI>
+__global__ __launch_bounds__(256) void k_sell_fill_fast(int64_t nthr, int nch, int kc,
+                                                        const int32_t* __restrict__ perm,
+                                                        const int32_t* __restrict__ rowptr, const CI* __restrict__ col,
+                                                        const float* __restrict__ val,
+                                                        const int32_t* __restrict__ soff, int4* __restrict__ blk) {
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= nthr) return;
+    const int c = (int)(id % nch);
+    const int64_t sg = id / nch, sl = sg / 4;
+    const int g = (int)(sg % 4);
+    const int32_t k0 = c * kc;
+    int sr[4];  // the group's slab rows
+    int32_t cur[4][4], cnt[4][4], n[4];
+    int32_t T = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sr[i] = 8 * (g >> 1) + kReadGroupRows[g & 1][i];
+        const int32_t row = perm[sl * pfr::kSellRows + sr[i]];
+        int32_t b = 0, e = 0;
+        if (row >= 0) {
+            const int32_t rb = rowptr[row], re = rowptr[row + 1];
+            b = first_at_least(col, rb, re, k0);
+            e = first_at_least(col, b, re, k0 + kc);
+        }
+        n[i] = e - b;
+        T = max(T, n[i]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cur[i][q] = b, cnt[i][q] = 0;
+        for (int32_t j = b; j < e; ++j) {
+            const int q = (int)(col[j] & 3);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) cnt[i][u] += u == q ? 1 : 0;
+        }
+    }
+    int4* run = blk + soff[sl * (nch + 1) + c];
+    for (int32_t t = 0; t < T; ++t) {
+        const bool pad = n[0] <= t || n[1] <= t || n[2] <= t || n[3] <= t;
+        int best = 0, best_score = -1;
+        for (int pi = 0; pi < 24; ++pi) {
+            const int code = kClassPerms[pi];
+            int score = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = (code >> (2 * i)) & 3;
+                if (t < n[i] && cnt[i][q] > 0 && !(pad && q == 0)) score += (1 << 16) + cnt[i][q];
+            }
+            if (score > best_score) best_score = score, best = code;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (t >= n[i]) continue;
+            int q = (best >> (2 * i)) & 3;
+            if (cnt[i][q] == 0 || (pad && q == 0)) {  // no quarter of its own: the fullest
+                int m = -1;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = cnt[i][u] * 2 + (pad && u == 0 ? 0 : 1);
+                    if (cnt[i][u] > 0 && v > m) m = v, q = u;
+                }
+            }
+            int32_t j = cur[i][q];
+            while ((int)(col[j] & 3) != q) ++j;
+            cur[i][q] = j + 1;
+            --cnt[i][q];
+            int32_t* dst = reinterpret_cast<int32_t*>(run + (t / 8) * 64 + 4 * sr[i] + (t % 8) / 2) + (t % 2) * 2;
+            dst[0] = ((int32_t)col[j] - k0) * 64;
+            dst[1] = __float_as_int(val[j]);
+        }
+    }
+}
+
 // Row-chain fill, one wave per sorted position i (row perm[i], slab i / R,
 // lane i % R): step t of the row goes to entry t % 4 of quad row
 // q0[slab] + t / 4, lane i % R, with its column times mul (4: byte offsets
@@ -845,7 +944,8 @@ void set_lazy(pfr_csr* w, const std::vector<int32_t>& rowptr, std::vector<int32_
               std::vector<int32_t> bal_cnt) {
     uint32_t bits = 0;
     if (w->M > 0 && w->nnz > 0) {
-        bits = pfr::kCopyChain | (sell_cnt.empty() ? 0u : pfr::kCopySell) | (bal_cnt.empty() ? 0u : pfr::kCopyBal);
+        bits = pfr::kCopyChain | (sell_cnt.empty() ? 0u : pfr::kCopySell | pfr::kCopySellFast) |
+               (bal_cnt.empty() ? 0u : pfr::kCopyBal);
         w->h_rowptr = rowptr;
         w->h_sell_cnt = std::move(sell_cnt);
         w->h_bal_cnt = std::move(bal_cnt);
@@ -867,7 +967,7 @@ void fill_sell(pfr_csr* w, const CI* col, hipStream_t s) {
     w->sell_blk = walloc<int4>(w, p.len + pfr::kSellTail);
     const int32_t pad = (int32_t)(p.kc * 64);
     fill_dev(w->sell_blk, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
-    set_sell(w, p, s);
+    if (w->sell_perm == nullptr) set_sell(w, p, s);  // else the fast copy's build uploaded them
     int64_t* off = dev_alloc_copy(p.off.data(), (int64_t)p.off.size(), s);
     const int64_t npos = p.nslab * pfr::kSellRows;  // perm's length
     hipLaunchKernelGGL(k_sell_fill<CI>, dim3(waves_grid(npos)), dim3(256), 0, s, npos, w->sell_perm, w->rowptr, col,
@@ -876,6 +976,24 @@ void fill_sell(pfr_csr* w, const CI* col, hipStream_t s) {
     (void)hipStreamSynchronize(s);
     (void)hipFree(off);
     if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_sell_fill: ") + hipGetErrorString(e));
+}
+
+// The fast mode's sliced-ELL copy: the same plan and tables (uploaded here
+// when the strict copy has not), its runs filled by k_sell_fill_fast.
+template <class CI>
+void fill_sell_fast(pfr_csr* w, const CI* col, hipStream_t s) {
+    SellPlan p;
+    if (!plan_sell(w->M, w->K, w->h_sell_cnt, &p)) return;
+    w->sell_blk_fast = walloc<int4>(w, p.len + pfr::kSellTail);
+    const int32_t pad = (int32_t)(p.kc * 64);
+    fill_dev(w->sell_blk_fast, p.len + pfr::kSellTail, make_int4(pad, 0, pad, 0), s);
+    if (w->sell_perm == nullptr) set_sell(w, p, s);
+    const int64_t nthr = p.nslab * 4 * p.nch;
+    hipLaunchKernelGGL(k_sell_fill_fast<CI>, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, nthr,
+                       (int)p.nch, (int)p.kc, w->sell_perm, w->rowptr, col, static_cast<const float*>(w->val),
+                       w->sell_soff, w->sell_blk_fast);
+    PFR_HIP(hipGetLastError());
+    PFR_HIP(hipStreamSynchronize(s));
 }
 
 // Row-chain copy; V is the value type (float or int8).
@@ -939,6 +1057,7 @@ template <class CI>
 void build_copy(pfr_csr* w, uint32_t bit, const CI* col, hipStream_t s) {
     const bool i8 = w->vdt == PFR_I8;
     if (bit == pfr::kCopySell) fill_sell(w, col, s);  // pending for float32 weights only
+    else if (bit == pfr::kCopySellFast) fill_sell_fast(w, col, s);  // likewise
     else if (bit == pfr::kCopyChain) i8 ? fill_chain<CI, int8_t>(w, col, s) : fill_chain<CI, float>(w, col, s);
     else i8 ? fill_bal<CI, int8_t>(w, col, s) : fill_bal<CI, float>(w, col, s);
 }
@@ -951,10 +1070,13 @@ void free_null(P*& p) {
 
 // Frees a copy left part-built by a failed build.
 void drop_copy(pfr_csr* w, uint32_t bit) {
-    if (bit == pfr::kCopySell) {
-        free_null(w->sell_perm), free_null(w->sell_soff), free_null(w->sell_blk);
-        w->sell_nslab = w->sell_nch = w->sell_kc = 0;
-        w->sell_len = 0;
+    if (bit == pfr::kCopySell || bit == pfr::kCopySellFast) {
+        free_null(bit == pfr::kCopySell ? w->sell_blk : w->sell_blk_fast);
+        if (w->sell_blk == nullptr && w->sell_blk_fast == nullptr) {  // the tables serve neither copy now
+            free_null(w->sell_perm), free_null(w->sell_soff);
+            w->sell_nslab = w->sell_nch = w->sell_kc = 0;
+            w->sell_len = 0;
+        }
     } else if (bit == pfr::kCopyChain) {
         free_null(w->chain_q0), free_null(w->chain_len), free_null(w->chain_perm);
         free_null(w->chain_val), free_null(w->chain_col);
@@ -1136,7 +1258,7 @@ void csr_build_copies(pfr_csr* w, uint32_t which) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     PFR_HIP(hipStreamIsCapturing(s, &st));
     if (st != hipStreamCaptureStatusNone) return;
-    for (const uint32_t bit : {kCopySell, kCopyChain, kCopyBal}) {
+    for (const uint32_t bit : {kCopySell, kCopySellFast, kCopyChain, kCopyBal}) {
         if ((which & bit) == 0) continue;
         const int64_t before = w->dev_bytes;
         try {

@@ -2048,6 +2048,11 @@ int next_pow2(int n) {
 }
 
 
+// The sliced-ELL runs a product in this mode reads (null: neither copy).
+const int4* sell_runs(const pfr_csr* W, bool fast) {
+    return fast && W->sell_blk_fast != nullptr ? W->sell_blk_fast : W->sell_blk;
+}
+
 // Column-slice kernel launch with W waves per workgroup.
 template <bool FAST, bool XVEC, int W, bool XT>
 void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64_t ldx, float* Y,
@@ -2065,7 +2070,7 @@ void launch_sell_w(pfr_ctx* ctx, const pfr_csr* Wt, const float* X, int N, int64
     }
     dim3 grid((unsigned)((Wt->sell_nslab + W - 1) / W), (unsigned)((N + pfr::kSellCols - 1) / pfr::kSellCols));
     hipLaunchKernelGGL(kern, grid, dim3(sell_threads<XVEC, W, XT>()), lds, ctx->stream, N, (int)Wt->K,
-                       Wt->sell_kc, Wt->sell_nch, Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, Wt->sell_blk, X, ldx,
+                       Wt->sell_kc, Wt->sell_nch, Wt->sell_nslab, Wt->sell_perm, Wt->sell_soff, sell_runs(Wt, FAST), X, ldx,
                        Y, ldy_r, ldy_c, yvec, bias, c_size, beta, act, alpha, alpha != 1.0f ? 1 : 0);
 }
 
@@ -2280,9 +2285,12 @@ __global__ __launch_bounds__(256) void k_nonfinite_fix(const float* __restrict__
     }
 }
 
-// The column-slice kernel serves this product (float32 weight, N >= 16).
-bool sell_serves(const pfr_csr* W, int64_t N) {
-    return W->vdt != PFR_I8 && N >= kSellMinN && W->sell_blk != nullptr && N < (int64_t)pfr::kSellCols * 65535;
+// The column-slice kernel serves this product (float32 weight, N >= 16):
+// the fast mode runs on either sliced-ELL copy (its own when built), the
+// strict mode on the storage-order one.
+bool sell_serves(const pfr_csr* W, int64_t N, bool fast) {
+    return W->vdt != PFR_I8 && N >= kSellMinN && sell_runs(W, fast) != nullptr &&
+           N < (int64_t)pfr::kSellCols * 65535;
 }
 
 // Its launch for N columns runs in one round, with 16-wave workgroups or,
@@ -2302,8 +2310,8 @@ void launch_spmm(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t N, int6
                  bool fast, int act, bool xt = false, float alpha = 1.0f) {
     if (W->M == 0 || N == 0) return;
     const bool i8 = W->vdt == PFR_I8;
-    pfr::require(!xt || sell_serves(W, N), "transposed activation without the column-slice copy");
-    if (sell_serves(W, N)) {
+    pfr::require(!xt || sell_serves(W, N, fast), "transposed activation without the column-slice copy");
+    if (sell_serves(W, N, fast)) {
         launch_sell(ctx, W, X, (int)N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, fast, act, xt, alpha);
     } else if (i8) {
         if (fast) launch_csr_kernels<true, true>(ctx, W, X, N, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
@@ -2337,7 +2345,7 @@ void check_act(int act) {
 // when the handle still has it pending (its first such product).
 void ensure_copies(const pfr_ctx* ctx, const pfr_csr* W, int64_t N, bool fast) {
     uint32_t need = 0;
-    if (W->vdt == PFR_F32 && N >= kSellMinN) need |= pfr::kCopySell;
+    if (W->vdt == PFR_F32 && N >= kSellMinN) need |= fast ? pfr::kCopySellFast : pfr::kCopySell;
     if (fast && ((N >= 2 && N <= 8) || (N == 1 && !(ctx->merge && W->mp_wave != nullptr)))) need |= pfr::kCopyBal;
     if (!fast && N <= 8) need |= pfr::kCopyChain;
     if ((W->pending.load(std::memory_order_acquire) & need) != 0) pfr::csr_build_copies(const_cast<pfr_csr*>(W), need);
@@ -2386,7 +2394,7 @@ void gemm_dev(pfr_ctx* ctx, const float* A, int64_t Mb, int64_t K, int transA, c
     };
     if (K == 0) {
         // No terms: every output is +0 (+ bias); At is never read.
-    } else if (!transA && ws == nullptr && sell_serves(BT, Mb) && K % 4 == 0 && aligned16(A) &&
+    } else if (!transA && ws == nullptr && sell_serves(BT, Mb, mode == PFR_MODE_FAST) && K % 4 == 0 && aligned16(A) &&
                sell_one_round(ctx, BT, Mb)) {
         // the column-slice kernel stages A's rows itself, transposed and
         // scaled on the way into LDS (the allocation-free entry keeps its

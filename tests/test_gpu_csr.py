@@ -2,8 +2,8 @@
 golden vectors written by the compiled reference.
 
 Bar: strict mode is bit-exact (fp32 bits compared with array_equal on the
-uint32 view).  Fast mode (fused multiply-add, same order) is checked with a
-normwise bound: max|y - r| <= 1e-5 * max|r|.
+uint32 view).  Fast mode (fused multiply-add, terms in an order the kernel
+chooses) is checked with a normwise bound: max|y - r| <= 1e-5 * max|r|.
 """
 import sys
 

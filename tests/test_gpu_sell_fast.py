@@ -1,0 +1,98 @@
+"""The fast mode's sliced-ELL copy (the column-slice kernel's runs with each
+row's terms reordered so that the four rows a 16-lane group reads take X
+rows in different LDS bank quarters).
+
+With small-integer weights and activations every product and partial sum is
+an integer below 2^24, so any order of the terms gives the same fp32 bits:
+the fast results must equal the oracle's exactly, which pins that the
+reordered copy holds every stored term once (a dropped, repeated or moved
+term changes an output by at least 1).  Also: a fresh handle's first fast
+product builds only the fast copy and its tables, a strict product then adds
+only the storage-order runs, and the footprint is the same in either order.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pyflamert_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from pyflamert_amd import rocm
+
+    c = rocm.Context(0)
+    yield c
+    c.close()
+
+
+def int_weight(M, K, density, seed, skew=False):
+    """CSR with values in {-3 .. 3} minus 0; uniform or lognormal row lengths."""
+    rng = np.random.default_rng(seed)
+    if skew:
+        ip, ix, _ = workloads.csr_lognormal_rows(M, K, density, 0.8, 1.0, seed)
+    else:
+        ip, ix, _ = workloads.csr_uniform(M, K, density, 1.0, seed)
+    v = rng.integers(1, 4, len(ix)).astype(np.float32) * rng.choice(np.float32([-1, 1]), len(ix))
+    return ip, ix, v
+
+
+@pytest.mark.parametrize("M,K,density,skew", [(4096, 4096, 0.1, False), (1000, 4097, 0.08, True),
+                                              (333, 2500, 0.3, True)])
+def test_fast_copy_exact_on_integers(ctx, M, K, density, skew):
+    """4096 x 4096 (four chunks, 16-wave launches at N = 256), 1000 x 4097
+    (a partial slab, a one-row last chunk, skewed rows) and 333 x 2500 (one
+    chunk, dense rows): N = 16, 64, 128, 256 in fast mode equal the oracle
+    bit for bit on integer data."""
+    ip, ix, v = int_weight(M, K, density, seed=M + K, skew=skew)
+    W = ctx.csr_upload(M, K, ip, ix, v)
+    rng = np.random.default_rng(K)
+    for N in (16, 64, 128, 256):
+        X = rng.integers(-4, 5, (K, N)).astype(np.float32)
+        say(f"fast {M}x{K} nnz={len(ix)} N={N}")
+        Y = W.spmm(X, mode="fast")
+        R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+        assert np.abs(R).max() < 2 ** 24
+        assert np.array_equal(bits(Y), bits(R)), N
+    W.free()
+
+
+def test_fast_copy_footprint_either_order(ctx):
+    """Fast then strict, and strict then fast, on fresh handles of the same
+    weight: each mode's first N = 64 product adds its own runs (the first
+    one also the slab tables), and both handles end at the same size."""
+    M, K = 2048, 3000
+    ip, ix, v = int_weight(M, K, 0.1, seed=7)
+    nnz = len(ix)
+    rng = np.random.default_rng(8)
+    X = rng.integers(-4, 5, (K, 64)).astype(np.float32)
+    R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+    ends = []
+    for order in (("fast", "strict"), ("strict", "fast")):
+        W = ctx.csr_upload(M, K, ip, ix, v)
+        b = [W.device_bytes()]
+        for mode in order:
+            assert np.array_equal(bits(W.spmm(X, mode=mode)), bits(R)), (order, mode)
+            b.append(W.device_bytes())
+            assert np.array_equal(bits(W.spmm(X, mode=mode)), bits(R)), (order, mode)
+            assert W.device_bytes() == b[-1]  # built once
+        say(f"{order}: {[(x - b[0]) / nnz for x in b]} B/nnz added")
+        runs = b[2] - b[1]  # the second copy: its runs only
+        assert runs >= 8 * nnz
+        assert b[1] - b[0] > runs  # the first copy brought the tables too
+        ends.append(b[2])
+        W.free()
+    assert ends[0] == ends[1]
