@@ -911,6 +911,97 @@ __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, con
     }
 }
 
+// Reorders the balanced copy's entries within each row and chunk, one
+// thread per (group, chunk), reading the filled copy (tv, tc) and writing v,
+// cidx.  The batch-8 kernel's 16-byte reads of 32-byte X rows (lane l: half
+// l & 1 of the X row of its record's entry j, then of its partner's) are
+// served in four sets of 16 lanes, the lanes 4r .. 4r + 3 of the slab-row
+// groups the sliced-ELL copy's ordering uses (k_sell_fill_fast); the 16
+// lanes of a set hit distinct banks when the eight of each parity take X
+// rows in distinct eighths of the banks (column % 8 in the chunk).  One
+// instruction reads records q = b G + l >> log2 R of rows l & (R - 1) for a
+// block b of G = 64 / R consecutive records; so block by block and entry by
+// entry, each set of eight lanes gets, lane by lane (fewest options first),
+// the class mod 8 with the most entries left in the lane's row among those
+// not yet taken in the set (a lane past its row's entries reads the zero
+// row, whose class the others then avoid), or its row's fullest class when
+// none is left.  Every row keeps its cells, so padding and the kernels are
+// unchanged; only the order of a row's terms changes (the copy serves the
+// fast mode only).  scratch: 1088 ints per thread.
+template <class V>
+__global__ __launch_bounds__(64) void k_bal_order(int ngroup, int C, int kcw, const int4* __restrict__ meta,
+                                                  const int2* __restrict__ cmeta, const V* __restrict__ tv,
+                                                  const uint16_t* __restrict__ tc, V* __restrict__ v,
+                                                  uint16_t* __restrict__ cidx, int32_t* __restrict__ scratch) {
+    const int64_t id = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (id >= (int64_t)ngroup * C) return;
+    const int g = (int)(id / C), c = (int)(id % C);
+    const int lgR = meta[g].x, R = 1 << lgR, G = 64 >> lgR;
+    const int2 cm = cmeta[(int64_t)g * C + c];
+    const int64_t rec0 = cm.x;
+    const int nq = cm.y;
+    const int base = c * (kcw + 1), zc = kcw & 7;
+    int32_t* cnt = scratch + id * 1088;  // [64][8] entries left per (row, class)
+    int32_t* cur = cnt + 512;            // [64][8] next entry to look at
+    int32_t* n = cur + 512;              // [64] the row's entries in the chunk
+    auto cell = [&](int r, int k) { return (rec0 + (int64_t)(k >> 2) * R + r) * 4 + (k & 3); };
+    auto cls = [&](int r, int k) { return ((int)tc[cell(r, k)] / 4 - base) & 7; };
+    for (int r = 0; r < R; ++r) {
+        int k = 0;
+        while (k < 4 * nq && (int)tc[cell(r, k)] != 4 * (base + kcw)) ++k;
+        n[r] = k;
+        for (int q = 0; q < 8; ++q) cnt[r * 8 + q] = 0, cur[r * 8 + q] = 0;
+        for (int e = 0; e < k; ++e) ++cnt[r * 8 + cls(r, e)];
+    }
+    const int nblk = (nq + G - 1) / G;
+    for (int b = 0; b < nblk; ++b)
+        for (int j = 0; j < 4; ++j)
+            for (int set = 0; set < 8; ++set) {
+                // the set's eight lanes: parity h = set & 1, read group set >> 1
+                int lane[8], m = 0;
+                for (int l = 0; l < 64; ++l)
+                    if ((l & 1) == (set & 1) && (l >> 5) * 2 + (__builtin_popcount((l >> 2) & 7) & 1) == (set >> 1))
+                        lane[m++] = l;
+                uint32_t used = 0;
+                bool live[8];
+                int opts[8];
+                for (int i = 0; i < 8; ++i) {
+                    const int r = lane[i] & (R - 1), q = b * G + (lane[i] >> lgR);
+                    live[i] = q < nq && 4 * q + j < n[r];
+                    if (q < nq && !live[i]) used |= 1u << zc;  // reads the zero row
+                }
+                for (int i = 0; i < 8; ++i) {
+                    opts[i] = 0;
+                    if (!live[i]) continue;
+                    const int r = lane[i] & (R - 1);
+                    for (int u = 0; u < 8; ++u) opts[i] += cnt[r * 8 + u] > 0 ? 1 : 0;
+                }
+                for (int done = 0; done < 8; ++done) {
+                    int i = -1;  // the live lane with the fewest classes left
+                    for (int t = 0; t < 8; ++t)
+                        if (live[t] && (i < 0 || opts[t] < opts[i])) i = t;
+                    if (i < 0) break;
+                    live[i] = false;
+                    const int r = lane[i] & (R - 1), q4 = 4 * (b * G + (lane[i] >> lgR)) + j;
+                    int best = -1, any = -1;
+                    for (int u = 0; u < 8; ++u) {
+                        const int cu = cnt[r * 8 + u];
+                        if (cu == 0) continue;
+                        if (any < 0 || cu > cnt[r * 8 + any]) any = u;
+                        if (!(used >> u & 1u) && (best < 0 || cu > cnt[r * 8 + best])) best = u;
+                    }
+                    const int u = best >= 0 ? best : any;
+                    used |= 1u << u;
+                    int k = cur[r * 8 + u];
+                    while (cls(r, k) != u) ++k;
+                    cur[r * 8 + u] = k + 1;
+                    --cnt[r * 8 + u];
+                    v[cell(r, q4)] = tv[cell(r, k)];
+                    cidx[cell(r, q4)] = tc[cell(r, k)];
+                }
+            }
+}
+
 unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
 
 // Stored-entry bitmap: one wave per row sets the bit of every stored column.
@@ -1047,10 +1138,34 @@ void fill_bal(pfr_csr* w, const CI* col, hipStream_t s) {
     hipLaunchKernelGGL((k_bal_fill<CI, V>), dim3(waves_grid(w->M)), dim3(256), 0, s, w->M, (int)p.C, (int)p.kcw,
                        w->bal_meta, w->bal_cmeta, w->bal_perm, gpos, w->rowptr, col, static_cast<const V*>(w->val),
                        v, w->bal_col);
-    const hipError_t e = hipGetLastError();
+    hipError_t e = hipGetLastError();
     (void)hipStreamSynchronize(s);
     (void)hipFree(gpos);
     if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_fill: ") + hipGetErrorString(e));
+    // the terms' order against LDS bank conflicts (k_bal_order), from a copy
+    // of the filled entries
+    const int64_t nt = p.G * p.C;
+    V* tv = nullptr;
+    uint16_t* tc = nullptr;
+    int32_t* scr = nullptr;
+    try {
+        tv = dev_alloc<V>(n);
+        tc = dev_alloc<uint16_t>(n);
+        scr = dev_alloc<int32_t>(nt * 1088);
+    } catch (...) {
+        (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(scr);
+        throw;
+    }
+    e = hipMemcpyAsync(tv, v, sizeof(V) * (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(tc, w->bal_col, sizeof(uint16_t) * (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_bal_order<V>, dim3((unsigned)((nt + 63) / 64)), dim3(64), 0, s, (int)p.G, (int)p.C,
+                           (int)p.kcw, w->bal_meta, w->bal_cmeta, tv, tc, v, w->bal_col, scr);
+        e = hipGetLastError();
+    }
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(scr);
+    if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_order: ") + hipGetErrorString(e));
 }
 
 template <class CI>

@@ -1,10 +1,13 @@
-"""The fast mode's sliced-ELL copy (the column-slice kernel's runs with each
-row's terms reordered so that the four rows a 16-lane group reads take X
-rows in different LDS bank quarters).
+"""The fast mode's reordered copies: the sliced-ELL copy's fast runs (the
+column-slice kernel, N >= 16; each row's terms reordered so that the four
+slab rows whose X reads the LDS serves together take different bank
+quarters) and the nnz-balanced copy (2 <= N <= 8; each row's terms reordered
+so that the lanes the LDS serves together read X rows in different eighths
+of the banks).
 
 With small-integer weights and activations every product and partial sum is
 an integer below 2^24, so any order of the terms gives the same fp32 bits:
-the fast results must equal the oracle's exactly, which pins that the
+the fast results must equal the oracle's exactly, which pins that a
 reordered copy holds every stored term once (a dropped, repeated or moved
 term changes an output by at least 1).  Also: a fresh handle's first fast
 product builds only the fast copy and its tables, a strict product then adds
@@ -96,3 +99,27 @@ def test_fast_copy_footprint_either_order(ctx):
         ends.append(b[2])
         W.free()
     assert ends[0] == ends[1]
+
+
+@pytest.mark.parametrize("M,K,i8", [(4096, 4096, True), (1000, 11008, True), (777, 5000, False)])
+def test_balanced_copy_exact_on_integers(ctx, M, K, i8):
+    """Fast N = 2, 5, 8 (the nnz-balanced copy, reordered) on skewed rows:
+    int8 weights with unit row scales over one chunk (4096 x 4096) and
+    three (1000 x 11008), and an integer-valued float32 weight, all bit for
+    bit against the oracle."""
+    rng = np.random.default_rng(M + K)
+    ip, ix, _ = workloads.csr_lognormal_rows(M, K, 0.3, 0.5, 1.0, seed=M * 3 + K)
+    q = (rng.integers(1, 100, len(ix)) * rng.choice([-1, 1], len(ix))).astype(np.int8)
+    v = q.astype(np.float32)
+    if i8:
+        W = ctx.csr_upload(M, K, ip, ix, q, row_scales=np.ones(M, np.float32))
+    else:
+        W = ctx.csr_upload(M, K, ip, ix, v)
+    for N in (2, 5, 8):
+        X = rng.integers(-4, 5, (K, N)).astype(np.float32)
+        say(f"balanced fast {M}x{K} nnz={len(ix)} N={N} i8={i8}")
+        Y = W.spmm(X, mode="fast")
+        R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+        assert np.abs(R).max() < 2 ** 24
+        assert np.array_equal(bits(Y), bits(R)), N
+    W.free()
