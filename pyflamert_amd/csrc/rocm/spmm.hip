@@ -1376,7 +1376,32 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
         // thread in flight, clamped; rows past the chunk or K are zero
         const int k0 = ch * kcw, nq4 = (kcw + 1) * 2;  // float4 slots
         const uint32_t cbase = (uint32_t)(ch * (kcw + 1) * 4);  // byte offset of the chunk's first float
-        for (int e0 = 0; e0 < nq4; e0 += 8 * NT) {
+        bool copied = false;
+        if constexpr (XV) {
+            if (kcw >= 32) {
+                // 16-byte rows straight from X into LDS: slot e (row e / 2,
+                // half e % 2) from lane e - base of a wave instruction at
+                // base, the last instruction moved back to end at the last
+                // row (it rewrites slots with the same bytes); rows are
+                // clamped to X's last one (rows past K in the last chunk are
+                // never read: every stored column is below K), and the zero
+                // row kcw is written once the copies have landed.  (Through
+                // registers this took about a quarter of the kernel's
+                // vector instructions: the 64-bit address of every piece.)
+                const int nslot = 2 * kcw;
+                for (int e0 = wave * 64; e0 < nslot; e0 += NT) {
+                    const int base = min(e0, nslot - 64), e = base + lane;
+                    const int k = min(k0 + (e >> 1), K - 1);
+                    __builtin_amdgcn_global_load_lds(X + (int64_t)k * ldx + (e & 1) * 4,
+                                                     (__attribute__((address_space(3))) void*)((__attribute__((address_space(3))) char*)xs + base * 16),
+                                                     16, 0, 0);
+                }
+                __builtin_amdgcn_s_waitcnt(0);  // every counter: this wave's copies have landed
+                if (tid < 2) xs[nslot + tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                copied = true;
+            }
+        }
+        for (int e0 = 0; !copied && e0 < nq4; e0 += 8 * NT) {
             float4 t[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
