@@ -33,6 +33,17 @@ constexpr int kSpmvThreads = 512;  // threads of the vector kernel's workgroup
 constexpr int kSpmvCap = 4096;     // products staged per workgroup chunk (16 KB)
 constexpr int64_t kSellMinN = 16;  // column-slice kernel from this many columns on
 
+// One 4-byte word per lane from base + off into LDS at dst + 4 lane, as a
+// buffer load (bytes: the buffer's size; a lane past it reads zero).  A
+// buffer load, not a global one: the compiler counts a global
+// direct-to-LDS load as a flat access that may finish out of order and then
+// turns every later wait on the memory counters into a wait for all loads.
+__device__ __forceinline__ void lds_copy_dword(const void* base, int bytes, int off,
+                                               __attribute__((address_space(3))) void* dst) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 4, off, 0, 0, 0);
+}
+
 template <bool FAST>
 __device__ __forceinline__ float madd(float acc, float w, float x) {
     if constexpr (FAST) {
@@ -1137,9 +1148,21 @@ __global__ __launch_bounds__(64 * pfr::kMergeWaves) void k_spmv_merge(
     };
     // x's loads first (XL per thread), then the first batch's, so the wait
     // before x goes to LDS leaves the batch in flight
+    // (x contiguous: copied straight into LDS, the slots from K on reading
+    // zero; else through registers)
+    const bool xdma = ldx == 1;
     float xt[XL];
+    if (xdma) {
 #pragma unroll
-    for (int i = 0; i < XL; ++i) xt[i] = x[(int64_t)min(tid + NT * i, K - 1) * ldx];
+        for (int i = 0; i < XL; ++i) {
+            const int sb = NT * i + wave * 64;
+            lds_copy_dword(x, 4 * K, 4 * (sb + lane), (__attribute__((address_space(3))) void*)(xs + sb));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) xt[i] = x[(int64_t)min(tid + NT * i, K - 1) * ldx];
+    }
     // lane l: rowptr[is + l] (up to ie + 1), so the walk reads its row ends
     // from registers instead of waiting on memory at each one
     const int my_rp = rowptr[min(is + lane, ie < M ? ie + 1 : M)];
@@ -1155,8 +1178,15 @@ __global__ __launch_bounds__(64 * pfr::kMergeWaves) void k_spmv_merge(
         sc_is = rs[min(is, M - 1)];
         sc_ie = rs[min(ie, M - 1)];
     }
+    if (xdma) {
+        // this wave's copies have landed: at most the first batch's 2 U
+        // loads (issued after them) are still in flight
+        constexpr int n = 2 * U;
+        __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (0xF << 8));
+    } else {
 #pragma unroll
-    for (int i = 0; i < XL; ++i) xs[tid + NT * i] = tid + NT * i < K ? xt[i] : 0.0f;
+        for (int i = 0; i < XL; ++i) xs[tid + NT * i] = tid + NT * i < K ? xt[i] : 0.0f;
+    }
     if (lane == 0) {
         gv[wave] = 0.0f;  // a share holding no entry of its last row adds nothing to it
         hv[wave] = 0.0f;
