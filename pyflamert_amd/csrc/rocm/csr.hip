@@ -911,95 +911,142 @@ __global__ __launch_bounds__(256) void k_bal_fill(int64_t M, int C, int kcw, con
     }
 }
 
-// Reorders the balanced copy's entries within each row and chunk, one
-// thread per (group, chunk), reading the filled copy (tv, tc) and writing v,
-// cidx.  The batch-8 kernel's 16-byte reads of 32-byte X rows (lane l: half
-// l & 1 of the X row of its record's entry j, then of its partner's) are
-// served in four sets of 16 lanes, the lanes 4r .. 4r + 3 of the slab-row
-// groups the sliced-ELL copy's ordering uses (k_sell_fill_fast); the 16
-// lanes of a set hit distinct banks when the eight of each parity take X
-// rows in distinct eighths of the banks (column % 8 in the chunk).  One
-// instruction reads records q = b G + l >> log2 R of rows l & (R - 1) for a
-// block b of G = 64 / R consecutive records; so block by block and entry by
-// entry, each set of eight lanes gets, lane by lane (fewest options first),
-// the class mod 8 with the most entries left in the lane's row among those
-// not yet taken in the set (a lane past its row's entries reads the zero
-// row, whose class the others then avoid), or its row's fullest class when
-// none is left.  Every row keeps its cells, so padding and the kernels are
-// unchanged; only the order of a row's terms changes (the copy serves the
-// fast mode only).  scratch: 1088 ints per thread.
+// Reorders the balanced copy's entries within each row and chunk, one wave
+// per (group, chunk), reading the filled copy (tv, tc) and writing v, cidx.
+// The batch-8 kernel's 16-byte reads of 32-byte X rows (lane l: half l & 1
+// of the X row of its record's entry j, then of its partner's) are served in
+// four sets of 16 lanes, the lanes 4r .. 4r + 3 of the slab-row groups the
+// sliced-ELL copy's ordering uses (k_sell_fill_fast); the 16 lanes of a set
+// hit distinct banks when the eight of each parity take X rows in distinct
+// eighths of the banks (column % 8 in the chunk).  One instruction reads
+// records q = b G + l >> log2 R of rows l & (R - 1) for a block b of
+// G = 64 / R consecutive records; so block by block and entry by entry, each
+// set of eight lanes gets, lane by lane (fewest options first), the class
+// mod 8 with the most entries left in the lane's row among those not yet
+// taken in the set (a lane past its row's entries reads the zero row, whose
+// class the others then avoid), or its row's fullest class when none is
+// left; a class hands out its entries in their stored order.  Every row
+// keeps its cells, so padding and the kernels are unchanged; only the order
+// of a row's terms changes (the copy serves the fast mode only).
+//
+// First each row's entries are sorted by class (stable) into spos, with the
+// class counts and first positions in LDS; then the choice runs set by set
+// with lane 8i + u of the wave holding class u of the set's entry i, and
+// records each cell's position in the sorted list in pick; last the wave
+// gathers every cell's entry through pick and spos.  spos and pick are as
+// long as the copy.
+__device__ inline int set_lane(int set, int i) {
+    const int m = (((set >> 1) & 1 ? 0x7421 : 0x6530) >> (4 * (i >> 1))) & 15;  // the read group's slab rows
+    return (set >> 2) << 5 | m << 2 | (i & 1) << 1 | (set & 1);
+}
+
 template <class V>
-__global__ __launch_bounds__(64) void k_bal_order(int ngroup, int C, int kcw, const int4* __restrict__ meta,
+__global__ __launch_bounds__(64) void k_bal_order(int C, int kcw, const int4* __restrict__ meta,
                                                   const int2* __restrict__ cmeta, const V* __restrict__ tv,
-                                                  const uint16_t* __restrict__ tc, V* __restrict__ v,
-                                                  uint16_t* __restrict__ cidx, int32_t* __restrict__ scratch) {
-    const int64_t id = (int64_t)blockIdx.x * 64 + threadIdx.x;
-    if (id >= (int64_t)ngroup * C) return;
-    const int g = (int)(id / C), c = (int)(id % C);
+                                                  const uint16_t* __restrict__ tc, uint16_t* __restrict__ spos,
+                                                  uint16_t* __restrict__ pick, V* __restrict__ v,
+                                                  uint16_t* __restrict__ cidx) {
+    __shared__ int n_l[64], cnt_l[512], ptr_l[512];  // per row: entries; per (row, class): left, next position
+    const int g = (int)(blockIdx.x / (unsigned)C), c = (int)(blockIdx.x % (unsigned)C), t = (int)threadIdx.x;
     const int lgR = meta[g].x, R = 1 << lgR, G = 64 >> lgR;
     const int2 cm = cmeta[(int64_t)g * C + c];
     const int64_t rec0 = cm.x;
-    const int nq = cm.y;
-    const int base = c * (kcw + 1), zc = kcw & 7;
-    int32_t* cnt = scratch + id * 1088;  // [64][8] entries left per (row, class)
-    int32_t* cur = cnt + 512;            // [64][8] next entry to look at
-    int32_t* n = cur + 512;              // [64] the row's entries in the chunk
+    const int nq = cm.y, base = c * (kcw + 1), zc = kcw & 7, zero = 4 * (base + kcw);
+    const uint64_t lt = (1ull << t) - 1;
     auto cell = [&](int r, int k) { return (rec0 + (int64_t)(k >> 2) * R + r) * 4 + (k & 3); };
-    auto cls = [&](int r, int k) { return ((int)tc[cell(r, k)] / 4 - base) & 7; };
     for (int r = 0; r < R; ++r) {
-        int k = 0;
-        while (k < 4 * nq && (int)tc[cell(r, k)] != 4 * (base + kcw)) ++k;
-        n[r] = k;
-        for (int q = 0; q < 8; ++q) cnt[r * 8 + q] = 0, cur[r * 8 + q] = 0;
-        for (int e = 0; e < k; ++e) ++cnt[r * 8 + cls(r, e)];
+        // the row's entries come before its first padding cell
+        int nr = 4 * nq, mine = 0;
+        for (int k0 = 0; k0 < nr; k0 += 64) {
+            const int k = k0 + t, cv = k < nr ? (int)tc[cell(r, k)] : zero;
+            const uint64_t z = __ballot(cv == zero);
+            const int lim = z ? k0 + __builtin_ctzll(z) : nr;
+            const int u = (cv / 4 - base) & 7;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int nqc = __builtin_popcountll(__ballot(k < lim && u == q));
+                if (t == q) mine += nqc;
+            }
+            nr = lim;
+        }
+        int run[8], off = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            run[q] = off;
+            off += __builtin_amdgcn_readlane(mine, q);
+        }
+        if (t < 8) {
+            int first = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) first = t == q ? run[q] : first;
+            cnt_l[r * 8 + t] = mine;
+            ptr_l[r * 8 + t] = first;
+        }
+        if (t == 0) n_l[r] = nr;
+        for (int k0 = 0; k0 < nr; k0 += 64) {
+            const int k = k0 + t;
+            const bool in = k < nr;
+            const int u = in ? ((int)tc[cell(r, k)] / 4 - base) & 7 : 0;
+            int pos = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint64_t m = __ballot(in && u == q);
+                if (u == q) pos = run[q] + __builtin_popcountll(m & lt);
+                run[q] += __builtin_popcountll(m);
+            }
+            if (in) spos[cell(r, pos)] = (uint16_t)k;
+        }
     }
-    const int nblk = (nq + G - 1) / G;
+    __syncthreads();
+    const int gi = t >> 3, u = t & 7, nblk = (nq + G - 1) / G;
     for (int b = 0; b < nblk; ++b)
         for (int j = 0; j < 4; ++j)
             for (int set = 0; set < 8; ++set) {
-                // the set's eight lanes: parity h = set & 1, read group set >> 1
-                int lane[8], m = 0;
-                for (int l = 0; l < 64; ++l)
-                    if ((l & 1) == (set & 1) && (l >> 5) * 2 + (__builtin_popcount((l >> 2) & 7) & 1) == (set >> 1))
-                        lane[m++] = l;
-                uint32_t used = 0;
-                bool live[8];
-                int opts[8];
+                const int li = set_lane(set, gi), r = li & (R - 1), q = b * G + (li >> lgR);
+                const bool inq = q < nq, live = inq && 4 * q + j < n_l[r];
+                const uint64_t lv = __ballot(live);
+                if (lv == 0) continue;
+                int cn = cnt_l[r * 8 + u], pt = ptr_l[r * 8 + u];
+                const uint64_t pz = __ballot(live && cn > 0);
+                uint32_t used = __ballot(inq && !live) ? 1u << zc : 0u, left = 0, opts = 0;
+#pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const int r = lane[i] & (R - 1), q = b * G + (lane[i] >> lgR);
-                    live[i] = q < nq && 4 * q + j < n[r];
-                    if (q < nq && !live[i]) used |= 1u << zc;  // reads the zero row
+                    left |= (uint32_t)(lv >> (8 * i) & 1) << i;
+                    opts |= (uint32_t)__builtin_popcountll((pz >> (8 * i)) & 0xff) << (4 * i);
                 }
-                for (int i = 0; i < 8; ++i) {
-                    opts[i] = 0;
-                    if (!live[i]) continue;
-                    const int r = lane[i] & (R - 1);
-                    for (int u = 0; u < 8; ++u) opts[i] += cnt[r * 8 + u] > 0 ? 1 : 0;
-                }
-                for (int done = 0; done < 8; ++done) {
-                    int i = -1;  // the live lane with the fewest classes left
-                    for (int t = 0; t < 8; ++t)
-                        if (live[t] && (i < 0 || opts[t] < opts[i])) i = t;
-                    if (i < 0) break;
-                    live[i] = false;
-                    const int r = lane[i] & (R - 1), q4 = 4 * (b * G + (lane[i] >> lgR)) + j;
-                    int best = -1, any = -1;
-                    for (int u = 0; u < 8; ++u) {
-                        const int cu = cnt[r * 8 + u];
-                        if (cu == 0) continue;
-                        if (any < 0 || cu > cnt[r * 8 + any]) any = u;
-                        if (!(used >> u & 1u) && (best < 0 || cu > cnt[r * 8 + best])) best = u;
+                while (left) {
+                    int bi = 0, bo = 16;  // the live entry with the fewest classes left, first on ties
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int o = (int)(opts >> (4 * i)) & 15;
+                        if ((left >> i & 1) && o < bo) bo = o, bi = i;
                     }
-                    const int u = best >= 0 ? best : any;
-                    used |= 1u << u;
-                    int k = cur[r * 8 + u];
-                    while (cls(r, k) != u) ++k;
-                    cur[r * 8 + u] = k + 1;
-                    --cnt[r * 8 + u];
-                    v[cell(r, q4)] = tv[cell(r, k)];
-                    cidx[cell(r, q4)] = tc[cell(r, k)];
+                    left &= ~(1u << bi);
+                    // untaken classes first, then the most entries, then the lowest class
+                    const int key = gi == bi && cn > 0 ? ((used >> u & 1) ? 0 : 1 << 30) | cn << 3 | (7 - u) : -1;
+                    int best = -1;
+#pragma unroll
+                    for (int w = 0; w < 8; ++w) best = max(best, __builtin_amdgcn_readlane(key, 8 * bi + w));
+                    const int bu = 7 - (best & 7), sp = __builtin_amdgcn_readlane(pt, 8 * bi + bu);
+                    used |= 1u << bu;
+                    const int bl = set_lane(set, bi), br = bl & (R - 1);
+                    if (r == br && u == bu) --cn, ++pt;
+                    if (t == 0) pick[cell(br, 4 * (b * G + (bl >> lgR)) + j)] = (uint16_t)sp;
                 }
+                cnt_l[r * 8 + u] = cn;  // lanes of one row hold the same values
+                ptr_l[r * 8 + u] = pt;
             }
+    __syncthreads();  // pick and spos are read back below
+#pragma unroll 4
+    for (int e = t; e < 4 * nq * R; e += 64) {  // the task's cells in storage order
+        const int r = (e >> 2) & (R - 1), k = (e >> 2 >> lgR) * 4 + (e & 3), nr = n_l[r];
+        if (k < nr) {
+            const int64_t to = rec0 * 4 + e;
+            const int64_t from = cell(r, min((int)spos[cell(r, min((int)pick[to], nr - 1))], nr - 1));
+            v[to] = tv[from];
+            cidx[to] = tc[from];
+        }
+    }
 }
 
 unsigned waves_grid(int64_t M) { return (unsigned)((M + 3) / 4); }
@@ -1146,25 +1193,24 @@ void fill_bal(pfr_csr* w, const CI* col, hipStream_t s) {
     // of the filled entries
     const int64_t nt = p.G * p.C;
     V* tv = nullptr;
-    uint16_t* tc = nullptr;
-    int32_t* scr = nullptr;
+    uint16_t *tc = nullptr, *sp = nullptr;
     try {
         tv = dev_alloc<V>(n);
         tc = dev_alloc<uint16_t>(n);
-        scr = dev_alloc<int32_t>(nt * 1088);
+        sp = dev_alloc<uint16_t>(2 * n);
     } catch (...) {
-        (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(scr);
+        (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(sp);
         throw;
     }
     e = hipMemcpyAsync(tv, v, sizeof(V) * (size_t)n, hipMemcpyDeviceToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(tc, w->bal_col, sizeof(uint16_t) * (size_t)n, hipMemcpyDeviceToDevice, s);
-    if (e == hipSuccess) {
-        hipLaunchKernelGGL(k_bal_order<V>, dim3((unsigned)((nt + 63) / 64)), dim3(64), 0, s, (int)p.G, (int)p.C,
-                           (int)p.kcw, w->bal_meta, w->bal_cmeta, tv, tc, v, w->bal_col, scr);
+    if (e == hipSuccess && nt > 0) {
+        hipLaunchKernelGGL(k_bal_order<V>, dim3((unsigned)nt), dim3(64), 0, s, (int)p.C, (int)p.kcw, w->bal_meta,
+                           w->bal_cmeta, tv, tc, sp, sp + n, v, w->bal_col);
         e = hipGetLastError();
     }
     (void)hipStreamSynchronize(s);
-    (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(scr);
+    (void)hipFree(tv), (void)hipFree(tc), (void)hipFree(sp);
     if (e != hipSuccess) throw pfr::Error(PFR_ERR_HIP, std::string("k_bal_order: ") + hipGetErrorString(e));
 }
 
