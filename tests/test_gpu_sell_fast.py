@@ -123,3 +123,45 @@ def test_balanced_copy_exact_on_integers(ctx, M, K, i8):
         assert np.abs(R).max() < 2 ** 24
         assert np.array_equal(bits(Y), bits(R)), N
     W.free()
+
+
+def test_balanced_copy_skewed_classes(ctx):
+    """The balanced copy's term order where the choice is hardest, fast
+    N = 2 and 8 bit for bit against the oracle: rows whose columns all fall
+    in one class mod 8 of their chunk, rows with two classes, empty rows,
+    rows confined to the first of three chunks (the others hold no terms of
+    theirs), and one row with every column (a group of its own), as int8
+    (unit scales) and integer-valued float32."""
+    M, K = 600, 9000  # three chunks of 3000 columns
+    rng = np.random.default_rng(77)
+    rows = []
+    for r in range(M):
+        kind = r % 5
+        if r == 7:
+            c = np.arange(K)
+        elif kind == 0:
+            c = np.array([], np.int64)
+        elif kind == 1:  # class 3 of chunk 0 only
+            c = np.sort(rng.choice(np.arange(3, 3000, 8), int(rng.integers(1, 300)), replace=False))
+        elif kind == 2:  # classes 0 and 5 of every chunk
+            base = np.concatenate([np.arange(ch * 3000, ch * 3000 + 3000, 8) for ch in range(3)])
+            pool = np.concatenate([base, base + 5])
+            c = np.sort(rng.choice(pool, int(rng.integers(1, 1200)), replace=False))
+        else:
+            c = np.sort(rng.choice(K, int(rng.integers(0, 2700)), replace=False))
+        rows.append(c.astype(np.int64))
+    ip = np.zeros(M + 1, np.int64)
+    np.cumsum([len(c) for c in rows], out=ip[1:])
+    ix = np.concatenate(rows)
+    q = (rng.integers(1, 100, len(ix)) * rng.choice([-1, 1], len(ix))).astype(np.int8)
+    v = q.astype(np.float32)
+    for tag, W in (("int8", ctx.csr_upload(M, K, ip, ix, q, row_scales=np.ones(M, np.float32))),
+                   ("fp32", ctx.csr_upload(M, K, ip, ix, v))):
+        for N in (2, 8):
+            X = rng.integers(-4, 5, (K, N)).astype(np.float32)
+            say(f"balanced skewed classes {tag} N={N} nnz={len(ix)}")
+            Y = W.spmm(X, mode="fast")
+            R = O.orc_csr_spmm(M, K, ip, ix, v, X)
+            assert np.abs(R).max() < 2 ** 24
+            assert np.array_equal(bits(Y), bits(R)), (tag, N)
+        W.free()
