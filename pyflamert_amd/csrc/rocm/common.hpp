@@ -201,6 +201,12 @@ struct pfr_csr {
     int4* bal_meta = nullptr;      // [bal_ngroup]
     int2* bal_cmeta = nullptr;     // [bal_ngroup * bal_nchunk]
     int32_t* bal_perm = nullptr;   // [M] row of each group lane
+    // The batch kernel's workgroups: bal_pair[i] = {group, group or -1,
+    // waves of the first}; groups are paired largest with smallest (by
+    // records) and a workgroup's 16 waves split between its two in
+    // proportion to their records, so every wave walks about as many.
+    int4* bal_pair = nullptr;      // [bal_npair]
+    int32_t bal_npair = 0;
     void* bal_val = nullptr;
     uint16_t* bal_col = nullptr;
     int32_t bal_ngroup = 0, bal_nchunk = 0, bal_kcw = 0;

@@ -74,7 +74,7 @@ void free_csr(pfr_csr* w) {
                     (void*)w->sell_perm, (void*)w->sell_soff, (void*)w->sell_blk, (void*)w->sell_blk_fast,
                     (void*)w->chain_q0, (void*)w->col16,
                     (void*)w->chain_len, (void*)w->chain_perm, w->chain_val, w->chain_col, (void*)w->bal_meta,
-                    (void*)w->bal_cmeta, (void*)w->bal_perm, w->bal_val, (void*)w->bal_col, (void*)w->pattern,
+                    (void*)w->bal_cmeta, (void*)w->bal_perm, (void*)w->bal_pair, w->bal_val, (void*)w->bal_col, (void*)w->pattern,
                     (void*)w->mp_wave, (void*)w->mp_wmeta, (void*)w->mp_grp, (void*)w->mp_xchg,
                     (void*)w->mp_carry, (void*)w->mp_cnt})
         if (p) (void)hipFree(p);
@@ -346,6 +346,7 @@ struct BalPlan {
     std::vector<int2> cmeta;   // [G * C] {first record, quad rows} of each (group, chunk)
     std::vector<int32_t> perm; // [M] row of each sorted position
     std::vector<int32_t> gpos; // [M] group of each sorted position
+    std::vector<int4> pair;    // [ceil(G / 2)] the batch kernel's workgroups (pfr_csr::bal_pair)
 };
 
 // nnz-balanced plan (layout described at pfr_csr::bal_meta) from the row
@@ -354,8 +355,12 @@ struct BalPlan {
 // 64 and at most the rows left) whose padded records -- R times the sum over
 // chunks of its longest row there -- fit the budget, so a row longer than
 // the budget makes a group of its own.  The budget is the smallest that
-// keeps the group count at most two per CU.  False when the copy would
-// outgrow 32-bit offsets.
+// keeps the group count at most two per CU.  Power-of-two heights leave the
+// heaviest group about 1.45 times the mean, so the batch kernel's
+// workgroups take the groups in pairs, largest with smallest, and split
+// their 16 waves between the two in proportion to their records (the
+// split with the least records per wave on the busier side).  False when
+// the copy would outgrow 32-bit offsets.
 bool plan_bal(const pfr_csr* w, const std::vector<int32_t>& len, const std::vector<int32_t>& cntc, BalPlan* p) {
     const int64_t M = w->M;
     if (!bal_geom(w->K, &p->C, &p->kcw)) return false;
@@ -422,6 +427,28 @@ bool plan_bal(const pfr_csr* w, const std::vector<int32_t>& len, const std::vect
         i += R;
     }
     p->nrec = nrec;
+    std::vector<int64_t> grec((size_t)G, 0);  // records per group
+    for (int64_t g = 0; g < G; ++g)
+        for (int64_t c = 0; c < C; ++c)
+            grec[(size_t)g] += ((int64_t)1 << p->meta[(size_t)g].x) * p->cmeta[(size_t)(g * C + c)].y;
+    std::vector<int32_t> by((size_t)G);
+    for (int64_t g = 0; g < G; ++g) by[(size_t)g] = (int32_t)g;
+    std::stable_sort(by.begin(), by.end(), [&](int32_t a, int32_t b) { return grec[(size_t)a] > grec[(size_t)b]; });
+    const int64_t P = (G + 1) / 2, WW = 16;
+    p->pair.resize((size_t)P);
+    for (int64_t i = 0; i < P; ++i) {
+        const int32_t a = by[(size_t)i], b = G - 1 - i > i ? by[(size_t)(G - 1 - i)] : -1;
+        int64_t na = WW;
+        if (b >= 0) {
+            const int64_t ra = std::max<int64_t>(grec[(size_t)a], 1), rb = std::max<int64_t>(grec[(size_t)b], 1);
+            double best = 0.0;
+            for (int64_t n = 1; n < WW; ++n) {
+                const double t = std::max((double)ra / (double)n, (double)rb / (double)(WW - n));
+                if (n == 1 || t < best) best = t, na = n;
+            }
+        }
+        p->pair[(size_t)i] = make_int4(a, b, (int)na, 0);
+    }
     return (nrec + 64) * 4 <= INT32_MAX && G <= INT32_MAX;
 }
 
@@ -430,6 +457,8 @@ void set_bal(pfr_csr* w, const BalPlan& p, hipStream_t s) {
     w->bal_meta = walloc_copy(w, p.meta.data(), p.G, s);
     w->bal_cmeta = walloc_copy(w, p.cmeta.data(), p.G * p.C, s);
     w->bal_perm = walloc_copy(w, p.perm.data(), (int64_t)p.perm.size(), s);
+    w->bal_pair = walloc_copy(w, p.pair.data(), (int64_t)p.pair.size(), s);
+    w->bal_npair = (int32_t)p.pair.size();
     w->bal_ngroup = (int32_t)p.G;
     w->bal_nchunk = (int32_t)p.C;
     w->bal_kcw = (int32_t)p.kcw;
@@ -1243,7 +1272,8 @@ void drop_copy(pfr_csr* w, uint32_t bit) {
         free_null(w->chain_val), free_null(w->chain_col);
         w->chain_nslab = 0;
     } else {
-        free_null(w->bal_meta), free_null(w->bal_cmeta), free_null(w->bal_perm);
+        free_null(w->bal_meta), free_null(w->bal_cmeta), free_null(w->bal_perm), free_null(w->bal_pair);
+        w->bal_npair = 0;
         free_null(w->bal_val), free_null(w->bal_col);
         w->bal_ngroup = w->bal_nchunk = w->bal_kcw = 0;
     }

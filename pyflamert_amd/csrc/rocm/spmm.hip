@@ -1333,12 +1333,13 @@ void launch_merge(pfr_ctx* ctx, const pfr_csr* W, const float* X, int64_t ldx, f
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Fast 2 <= N <= 8 over the nnz-balanced copy: a workgroup takes groups b
-// and b + gridDim.x (the copy holds at most two per CU), waves 0..7 the first
-// and 8..15 the second, and walks K chunk by chunk: the chunk's X rows are
-// staged in LDS as rows of eight floats (kcw + 1 rows with the zero row, 32 B
-// each), then each half of the workgroup folds its group's records of that
-// chunk into per-lane sums (the two groups' record streams, and the
+// Fast 2 <= N <= 8 over the nnz-balanced copy: workgroup i takes the two
+// groups of bal_pair[i] (the copy holds at most two per CU, paired largest
+// with smallest), waves 0 .. na - 1 the first and the rest the second, na in
+// proportion to their records, and walks K chunk by chunk: the chunk's X
+// rows are staged in LDS as rows of eight floats (kcw + 1 rows with the zero
+// row, 32 B each), then each group's waves fold its records of that chunk
+// into per-lane sums (the two groups' record streams, and the
 // latencies of their starts, overlap; walked one after the other with all
 // sixteen waves, the second group's start measured as a bubble).  Lanes work
 // in pairs: each lane loads its own record (four nonzeros of one row), takes
@@ -1346,27 +1347,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 // nonzeros (columns 4h .. 4h + 3 for lane parity h), so a pair reads a whole
 // 32-byte row.  Records are loaded a batch ahead of the one folded, and each
 // group's first batch of a chunk before the chunk is staged.  The sums of a
-// row's lanes meet by shuffles, then across the group's waves in LDS (waves
-// 4..7 of a half add theirs to waves 0..3 first, so the order is fixed).
+// row's lanes meet by shuffles, then across the group's waves in LDS (added
+// in wave order, so the order is fixed).
 template <bool I8, int W, int U, bool XV>
 __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
-    int K, int N, int ngroup, int nch, int kcw, const int4* __restrict__ meta, const int2* __restrict__ cmeta,
-    const int32_t* __restrict__ perm, const void* __restrict__ vals, const uint16_t* __restrict__ cols,
-    const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy_r,
-    int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta, int act) {
-    static_assert(W == 16, "two groups of eight waves; the cross-wave sum pairs waves w and w + 4");
-    constexpr int NT = 64 * W, WG = W / 2;
-    extern __shared__ float4 xs[];  // [(kcw + 1) * 2]: row k at xs[2k], xs[2k + 1]
-    __shared__ float part[2][4][64][8];
+    int K, int N, int kcw, int nch, const int4* __restrict__ pair, const int4* __restrict__ meta,
+    const int2* __restrict__ cmeta, const int32_t* __restrict__ perm, const void* __restrict__ vals,
+    const uint16_t* __restrict__ cols, const float* __restrict__ rs, const float* __restrict__ X, int64_t ldx,
+    float* __restrict__ Y, int64_t ldy_r, int64_t ldy_c, const float* __restrict__ bias, int64_t c_size, float beta,
+    int act) {
+    static_assert(W == 16, "the pair table splits sixteen waves");
+    constexpr int NT = 64 * W;
+    // [(kcw + 1) * 2]: row k at xs[2k], xs[2k + 1]; after the walk, each
+    // wave's row sums ([W][64][8] floats)
+    extern __shared__ float4 xs[];
     const int tid = threadIdx.x, lane = tid & 63, h = lane & 1;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int half = wave / WG, gw = wave % WG, gt = tid % (64 * WG);  // group half, wave and thread in it
+    // the workgroup's pair: waves 0 .. na - 1 walk the first group, the rest
+    // the second (wb: the group's first wave, nw its waves, gw and gt the
+    // wave and thread in them)
+    const int4 pq = pair[blockIdx.x];
+    const int na = __builtin_amdgcn_readfirstlane(pq.z), second = wave >= na ? 1 : 0;
+    const int wb = second ? na : 0, nw = second ? W - na : na, gw = wave - wb, gt = tid - 64 * wb;
     using ValT = typename std::conditional<I8, uint32_t, float4>::type;
     const ValT* V = static_cast<const ValT*>(vals);
     const uint2* Cl = reinterpret_cast<const uint2*>(cols);
     const char* xbh = reinterpret_cast<const char*>(xs) + 16 * h;  // this lane's half of every X row
-    const int grp = (int)blockIdx.x + half * (int)gridDim.x;
-    const bool live = grp < ngroup;
+    const int grp = __builtin_amdgcn_readfirstlane(second ? pq.y : pq.x);
+    const bool live = grp >= 0;
     const int lgR = live ? __builtin_amdgcn_readfirstlane(meta[grp].x) : 0;
     const int R = 1 << lgR, G = 64 >> lgR;
     const int r = lane & (R - 1), sub = lane >> lgR, psub = (lane ^ 1) >> lgR;
@@ -1378,7 +1386,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
     auto load = [&](ValT* v, uint2* cc, int rec0, int nq, int b) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t at = rec0 + (int64_t)min(b + sub + G * WG * u, nq - 1) * R + r;
+            const int64_t at = rec0 + (int64_t)min(b + sub + G * nw * u, nq - 1) * R + r;
             v[u] = V[at];
             cc[u] = Cl[at];
         }
@@ -1393,7 +1401,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
     }
     // DPP quad_perm [1, 0, 3, 2]: the partner lane's value
     auto swap = [](auto v) { return __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false); };
-    const int step = G * WG * U, b0 = G * gw;
+    const int step = G * nw * U, b0 = G * gw;
     int2 cm = live ? cmeta[grp * nch] : make_int2(0, 0);
     for (int ch = 0; ch < nch; ++ch) {
         const int rec0 = __builtin_amdgcn_readfirstlane(cm.x), nq = __builtin_amdgcn_readfirstlane(cm.y);
@@ -1468,7 +1476,7 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
         auto fold = [&](const ValT* v, const uint2* cc, int b) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const bool in_own = b + sub + G * WG * u < nq, in_par = b + psub + G * WG * u < nq;
+                const bool in_own = b + sub + G * nw * u < nq, in_par = b + psub + G * nw * u < nq;
                 float wo[4], wp[4];
                 if constexpr (I8) {
                     const uint32_t qo = v[u], qp = (uint32_t)swap(v[u]);
@@ -1536,27 +1544,28 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
             if (R > 1) par[e] += __shfl_xor(par[e], s, 64);
         }
     // lane r < max(R, 2) holds row r's half h (own) and, for R > 1, row r ^
-    // 1's half h (par): every (row, column) once per wave
-    auto put = [&](float (*dst)[8], bool add) {
-        if (lane < (R < 2 ? 2 : R)) {
-            const int ro = R < 2 ? 0 : lane, rp = lane ^ 1;
+    // 1's half h (par): every (row, column) once per wave, stored to the
+    // wave's slot (X is no longer read: the last chunk's barrier is behind)
+    float(*const ws)[64][8] = reinterpret_cast<float(*)[64][8]>(xs);
+    if (lane < (R < 2 ? 2 : R)) {
+        const int ro = R < 2 ? 0 : lane, rp = lane ^ 1;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dst[ro][4 * h + e] = add ? dst[ro][4 * h + e] + own[e] : own[e];
-                if (R > 1) dst[rp][4 * h + e] = add ? dst[rp][4 * h + e] + par[e] : par[e];
-            }
+        for (int e = 0; e < 4; ++e) {
+            ws[wave][ro][4 * h + e] = own[e];
+            if (R > 1) ws[wave][rp][4 * h + e] = par[e];
         }
-    };
-    if (gw >= 4) put(part[half][gw - 4], false);
+    }
     __syncthreads();
-    if (gw < 4) put(part[half][gw], true);
-    __syncthreads();
-    if (live && gt < R * 8) {  // row gt / 8, column gt % 8
-        const int rr = gt >> 3, c = gt & 7;
-        float sum = ((part[half][0][rr][c] + part[half][1][rr][c]) + part[half][2][rr][c]) + part[half][3][rr][c];
+    // the group's threads write its R x 8 outputs (row o / 8, column o % 8),
+    // each the sum of the group's waves in wave order
+    for (int o = gt; live && o < R * 8; o += 64 * nw) {
+        const int rr = o >> 3, c = o & 7;
+        float sum = ws[wb][rr][c];
+        for (int w2 = 1; w2 < nw; ++w2) sum += ws[wb + w2][rr][c];
         if (c < N) {
-            if constexpr (I8) sum *= oscale;
-            const int64_t f = (int64_t)orow * ldy_r + (int64_t)c * ldy_c;
+            const int row = o == gt ? orow : perm[meta[grp].y + rr];
+            if constexpr (I8) sum *= o == gt ? oscale : rs[row];
+            const int64_t f = (int64_t)row * ldy_r + (int64_t)c * ldy_c;
             Y[f] = bias_add(sum, f, bias, c_size, beta, act);
         }
     }
@@ -1568,7 +1577,9 @@ template <bool I8, bool XV>
 void launch_bal_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
                       int64_t ldy_r, int64_t ldy_c, const float* bias, int64_t c_size, float beta, int act) {
     auto kern = k_spmm_bal_fast8<I8, 16, kBalFast8U, XV>;
-    const size_t lds = (size_t)(W->bal_kcw + 1) * 32;  // <= (4096 + 1) * 32 B, with part[8][64][8]: 144 KiB
+    // the X chunk, and after the walk the waves' sums (16 x 64 x 8 floats):
+    // <= (4096 + 1) * 32 B = 128 KiB
+    const size_t lds = std::max<size_t>((size_t)(W->bal_kcw + 1) * 32, 16 * 64 * 8 * sizeof(float));
     static uint64_t allowed = 0;  // bit d: the dynamic LDS limit raised on device d (< 64)
     const uint64_t bit = ctx->device < 64 ? (uint64_t(1) << ctx->device) : 0;
     if (lds > 65536 && (!bit || !(__atomic_load_n(&allowed, __ATOMIC_ACQUIRE) & bit))) {
@@ -1576,9 +1587,8 @@ void launch_bal_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int
                                     (int)((pfr::kBalChunk + 1) * 32)));
         if (bit) __atomic_fetch_or(&allowed, bit, __ATOMIC_RELEASE);
     }
-    const int grid = (W->bal_ngroup + 1) / 2;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * 16), lds, ctx->stream, (int)W->K, N, W->bal_ngroup,
-                       W->bal_nchunk, W->bal_kcw, W->bal_meta, W->bal_cmeta, W->bal_perm, W->bal_val, W->bal_col,
+    hipLaunchKernelGGL(kern, dim3((unsigned)W->bal_npair), dim3(64 * 16), lds, ctx->stream, (int)W->K, N,
+                       W->bal_kcw, W->bal_nchunk, W->bal_pair, W->bal_meta, W->bal_cmeta, W->bal_perm, W->bal_val, W->bal_col,
                        W->row_scale, X, ldx, Y, ldy_r, ldy_c, bias, c_size, beta, act);
 }
 
