@@ -1571,7 +1571,12 @@ __global__ __launch_bounds__(64 * W) void k_spmm_bal_fast8(
     }
 }
 
-constexpr int kBalFast8U = 4;
+// Records per lane and batch of the batch kernel.  With the waves balanced
+// by the pair table, one record per batch measured fastest: the first
+// batch, which all 4096 waves ask for together, is a quarter of the size
+// at U = 4 (stacked batch-8 step 2.42-2.49 ms against 2.50-2.61 at U = 2
+// and 2.67-2.84 at U = 4).
+constexpr int kBalFast8U = 1;
 
 template <bool I8, bool XV>
 void launch_bal_fast8(pfr_ctx* ctx, const pfr_csr* W, const float* X, int N, int64_t ldx, float* Y,
